@@ -1,0 +1,1050 @@
+/*
+ * whisper_ref.c -- the oracle: CPU restatement of whisper4j's Linux text-decoder path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see whisper_ref.h).  It is the checker for the HIP product and the
+ * timed CPU baseline ("port"); nothing in whisper4j_amd/ links, loads or calls it.
+ *
+ * Build: gcc -O3 -march=x86-64-v3 -ffp-contract=off -fPIC -shared whisper_ref.c -lz -lm
+ * (-ffp-contract=off is part of the contract: Java evaluates a*b+c as two roundings.)
+ */
+#include "whisper_ref.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <zlib.h>
+
+/* ------------------------------------------------------------------------------------------ */
+/* f16 <-> f32: Float.float16ToFloat / Float.floatToFloat16 (IEEE binary16, round-to-nearest-even) */
+
+float orc_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1fu;
+  uint32_t man = h & 0x3ffu;
+  uint32_t bits;
+  if (exp == 0) {
+    if (man == 0) {
+      bits = sign;
+    } else { /* subnormal: normalise */
+      int e = -1;
+      do { man <<= 1; e++; } while ((man & 0x400u) == 0);
+      man &= 0x3ffu;
+      bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+    }
+  } else if (exp == 31) {
+    bits = sign | 0x7f800000u | (man << 13);
+  } else {
+    bits = sign | ((exp + 127 - 15) << 23) | (man << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+uint16_t orc_f32_to_f16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) { /* inf or NaN */
+    if (ax == 0x7f800000u) return (uint16_t)(sign | 0x7c00u);
+    uint32_t m = (ax >> 13) & 0x3ffu;
+    return (uint16_t)(sign | 0x7c00u | (m ? m : 0x200u));
+  }
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* rounds to >= 65520 -> inf */
+  if (ax < 0x38800000u) {                                      /* result is subnormal or zero */
+    if (ax < 0x33000000u) return (uint16_t)sign;               /* < 2^-25 rounds to 0 */
+    uint32_t e = ax >> 23;
+    uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+    uint32_t shift = 126 - e; /* so that value = m * 2^-(shift+...)*/
+    /* f = m * 2^(e-150); subnormal unit is 2^-24 -> q = m * 2^(e-150+24) = m >> (126-e) */
+    uint32_t q = m >> shift;
+    uint32_t rem = m & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+  }
+  uint32_t e = (ax >> 23) - 127 + 15;
+  uint32_t m = ax & 0x7fffffu;
+  uint32_t q = (e << 10) | (m >> 13);
+  uint32_t rem = m & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
+  return (uint16_t)(sign | q);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* GELU table: main/tensor/Tensor.java:493-501.  Same float expression tree, Math.tanh on the
+ * widened argument, rounded back to float. */
+void orc_gelu_table(float* table) {
+  float s = (float)sqrt(2.0 / 3.14159265358979323846);
+  for (int i = 0; i < 65536; i++) {
+    float x = orc_f16_to_f32((uint16_t)i);
+    float inner = s * (x + 0.044715f * x * x * x);
+    table[i] = 0.5f * x * (1.0f + (float)tanh((double)inner));
+  }
+}
+
+static float* g_gelu_table = NULL;
+static const float* gelu_table(void) {
+  if (!g_gelu_table) {
+    float* t = (float*)malloc(65536 * sizeof(float));
+    orc_gelu_table(t);
+    g_gelu_table = t;
+  }
+  return g_gelu_table;
+}
+
+/* Tensor.geluInPlace: main/tensor/Tensor.java:524-538 */
+void orc_gelu(float* x, int n) {
+  const float* t = gelu_table();
+  for (int i = 0; i < n; i++) x[i] = t[orc_f32_to_f16(x[i])];
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* VectorSimdOps.dot: java26/.../VectorSimdOps.java:20-39.  acc = acc + a*b lane-wise over
+ * loopBound(len); reduceLanes(ADD); scalar tail added in order. */
+float orc_dot(const float* a, const float* b, int n) {
+  float acc[ORC_LANES];
+  for (int l = 0; l < ORC_LANES; l++) acc[l] = 0.0f;
+  int bound = n - n % ORC_LANES;
+  int i = 0;
+  for (; i < bound; i += ORC_LANES)
+    for (int l = 0; l < ORC_LANES; l++) acc[l] = acc[l] + a[i + l] * b[i + l];
+  float sum = acc[0];
+  for (int l = 1; l < ORC_LANES; l++) sum = sum + acc[l];
+  for (; i < n; i++) sum = sum + a[i] * b[i];
+  return sum;
+}
+
+/* Tensor.layerNorm: main/tensor/Tensor.java:592-619 (eps 1e-5 from main/nn/LayerNorm.java:16) */
+void orc_layernorm(const float* x, int rows, int n, const float* g, const float* b, float eps, float* out) {
+  for (int r = 0; r < rows; r++) {
+    const float* row = x + (size_t)r * n;
+    float* o = out + (size_t)r * n;
+    float mean = 0.0f;
+    for (int j = 0; j < n; j++) mean += row[j];
+    mean /= (float)n;
+    float variance = 0.0f;
+    for (int j = 0; j < n; j++) {
+      float d = row[j] - mean;
+      variance += d * d;
+    }
+    float invStd = 1.0f / (float)sqrt((double)(variance / (float)n + eps));
+    for (int j = 0; j < n; j++) o[j] = (row[j] - mean) * invStd * g[j] + b[j];
+  }
+}
+
+/* Linear.forward = x.matmul(W^T) then bias addInPlace: main/nn/Linear.java:23-26.
+ * M==1: Tensor.matmulVec -> matmulVecAccumulate (main/tensor/Tensor.java:383-398,
+ * java26/.../VectorSimdOps.java:114-133): y_j = y_j + x_k * wt[k][j], k ascending, y zeroed.
+ * M>1: Tensor.matmulTiled (main/tensor/Tensor.java:460-489): per element the same ascending-k
+ * sum from 0 (tiles only reorder independent elements), so one loop order serves both.
+ * Bias: Tensor.addInPlace broadcast (main/tensor/Tensor.java:251-263): y = y + b. */
+void orc_linear(const float* x, int m, int k, const float* wt, int n, const float* bias, float* y) {
+  for (int i = 0; i < m; i++) {
+    float* yi = y + (size_t)i * n;
+    const float* xi = x + (size_t)i * k;
+    for (int j = 0; j < n; j++) yi[j] = 0.0f;
+    for (int kk = 0; kk < k; kk++) {
+      float xk = xi[kk];
+      const float* w = wt + (size_t)kk * n;
+      for (int j = 0; j < n; j++) yi[j] = yi[j] + xk * w[j];
+    }
+    if (bias)
+      for (int j = 0; j < n; j++) yi[j] = yi[j] + bias[j];
+  }
+}
+
+/* VectorSimdOps.fusedAttentionHead: java26/.../VectorSimdOps.java:137-203 (scores with the lane
+ * dot, float max, (float)Math.exp, sequential float sum, p = e * (1/sum), out = out + p*v). */
+void orc_attention_head(const float* q, const float* k, const float* v, int kv_len, int hd, float scale,
+                        float* out) {
+  float* scores = (float*)malloc(sizeof(float) * (size_t)(kv_len > 0 ? kv_len : 1));
+  float maxScore = -INFINITY;
+  for (int j = 0; j < kv_len; j++) {
+    float s = orc_dot(q, k + (size_t)j * hd, hd) * scale;
+    scores[j] = s;
+    if (s > maxScore) maxScore = s;
+  }
+  float sum = 0.0f;
+  for (int j = 0; j < kv_len; j++) {
+    scores[j] = (float)exp((double)(scores[j] - maxScore));
+    sum += scores[j];
+  }
+  float invSum = 1.0f / sum;
+  for (int j = 0; j < kv_len; j++) scores[j] *= invSum;
+  for (int d = 0; d < hd; d++) out[d] = 0.0f;
+  for (int j = 0; j < kv_len; j++) {
+    float sj = scores[j];
+    const float* vr = v + (size_t)j * hd;
+    for (int d = 0; d < hd; d++) out[d] = out[d] + sj * vr[d];
+  }
+  free(scores);
+}
+
+/* Tensor.softmax non-Accelerate path: main/tensor/Tensor.java:550-568 (max seeded with row[0]). */
+void orc_softmax_rows(float* x, int rows, int n) {
+  for (int r = 0; r < rows; r++) {
+    float* row = x + (size_t)r * n;
+    float max = row[0];
+    for (int j = 1; j < n; j++)
+      if (row[j] > max) max = row[j];
+    float sum = 0.0f;
+    for (int j = 0; j < n; j++) {
+      row[j] = (float)exp((double)(row[j] - max));
+      sum += row[j];
+    }
+    float invSum = 1.0f / sum;
+    for (int j = 0; j < n; j++) row[j] *= invSum;
+  }
+}
+
+/* WhisperDecoder.argmax: main/nn/WhisperDecoder.java:566-574 (first index of the maximum). */
+int orc_argmax(const float* a, int n) {
+  int best = 0;
+  for (int i = 1; i < n; i++)
+    if (a[i] > a[best]) best = i;
+  return best;
+}
+
+/* WhisperDecoder.computeLogSoftmax: main/nn/WhisperDecoder.java:397-412. */
+void orc_log_softmax(const float* logits, int n, float* out) {
+  float max = -INFINITY;
+  for (int i = 0; i < n; i++)
+    if (logits[i] > max) max = logits[i];
+  double logSum = 0;
+  for (int i = 0; i < n; i++) logSum += exp((double)(logits[i] - max));
+  float logSumF = (float)((double)max + log(logSum));
+  for (int i = 0; i < n; i++) out[i] = logits[i] - logSumF;
+}
+
+/* WhisperDecoder.topkIndices: main/nn/WhisperDecoder.java:415-431 (insertion with strict >,
+ * so ties keep the lower index; unfilled slots keep index 0). */
+void orc_topk(const float* values, int n, int k, int32_t* idx) {
+  float* top = (float*)malloc(sizeof(float) * (size_t)k);
+  for (int i = 0; i < k; i++) { top[i] = -INFINITY; idx[i] = 0; }
+  for (int i = 0; i < n; i++) {
+    if (values[i] > top[k - 1]) {
+      int pos = k - 1;
+      while (pos > 0 && values[i] > top[pos - 1]) pos--;
+      memmove(top + pos + 1, top + pos, sizeof(float) * (size_t)(k - 1 - pos));
+      memmove(idx + pos + 1, idx + pos, sizeof(int32_t) * (size_t)(k - 1 - pos));
+      top[pos] = values[i];
+      idx[pos] = i;
+    }
+  }
+  free(top);
+}
+
+/* WhisperDecoder.compressionRatio: main/nn/WhisperDecoder.java:628-647 (tokens as 2 LE bytes,
+ * java.util.zip.Deflater defaults = zlib stream at the default level). */
+float orc_compression_ratio(const int32_t* tokens, int n) {
+  if (n == 0) return 0.0f;
+  uLong len = (uLong)n * 2;
+  unsigned char* bytes = (unsigned char*)malloc(len);
+  for (int i = 0; i < n; i++) {
+    bytes[2 * i] = (unsigned char)(tokens[i] & 0xff);
+    bytes[2 * i + 1] = (unsigned char)((tokens[i] >> 8) & 0xff);
+  }
+  uLongf clen = compressBound(len);
+  unsigned char* dst = (unsigned char*)malloc(clen);
+  compress2(dst, &clen, bytes, len, Z_DEFAULT_COMPRESSION);
+  free(bytes);
+  free(dst);
+  return (float)len / (float)(clen > 1 ? clen : 1);
+}
+
+/* GgmlLoader.dequantizeQ8_0: main/model/GgmlLoader.java:292-300 (34-byte blocks: f16 d, 32 int8). */
+void orc_dequant_q8_0(const void* src, int64_t n, float* dst) {
+  const unsigned char* p = (const unsigned char*)src;
+  for (int64_t b = 0; b < n / 32; b++) {
+    uint16_t hd = (uint16_t)(p[0] | (p[1] << 8));
+    float scale = orc_f16_to_f32(hd);
+    for (int j = 0; j < 32; j++) dst[b * 32 + j] = (float)(int8_t)p[2 + j] * scale;
+    p += 34;
+  }
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Model                                                                                        */
+
+typedef struct {
+  float *wt, *b; /* wt: [in][out] (Linear's transposed copy), b may be NULL */
+  int in, out;
+} orc_lin;
+
+typedef struct {
+  orc_lin q, k, v, o;
+} orc_mha;
+
+typedef struct {
+  orc_mha attn, cross;
+  float *attn_ln_g, *attn_ln_b, *cross_ln_g, *cross_ln_b, *mlp_ln_g, *mlp_ln_b;
+  orc_lin mlp1, mlp2;
+} orc_block;
+
+struct orc_model {
+  orc_dims d;
+  float* tok_emb; /* [V][d] */
+  float* pos_emb; /* [ctx][d] */
+  float *ln_g, *ln_b;
+  orc_block* blocks;
+};
+
+static const orc_tensor* find_tensor(const orc_tensor* t, int n, const char* name) {
+  for (int i = 0; i < n; i++)
+    if (strcmp(t[i].name, name) == 0) return &t[i];
+  return NULL;
+}
+
+/* GgmlLoader.dequantize (F32 slice, F16 exact widening, Q8_0): main/model/GgmlLoader.java:186-201, 224-238 */
+static float* load_f32(const orc_tensor* tab, int ntab, const char* name, int64_t expect, char* err, int errlen) {
+  const orc_tensor* t = find_tensor(tab, ntab, name);
+  if (!t) {
+    snprintf(err, errlen, "missing tensor: %s", name);
+    return NULL;
+  }
+  int64_t numel = 1;
+  for (int i = 0; i < t->n_dims; i++) numel *= t->ne[i];
+  if (numel != expect) {
+    snprintf(err, errlen, "tensor %s has %lld elements, expected %lld", name, (long long)numel, (long long)expect);
+    return NULL;
+  }
+  float* out = (float*)malloc(sizeof(float) * (size_t)numel);
+  if (t->type == ORC_TYPE_F32) {
+    memcpy(out, t->data, sizeof(float) * (size_t)numel);
+  } else if (t->type == ORC_TYPE_F16) {
+    const uint16_t* h = (const uint16_t*)t->data;
+    for (int64_t i = 0; i < numel; i++) out[i] = orc_f16_to_f32(h[i]);
+  } else if (t->type == ORC_TYPE_Q8_0) {
+    if (numel % 32) {
+      snprintf(err, errlen, "tensor %s: q8_0 needs a multiple of 32 elements", name);
+      free(out);
+      return NULL;
+    }
+    orc_dequant_q8_0(t->data, numel, out);
+  } else {
+    snprintf(err, errlen, "tensor %s: unsupported type %d", name, t->type);
+    free(out);
+    return NULL;
+  }
+  return out;
+}
+
+/* Linear ctor: weight.transposeNative() (main/nn/Linear.java:16-19, main/tensor/Tensor.java:191-212) */
+static int load_lin(orc_lin* l, const orc_tensor* tab, int ntab, const char* wname, const char* bname, int in,
+                    int out, char* err, int errlen) {
+  float* w = load_f32(tab, ntab, wname, (int64_t)in * out, err, errlen); /* [out][in] */
+  if (!w) return -1;
+  l->wt = (float*)malloc(sizeof(float) * (size_t)in * out);
+  for (int r = 0; r < out; r++)
+    for (int c = 0; c < in; c++) l->wt[(size_t)c * out + r] = w[(size_t)r * in + c];
+  free(w);
+  l->b = NULL;
+  if (bname && find_tensor(tab, ntab, bname)) {
+    l->b = load_f32(tab, ntab, bname, out, err, errlen);
+    if (!l->b) return -1;
+  }
+  l->in = in;
+  l->out = out;
+  return 0;
+}
+
+static void free_lin(orc_lin* l) {
+  free(l->wt);
+  free(l->b);
+}
+
+void orc_model_destroy(orc_model* m) {
+  if (!m) return;
+  free(m->tok_emb);
+  free(m->pos_emb);
+  free(m->ln_g);
+  free(m->ln_b);
+  if (m->blocks) {
+    for (int i = 0; i < m->d.n_text_layer; i++) {
+      orc_block* b = &m->blocks[i];
+      orc_lin* ls[] = {&b->attn.q, &b->attn.k, &b->attn.v, &b->attn.o, &b->cross.q, &b->cross.k,
+                       &b->cross.v, &b->cross.o, &b->mlp1, &b->mlp2};
+      for (size_t j = 0; j < sizeof(ls) / sizeof(ls[0]); j++) free_lin(ls[j]);
+      free(b->attn_ln_g); free(b->attn_ln_b); free(b->cross_ln_g); free(b->cross_ln_b);
+      free(b->mlp_ln_g); free(b->mlp_ln_b);
+    }
+    free(m->blocks);
+  }
+  free(m);
+}
+
+/* WhisperDecoder ctor + buildDecoderBlock + WhisperEncoder.buildMHA:
+ * main/nn/WhisperDecoder.java:36-56, 658-669; main/nn/WhisperEncoder.java:98-105 (key bias optional). */
+orc_model* orc_model_create(const orc_dims* dims, const orc_tensor* tab, int ntab, char* err, int errlen) {
+  orc_model* m = (orc_model*)calloc(1, sizeof(orc_model));
+  m->d = *dims;
+  int d = dims->n_text_state, V = dims->n_vocab, C = dims->n_text_ctx, L = dims->n_text_layer;
+  char nb[256], bb[256];
+  if (d % 64 != 0 || dims->n_text_head * 64 != d) {
+    snprintf(err, errlen, "n_text_state %d must equal 64 * n_text_head %d", d, dims->n_text_head);
+    goto fail;
+  }
+  if (!(m->tok_emb = load_f32(tab, ntab, "decoder.token_embedding.weight", (int64_t)V * d, err, errlen))) goto fail;
+  if (!(m->pos_emb = load_f32(tab, ntab, "decoder.positional_embedding", (int64_t)C * d, err, errlen))) goto fail;
+  if (!(m->ln_g = load_f32(tab, ntab, "decoder.ln.weight", d, err, errlen))) goto fail;
+  if (!(m->ln_b = load_f32(tab, ntab, "decoder.ln.bias", d, err, errlen))) goto fail;
+  m->blocks = (orc_block*)calloc((size_t)L, sizeof(orc_block));
+  for (int i = 0; i < L; i++) {
+    orc_block* b = &m->blocks[i];
+    const char* mh[2] = {"attn", "cross_attn"};
+    orc_mha* mp[2] = {&b->attn, &b->cross};
+    for (int a = 0; a < 2; a++) {
+      const char* pr[4] = {"query", "key", "value", "out"};
+      orc_lin* lp[4] = {&mp[a]->q, &mp[a]->k, &mp[a]->v, &mp[a]->o};
+      for (int j = 0; j < 4; j++) {
+        snprintf(nb, sizeof nb, "decoder.blocks.%d.%s.%s.weight", i, mh[a], pr[j]);
+        snprintf(bb, sizeof bb, "decoder.blocks.%d.%s.%s.bias", i, mh[a], pr[j]);
+        if (j != 1 && !find_tensor(tab, ntab, bb)) {
+          snprintf(err, errlen, "missing tensor: %s", bb);
+          goto fail;
+        }
+        if (load_lin(lp[j], tab, ntab, nb, bb, d, d, err, errlen)) goto fail;
+      }
+    }
+    const char* lnn[3] = {"attn_ln", "cross_attn_ln", "mlp_ln"};
+    float** lg[3] = {&b->attn_ln_g, &b->cross_ln_g, &b->mlp_ln_g};
+    float** lb[3] = {&b->attn_ln_b, &b->cross_ln_b, &b->mlp_ln_b};
+    for (int j = 0; j < 3; j++) {
+      snprintf(nb, sizeof nb, "decoder.blocks.%d.%s.weight", i, lnn[j]);
+      if (!(*lg[j] = load_f32(tab, ntab, nb, d, err, errlen))) goto fail;
+      snprintf(nb, sizeof nb, "decoder.blocks.%d.%s.bias", i, lnn[j]);
+      if (!(*lb[j] = load_f32(tab, ntab, nb, d, err, errlen))) goto fail;
+    }
+    snprintf(nb, sizeof nb, "decoder.blocks.%d.mlp.0.weight", i);
+    snprintf(bb, sizeof bb, "decoder.blocks.%d.mlp.0.bias", i);
+    if (load_lin(&b->mlp1, tab, ntab, nb, bb, d, 4 * d, err, errlen)) goto fail;
+    snprintf(nb, sizeof nb, "decoder.blocks.%d.mlp.2.weight", i);
+    snprintf(bb, sizeof bb, "decoder.blocks.%d.mlp.2.bias", i);
+    if (load_lin(&b->mlp2, tab, ntab, nb, bb, 4 * d, d, err, errlen)) goto fail;
+  }
+  return m;
+fail:
+  orc_model_destroy(m);
+  return NULL;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* KV cache: the reference keeps a HashMap<String,Tensor> per decode call; appends allocate a new
+ * (H, L+n, 64) tensor and copy (main/nn/MultiHeadAttention.java:140-164), beams copy the map so
+ * tensors are shared (main/nn/WhisperDecoder.java:239-266, 342-361).  Here: refcounted tensors in
+ * a refcounted per-call cache.                                                                 */
+
+typedef struct {
+  int refs;
+  int h, len, hd;
+  float* data; /* [h][len][hd] */
+} orc_kv;
+
+struct orc_cache {
+  int refs;
+  int n_layer;
+  orc_kv** self_k;
+  orc_kv** self_v;
+  orc_kv** cross_k;
+  orc_kv** cross_v;
+};
+
+static orc_kv* kv_new(int h, int len, int hd) {
+  orc_kv* t = (orc_kv*)malloc(sizeof(orc_kv));
+  t->refs = 1;
+  t->h = h;
+  t->len = len;
+  t->hd = hd;
+  t->data = (float*)malloc(sizeof(float) * (size_t)h * (size_t)(len > 0 ? len : 1) * hd);
+  return t;
+}
+static void kv_unref(orc_kv* t) {
+  if (t && --t->refs == 0) {
+    free(t->data);
+    free(t);
+  }
+}
+static orc_kv* kv_ref(orc_kv* t) {
+  if (t) t->refs++;
+  return t;
+}
+
+orc_cache* orc_cache_create(const orc_model* m) {
+  orc_cache* c = (orc_cache*)calloc(1, sizeof(orc_cache));
+  c->refs = 1;
+  c->n_layer = m->d.n_text_layer;
+  c->self_k = (orc_kv**)calloc((size_t)c->n_layer, sizeof(orc_kv*));
+  c->self_v = (orc_kv**)calloc((size_t)c->n_layer, sizeof(orc_kv*));
+  c->cross_k = (orc_kv**)calloc((size_t)c->n_layer, sizeof(orc_kv*));
+  c->cross_v = (orc_kv**)calloc((size_t)c->n_layer, sizeof(orc_kv*));
+  return c;
+}
+
+void orc_cache_destroy(orc_cache* c) {
+  if (!c || --c->refs > 0) return;
+  for (int i = 0; i < c->n_layer; i++) {
+    kv_unref(c->self_k[i]);
+    kv_unref(c->self_v[i]);
+    kv_unref(c->cross_k[i]);
+    kv_unref(c->cross_v[i]);
+  }
+  free(c->self_k);
+  free(c->self_v);
+  free(c->cross_k);
+  free(c->cross_v);
+  free(c);
+}
+
+int orc_cache_len(const orc_cache* c) { return (c && c->self_k[0]) ? c->self_k[0]->len : 0; }
+
+/* new map with the same entries (tensors shared) */
+static orc_cache* cache_copy(const orc_cache* s) {
+  orc_cache* c = (orc_cache*)calloc(1, sizeof(orc_cache));
+  c->refs = 1;
+  c->n_layer = s->n_layer;
+  c->self_k = (orc_kv**)calloc((size_t)c->n_layer, sizeof(orc_kv*));
+  c->self_v = (orc_kv**)calloc((size_t)c->n_layer, sizeof(orc_kv*));
+  c->cross_k = (orc_kv**)calloc((size_t)c->n_layer, sizeof(orc_kv*));
+  c->cross_v = (orc_kv**)calloc((size_t)c->n_layer, sizeof(orc_kv*));
+  for (int i = 0; i < c->n_layer; i++) {
+    c->self_k[i] = kv_ref(s->self_k[i]);
+    c->self_v[i] = kv_ref(s->self_v[i]);
+    c->cross_k[i] = kv_ref(s->cross_k[i]);
+    c->cross_v[i] = kv_ref(s->cross_v[i]);
+  }
+  return c;
+}
+
+/* (S, H*hd) -> (H, S, hd): Tensor.rearrangeToHeads main/tensor/Tensor.java:645-659 */
+static void to_heads(const float* x, int s, int h, int hd, float* out) {
+  for (int t = 0; t < s; t++)
+    for (int i = 0; i < h; i++) memcpy(out + ((size_t)i * s + t) * hd, x + ((size_t)t * h + i) * hd, sizeof(float) * hd);
+}
+
+/* appendHeadsCache: main/nn/MultiHeadAttention.java:140-164 */
+static orc_kv* kv_append(orc_kv* old, const float* heads, int n, int h, int hd) {
+  int ol = old ? old->len : 0;
+  orc_kv* t = kv_new(h, ol + n, hd);
+  for (int i = 0; i < h; i++) {
+    float* dst = t->data + (size_t)i * t->len * hd;
+    if (ol) memcpy(dst, old->data + (size_t)i * ol * hd, sizeof(float) * (size_t)ol * hd);
+    memcpy(dst + (size_t)ol * hd, heads + (size_t)i * n * hd, sizeof(float) * (size_t)n * hd);
+  }
+  return t;
+}
+
+/* MultiHeadAttention.forward: main/nn/MultiHeadAttention.java:37-96, with the fused M==1 branch
+ * (:80-82, :110-132) and the unfused masked branch (:84-95). */
+static void mha_forward(const orc_model* m, const orc_mha* a, const float* x, int n, const float* xa,
+                        orc_cache* cache, int layer, int is_cross, float* out) {
+  int d = m->d.n_text_state, H = m->d.n_text_head, hd = 64, A = m->d.n_audio_ctx;
+  float scale = (float)(1.0 / sqrt((double)hd));
+  float* q = (float*)malloc(sizeof(float) * (size_t)n * d);
+  orc_linear(x, n, d, a->q.wt, d, a->q.b, q);
+  orc_kv **kslot = is_cross ? &cache->cross_k[layer] : &cache->self_k[layer];
+  orc_kv **vslot = is_cross ? &cache->cross_v[layer] : &cache->self_v[layer];
+  orc_kv *kr, *vr;
+  if (is_cross && *kslot) {
+    kr = *kslot;
+    vr = *vslot;
+  } else if (!is_cross && *kslot) {
+    float* nk = (float*)malloc(sizeof(float) * (size_t)n * d);
+    float* nv = (float*)malloc(sizeof(float) * (size_t)n * d);
+    float* hk = (float*)malloc(sizeof(float) * (size_t)n * d);
+    float* hv = (float*)malloc(sizeof(float) * (size_t)n * d);
+    orc_linear(x, n, d, a->k.wt, d, a->k.b, nk);
+    orc_linear(x, n, d, a->v.wt, d, a->v.b, nv);
+    to_heads(nk, n, H, hd, hk);
+    to_heads(nv, n, H, hd, hv);
+    orc_kv* ak = kv_append(*kslot, hk, n, H, hd);
+    orc_kv* av = kv_append(*vslot, hv, n, H, hd);
+    kv_unref(*kslot);
+    kv_unref(*vslot);
+    *kslot = ak;
+    *vslot = av;
+    kr = ak;
+    vr = av;
+    free(nk); free(nv); free(hk); free(hv);
+  } else {
+    const float* src = is_cross ? xa : x;
+    int sl = is_cross ? A : n;
+    float* k = (float*)malloc(sizeof(float) * (size_t)sl * d);
+    float* v = (float*)malloc(sizeof(float) * (size_t)sl * d);
+    orc_linear(src, sl, d, a->k.wt, d, a->k.b, k);
+    orc_linear(src, sl, d, a->v.wt, d, a->v.b, v);
+    kr = kv_new(H, sl, hd);
+    vr = kv_new(H, sl, hd);
+    to_heads(k, sl, H, hd, kr->data);
+    to_heads(v, sl, H, hd, vr->data);
+    free(k);
+    free(v);
+    *kslot = kr;
+    *vslot = vr;
+  }
+  int kvLen = kr->len;
+  float* merged = (float*)malloc(sizeof(float) * (size_t)n * d);
+  if (n == 1) {
+    for (int h = 0; h < H; h++)
+      orc_attention_head(q + (size_t)h * hd, kr->data + (size_t)h * kvLen * hd, vr->data + (size_t)h * kvLen * hd,
+                         kvLen, hd, scale, merged + (size_t)h * hd);
+  } else {
+    /* qr.matmulTransB(kr, scale) -> addMaskInPlace (no offset) -> softmax -> matmul(vr) */
+    int C = m->d.n_text_ctx;
+    float* w = (float*)malloc(sizeof(float) * (size_t)H * n * kvLen);
+    float* qr = (float*)malloc(sizeof(float) * (size_t)n * d);
+    to_heads(q, n, H, hd, qr);
+    for (int h = 0; h < H; h++)
+      for (int i = 0; i < n; i++)
+        for (int j = 0; j < kvLen; j++)
+          w[((size_t)h * n + i) * kvLen + j] =
+              orc_dot(qr + ((size_t)h * n + i) * hd, kr->data + ((size_t)h * kvLen + j) * hd, hd) * scale;
+    if (!is_cross) { /* mask passed only to self-attention (main/nn/ResidualAttentionBlock.java:46-47) */
+      int aq = n < C ? n : C, ak = kvLen < C ? kvLen : C;
+      for (int h = 0; h < H; h++)
+        for (int i = 0; i < aq; i++)
+          for (int j = 0; j < ak; j++) {
+            float mv = j > i ? -INFINITY : 0.0f;
+            w[((size_t)h * n + i) * kvLen + j] = w[((size_t)h * n + i) * kvLen + j] + mv;
+          }
+    }
+    orc_softmax_rows(w, H * n, kvLen);
+    for (int h = 0; h < H; h++)
+      for (int i = 0; i < n; i++) {
+        float* o = merged + (size_t)i * d + (size_t)h * hd; /* rearrangeFromHeads */
+        for (int e = 0; e < hd; e++) o[e] = 0.0f;
+        for (int j = 0; j < kvLen; j++) {
+          float p = w[((size_t)h * n + i) * kvLen + j];
+          const float* vv = vr->data + ((size_t)h * kvLen + j) * hd;
+          for (int e = 0; e < hd; e++) o[e] = o[e] + p * vv[e];
+        }
+      }
+    free(w);
+    free(qr);
+  }
+  orc_linear(merged, n, d, a->o.wt, d, a->o.b, out);
+  free(merged);
+  free(q);
+}
+
+/* WhisperDecoder.forwardWithAttn: main/nn/WhisperDecoder.java:66-104;
+ * ResidualAttentionBlock.forwardWithAttn: main/nn/ResidualAttentionBlock.java:42-60. */
+int orc_forward(const orc_model* m, const int32_t* tokens, int n, const float* xa, orc_cache* cache,
+                float* logits) {
+  int d = m->d.n_text_state, C = m->d.n_text_ctx, V = m->d.n_vocab;
+  int offset = 0;
+  if (cache) {
+    int inf = orc_cache_len(cache);
+    offset = inf < C - n ? inf : C - n;
+  }
+  for (int t = 0; t < n; t++)
+    if (tokens[t] < 0 || tokens[t] >= V) return -1;
+  if (offset < 0 || offset + n > C) return -2;
+  float* x = (float*)malloc(sizeof(float) * (size_t)n * d);
+  float* h = (float*)malloc(sizeof(float) * (size_t)n * d);
+  float* a = (float*)malloc(sizeof(float) * (size_t)n * d);
+  float* f = (float*)malloc(sizeof(float) * (size_t)n * 4 * d);
+  for (int t = 0; t < n; t++)
+    for (int j = 0; j < d; j++)
+      x[(size_t)t * d + j] = m->tok_emb[(size_t)tokens[t] * d + j] + m->pos_emb[(size_t)(offset + t) * d + j];
+  orc_cache* tmp = cache ? NULL : orc_cache_create(m);
+  orc_cache* c = cache ? cache : tmp;
+  for (int l = 0; l < m->d.n_text_layer; l++) {
+    const orc_block* b = &m->blocks[l];
+    orc_layernorm(x, n, d, b->attn_ln_g, b->attn_ln_b, 1e-5f, h);
+    if (!cache) { /* forward without a cache: fresh K/V each call */
+      kv_unref(c->self_k[l]); kv_unref(c->self_v[l]);
+      c->self_k[l] = c->self_v[l] = NULL;
+    }
+    mha_forward(m, &b->attn, h, n, NULL, c, l, 0, a);
+    for (size_t i = 0; i < (size_t)n * d; i++) x[i] = a[i] + x[i];
+    orc_layernorm(x, n, d, b->cross_ln_g, b->cross_ln_b, 1e-5f, h);
+    mha_forward(m, &b->cross, h, n, xa, c, l, 1, a);
+    for (size_t i = 0; i < (size_t)n * d; i++) x[i] = x[i] + a[i];
+    orc_layernorm(x, n, d, b->mlp_ln_g, b->mlp_ln_b, 1e-5f, h);
+    orc_linear(h, n, d, b->mlp1.wt, 4 * d, b->mlp1.b, f);
+    orc_gelu(f, n * 4 * d);
+    orc_linear(f, n, 4 * d, b->mlp2.wt, d, b->mlp2.b, a);
+    for (size_t i = 0; i < (size_t)n * d; i++) x[i] = x[i] + a[i];
+  }
+  orc_layernorm(x, n, d, m->ln_g, m->ln_b, 1e-5f, h);
+  /* x.matmulTransB(tokenEmbedding, 1f): main/tensor/Tensor.java:327-340 (M==1) and :357-371 */
+  for (int t = 0; t < n; t++)
+    for (int v = 0; v < V; v++)
+      logits[(size_t)t * V + v] = orc_dot(h + (size_t)t * d, m->tok_emb + (size_t)v * d, d) * 1.0f;
+  if (tmp) orc_cache_destroy(tmp);
+  free(x); free(h); free(a); free(f);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Logit rules and selection: main/nn/WhisperDecoder.java:442-626                               */
+
+static float softmax_at(const float* l, int n, int index) { /* :600-612 */
+  float max = -INFINITY;
+  for (int i = 0; i < n; i++)
+    if (l[i] > max) max = l[i];
+  double sum = 0;
+  for (int i = 0; i < n; i++) sum += exp((double)(l[i] - max));
+  return (float)(exp((double)(l[index] - max)) / sum);
+}
+
+static double log_softmax_at(const float* l, int n, int index) { /* :614-626 */
+  float max = -INFINITY;
+  for (int i = 0; i < n; i++)
+    if (l[i] > max) max = l[i];
+  double logSum = 0;
+  for (int i = 0; i < n; i++) logSum += exp((double)(l[i] - max));
+  return (double)(l[index] - max) - log(logSum);
+}
+
+static void suppress_blank(float* l, int n, int eot) { /* :450-455 */
+  l[eot] = -INFINITY;
+  if (220 < n) l[220] = -INFINITY;
+}
+
+static void apply_suppress(float* l, const int32_t* s, int ns, int n) { /* :457-466 */
+  if (!s) return;
+  for (int i = 0; i < ns; i++)
+    if (s[i] >= 0 && s[i] < n) l[s[i]] = -INFINITY;
+}
+
+static void ngram_block(float* l, const int32_t* g, int cnt, int nn, int nvocab) { /* :543-564 */
+  if (cnt < nn - 1) return;
+  for (int i = 0; i <= cnt - nn; i++) {
+    int match = 1;
+    for (int j = 0; j < nn - 1; j++)
+      if (g[i + j] != g[cnt - (nn - 1) + j]) { match = 0; break; }
+    if (match) {
+      int blocked = g[i + nn - 1];
+      if (blocked >= 0 && blocked < nvocab) l[blocked] = -INFINITY;
+    }
+  }
+}
+
+static void repetition_penalty(float* l, const int32_t* g, int cnt, int nvocab) { /* :472-476 */
+  ngram_block(l, g, cnt, 3, nvocab);
+  ngram_block(l, g, cnt, 4, nvocab);
+}
+
+static void timestamp_rules(float* l, const int32_t* g, int cnt, int tsb, int eot, int nvocab, int first) {
+  /* :484-541 */
+  if (tsb > 0 && tsb - 1 >= 0 && tsb - 1 < nvocab) l[tsb - 1] = -INFINITY;
+  if (first) {
+    for (int i = 0; i < tsb && i < nvocab; i++) l[i] = -INFINITY;
+    int lastAllowed = tsb + 50;
+    for (int i = lastAllowed + 1; i < nvocab; i++) l[i] = -INFINITY;
+    return;
+  }
+  if (cnt == 0) return;
+  int lastWasTs = g[cnt - 1] >= tsb;
+  int penultimateWasTs = cnt < 2 || g[cnt - 2] >= tsb;
+  if (lastWasTs) {
+    if (penultimateWasTs) {
+      for (int i = tsb; i < nvocab; i++) l[i] = -INFINITY;
+    } else {
+      for (int i = 0; i < eot && i < nvocab; i++) l[i] = -INFINITY;
+    }
+  }
+  int lastTs = -1;
+  for (int i = cnt - 1; i >= 0; i--)
+    if (g[i] >= tsb) { lastTs = g[i]; break; }
+  if (lastTs >= 0) {
+    int blockUpTo = (lastWasTs && !penultimateWasTs) ? lastTs + 1 : lastTs;
+    for (int i = tsb; i < blockUpTo && i < nvocab; i++) l[i] = -INFINITY;
+  }
+}
+
+/* Math.random() replaced by a seeded SplitMix64 -> [0,1) so runs repeat (the reference's draw is
+ * unseeded). */
+static double rng_uniform(uint64_t* s) {
+  uint64_t z = (*s += 0x9e3779b97f4a7c15ull);
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  z ^= z >> 31;
+  return (double)(z >> 11) * (1.0 / 9007199254740992.0);
+}
+
+static int sample_tok(float* l, int n, float temperature, uint64_t* rng) { /* :576-598 (mutates l) */
+  float max = -INFINITY;
+  for (int i = 0; i < n; i++)
+    if (l[i] > max) max = l[i];
+  double sum = 0;
+  for (int i = 0; i < n; i++) {
+    double p = exp((double)((l[i] - max) / temperature));
+    l[i] = (float)p;
+    sum += p;
+  }
+  double r = rng_uniform(rng) * sum;
+  double cum = 0;
+  for (int i = 0; i < n; i++) {
+    cum += l[i];
+    if (cum >= r) return i;
+  }
+  return n - 1;
+}
+
+/* WhisperDecoder.decode: main/nn/WhisperDecoder.java:161-204 */
+int orc_decode(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, int eot, int max_tokens,
+               const int32_t* suppress, int n_suppress, int no_speech, float temperature, int ts_begin,
+               uint64_t seed, orc_result* out) {
+  int V = m->d.n_vocab;
+  if (max_tokens > 1024) return -3;
+  orc_cache* cache = orc_cache_create(m);
+  int32_t generated[1024];
+  int genCount = 0;
+  double sumLogprob = 0;
+  float noSpeechProb = 0;
+  uint64_t rng = seed;
+  const int32_t* cur = prompt;
+  int ncur = n_prompt;
+  int32_t one;
+  float* logits = (float*)malloc(sizeof(float) * (size_t)(n_prompt > 1 ? n_prompt : 1) * V);
+  for (int step = 0; step < max_tokens; step++) {
+    if (orc_forward(m, cur, ncur, xa, cache, logits)) {
+      free(logits);
+      orc_cache_destroy(cache);
+      return -1;
+    }
+    float* last = logits + (size_t)(ncur - 1) * V;
+    if (step == 0) {
+      noSpeechProb = (no_speech < 0 || no_speech >= V) ? 0.0f : softmax_at(logits, V, no_speech);
+      suppress_blank(last, V, eot);
+    }
+    apply_suppress(last, suppress, n_suppress, V);
+    repetition_penalty(last, generated, genCount, V);
+    if (ts_begin > 0) timestamp_rules(last, generated, genCount, ts_begin, eot, V, step == 0);
+    int best = temperature == 0.0f ? orc_argmax(last, V) : sample_tok(last, V, temperature, &rng);
+    sumLogprob += log_softmax_at(last, V, best);
+    if (best == eot) break;
+    generated[genCount++] = best;
+    one = best;
+    cur = &one;
+    ncur = 1;
+  }
+  free(logits);
+  orc_cache_destroy(cache);
+  out->n_tokens = genCount;
+  memcpy(out->tokens, generated, sizeof(int32_t) * (size_t)genCount);
+  out->avg_logprob = genCount > 0 ? (float)(sumLogprob / genCount) : 0.0f;
+  out->compression_ratio = orc_compression_ratio(generated, genCount);
+  out->no_speech_prob = noSpeechProb;
+  out->temperature = temperature;
+  return 0;
+}
+
+typedef struct {
+  double score;
+  int beam, tok;
+} cand_t;
+
+/* WhisperDecoder.decodeBeam: main/nn/WhisperDecoder.java:214-394 */
+int orc_decode_beam(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, int eot,
+                    int max_tokens, const int32_t* suppress, int n_suppress, int no_speech, int ts_begin, int beam,
+                    orc_result* out) {
+  int V = m->d.n_vocab;
+  if (max_tokens > 1024 || beam < 1 || beam > 16) return -3;
+  orc_cache** caches = (orc_cache**)calloc((size_t)beam, sizeof(orc_cache*));
+  int32_t(*toks)[1024] = calloc((size_t)beam, sizeof(*toks));
+  int* lens = (int*)calloc((size_t)beam, sizeof(int));
+  double* lps = (double*)calloc((size_t)beam, sizeof(double));
+  int maxfin = beam + beam * (beam + 1) + 1;
+  int32_t(*fin_t)[1024] = calloc((size_t)maxfin, sizeof(*fin_t));
+  int* fin_len = (int*)calloc((size_t)maxfin, sizeof(int));
+  double* fin_lp = (double*)calloc((size_t)maxfin, sizeof(double));
+  int nfin = 0;
+  float* logits = (float*)malloc(sizeof(float) * (size_t)(n_prompt > 1 ? n_prompt : 1) * V);
+  float* lp = (float*)malloc(sizeof(float) * (size_t)V);
+  int32_t* top = (int32_t*)malloc(sizeof(int32_t) * (size_t)(beam + 1));
+  cand_t* cands = (cand_t*)malloc(sizeof(cand_t) * (size_t)beam * (beam + 1));
+  caches[0] = orc_cache_create(m);
+  orc_forward(m, prompt, n_prompt, xa, caches[0], logits);
+  float noSpeechProb = (no_speech < 0 || no_speech >= V) ? 0.0f : softmax_at(logits, V, no_speech);
+  float* last0 = logits + (size_t)(n_prompt - 1) * V;
+  suppress_blank(last0, V, eot);
+  apply_suppress(last0, suppress, n_suppress, V);
+  orc_log_softmax(last0, V, lp);
+  orc_topk(lp, V, beam, top);
+  for (int b = 0; b < beam; b++) {
+    toks[b][0] = top[b];
+    lens[b] = 1;
+    lps[b] = (double)lp[top[b]];
+    if (b > 0) caches[b] = cache_copy(caches[0]); /* cross + self entries shared by reference */
+  }
+  for (int step = 1; step < max_tokens; step++) {
+    int nc = 0;
+    for (int b = 0; b < beam; b++) {
+      if (toks[b][lens[b] - 1] == eot) continue;
+      int32_t lt = toks[b][lens[b] - 1];
+      orc_forward(m, &lt, 1, xa, caches[b], logits);
+      apply_suppress(logits, suppress, n_suppress, V);
+      repetition_penalty(logits, toks[b], lens[b], V);
+      if (ts_begin > 0) timestamp_rules(logits, toks[b], lens[b], ts_begin, eot, V, 0);
+      orc_log_softmax(logits, V, lp);
+      orc_topk(lp, V, beam + 1, top);
+      for (int k = 0; k < beam + 1; k++) {
+        cands[nc].score = lps[b] + (double)lp[top[k]];
+        cands[nc].beam = b;
+        cands[nc].tok = top[k];
+        nc++;
+      }
+    }
+    if (nc == 0) break;
+    /* candidates.sort(descending): stable insertion sort on double scores (List.sort is stable) */
+    for (int i = 1; i < nc; i++) {
+      cand_t c = cands[i];
+      int j = i - 1;
+      while (j >= 0 && cands[j].score < c.score) {
+        cands[j + 1] = cands[j];
+        j--;
+      }
+      cands[j + 1] = c;
+    }
+    int32_t(*ntoks)[1024] = calloc((size_t)beam, sizeof(*ntoks));
+    int* nlens = (int*)calloc((size_t)beam, sizeof(int));
+    double* nlps = (double*)calloc((size_t)beam, sizeof(double));
+    int* src = (int*)calloc((size_t)beam, sizeof(int));
+    int saved = 0;
+    for (int ci = 0; ci < nc; ci++) {
+      int sb = cands[ci].beam, tok = cands[ci].tok;
+      double score = cands[ci].score;
+      if (tok == eot) {
+        memcpy(fin_t[nfin], toks[sb], sizeof(int32_t) * (size_t)lens[sb]);
+        fin_len[nfin] = lens[sb];
+        fin_lp[nfin] = score;
+        nfin++;
+        if (nfin >= beam) break;
+        continue;
+      }
+      if (saved >= beam) continue;
+      memcpy(ntoks[saved], toks[sb], sizeof(int32_t) * (size_t)lens[sb]);
+      ntoks[saved][lens[sb]] = tok;
+      nlens[saved] = lens[sb] + 1;
+      nlps[saved] = score;
+      src[saved] = sb;
+      saved++;
+    }
+    int stop = (saved == 0 || nfin >= beam);
+    if (!stop) {
+      orc_cache** nc2 = (orc_cache**)calloc((size_t)beam, sizeof(orc_cache*));
+      for (int b = 0; b < saved; b++) {
+        if (src[b] == b) {
+          nc2[b] = caches[b];
+          caches[b]->refs++;
+        } else {
+          nc2[b] = cache_copy(caches[src[b]]);
+        }
+      }
+      for (int b = saved; b < beam; b++) { /* leftover beams alias beam 0's map (:356-361) */
+        nc2[b] = nc2[0];
+        nc2[0]->refs++;
+        memcpy(ntoks[b], ntoks[0], sizeof(int32_t) * (size_t)nlens[0]);
+        nlens[b] = nlens[0];
+        nlps[b] = nlps[0];
+      }
+      for (int b = 0; b < beam; b++) orc_cache_destroy(caches[b]);
+      free(caches);
+      caches = nc2;
+      memcpy(toks, ntoks, sizeof(*toks) * (size_t)beam);
+      memcpy(lens, nlens, sizeof(int) * (size_t)beam);
+      memcpy(lps, nlps, sizeof(double) * (size_t)beam);
+    }
+    free(ntoks); free(nlens); free(nlps); free(src);
+    if (stop) break;
+  }
+  if (nfin < beam) {
+    for (int b = 0; b < beam && nfin < beam; b++) {
+      memcpy(fin_t[nfin], toks[b], sizeof(int32_t) * (size_t)lens[b]);
+      fin_len[nfin] = lens[b];
+      fin_lp[nfin] = lps[b];
+      nfin++;
+    }
+  }
+  int bestIdx = 0;
+  double bestScore = -INFINITY;
+  for (int i = 0; i < nfin; i++) {
+    double score = fin_lp[i] / (double)(fin_len[i] > 1 ? fin_len[i] : 1);
+    if (score > bestScore) {
+      bestScore = score;
+      bestIdx = i;
+    }
+  }
+  out->n_tokens = fin_len[bestIdx];
+  memcpy(out->tokens, fin_t[bestIdx], sizeof(int32_t) * (size_t)fin_len[bestIdx]);
+  out->avg_logprob = fin_len[bestIdx] > 0 ? (float)(fin_lp[bestIdx] / fin_len[bestIdx]) : 0.0f;
+  out->compression_ratio = orc_compression_ratio(out->tokens, out->n_tokens);
+  out->no_speech_prob = noSpeechProb;
+  out->temperature = 0.0f;
+  for (int b = 0; b < beam; b++) orc_cache_destroy(caches[b]);
+  free(caches); free(toks); free(lens); free(lps); free(fin_t); free(fin_len); free(fin_lp);
+  free(logits); free(lp); free(top); free(cands);
+  return 0;
+}
+
+static int needs_fallback(const orc_result* r) { /* :435-440 */
+  if (r->compression_ratio > 2.4f) return !(r->no_speech_prob > 0.6f && r->avg_logprob < -1.0f);
+  return r->avg_logprob < -1.0f && !(r->no_speech_prob > 0.6f);
+}
+
+/* WhisperDecoder.decodeWithFallback: main/nn/WhisperDecoder.java:119-149 */
+int orc_decode_with_fallback(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, int eot,
+                             int max_tokens, const int32_t* suppress, int n_suppress, int no_speech, int ts_begin,
+                             int beam, uint64_t seed, orc_result* out) {
+  const float temps[6] = {0.0f, 0.2f, 0.4f, 0.6f, 0.8f, 1.0f};
+  orc_result cur, best;
+  int have = 0;
+  for (int i = 0; i < 6; i++) {
+    float t = temps[i];
+    int rc = (beam > 1 && t == 0.0f)
+                 ? orc_decode_beam(m, xa, prompt, n_prompt, eot, max_tokens, suppress, n_suppress, no_speech, ts_begin,
+                                   beam, &cur)
+                 : orc_decode(m, xa, prompt, n_prompt, eot, max_tokens, suppress, n_suppress, no_speech, t, ts_begin,
+                              seed + (uint64_t)i, &cur);
+    if (rc) return rc;
+    if (!needs_fallback(&cur)) {
+      *out = cur;
+      return 0;
+    }
+    if (!have || cur.avg_logprob > best.avg_logprob) {
+      best = cur;
+      have = 1;
+    }
+    if (t == 0.0f && cur.compression_ratio <= 2.4f) break;
+    if (t > 0.0f && cur.avg_logprob < best.avg_logprob - 1.0f) break;
+  }
+  *out = best;
+  return 0;
+}
+
+/* Teacher-forced greedy sweep (the workload of the parity tests and the CPU baseline). */
+int orc_forced(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, const int32_t* forced,
+               int n_steps, int32_t* argmax_out, float* max_out, float* second_out, float* lse_out,
+               float* logits_out) {
+  int V = m->d.n_vocab;
+  orc_cache* cache = orc_cache_create(m);
+  float* logits = (float*)malloc(sizeof(float) * (size_t)(n_prompt > 1 ? n_prompt : 1) * V);
+  int rc = 0;
+  for (int r = 0; r <= n_steps; r++) {
+    const int32_t* tk = r == 0 ? prompt : &forced[r - 1];
+    int n = r == 0 ? n_prompt : 1;
+    if ((rc = orc_forward(m, tk, n, xa, cache, logits))) break;
+    const float* row = logits + (size_t)(n - 1) * V;
+    int am = orc_argmax(row, V);
+    float mx = row[am], sec = -INFINITY;
+    double s = 0;
+    for (int i = 0; i < V; i++) {
+      if (i != am && row[i] > sec) sec = row[i];
+      s += exp((double)(row[i] - mx));
+    }
+    if (argmax_out) argmax_out[r] = am;
+    if (max_out) max_out[r] = mx;
+    if (second_out) second_out[r] = sec;
+    if (lse_out) lse_out[r] = (float)((double)mx + log(s));
+    if (logits_out) memcpy(logits_out + (size_t)r * V, row, sizeof(float) * (size_t)V);
+  }
+  free(logits);
+  orc_cache_destroy(cache);
+  return rc;
+}

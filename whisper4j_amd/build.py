@@ -1,0 +1,59 @@
+"""Build libw4h.so (HIP for gfx950 + host runtime) in-tree.
+
+Usage: python -m whisper4j_amd.build   (or whisper4j_amd.build.build()).
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+BUILD = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "libw4h.so")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+# Packed FP32 (v_pk_*_f32) is disabled for all device code.
+DEVICE_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+CLANG = os.environ.get("W4H_HOST_CXX", "/opt/rocm/lib/llvm/bin/clang++")
+# Host-only translation units: plain C++ against the HIP runtime API (no device code).
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include"]
+SOURCES = [("w4h_device.hip", HIPCC, DEVICE_FLAGS), ("w4h_api.cpp", CLANG, HOST_FLAGS),
+           ("w4h_ggml.cpp", CLANG, HOST_FLAGS), ("w4h_decode.cpp", CLANG, HOST_FLAGS)]
+
+
+def _compile(src, cxx, flags):
+    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+    cmd = [cxx, *flags, "-c", os.path.join(CSRC, src), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(ln for ln in (r.stdout + r.stderr).splitlines() if noise not in ln)
+    if r.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{err}")
+    return obj, err
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+        results = list(ex.map(lambda s: _compile(*s), SOURCES))
+    if verbose:
+        for _, msg in results:
+            if msg.strip():
+                print(msg, file=sys.stderr)
+    objs = [o for o, _ in results]
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", *objs, "-o", tmp, "-lz"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}{r.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,842 @@
+// Host runtime of whisper4j_amd: models, sessions, the decoder step and the kernel-level entry
+// points of the C ABI (include/w4h.h).  Device work is launched through w4h_internal.h.
+
+#include <hip/hip_runtime_api.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "w4h_host.h"
+#include "w4h_internal.h"
+
+using w4h::LayerDev;
+using w4h::StepParams;
+using w4h::u64;
+
+namespace w4h {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIPCHK(expr)                                                                                   \
+  do {                                                                                                 \
+    hipError_t e_ = (expr);                                                                            \
+    if (e_ != hipSuccess) return fail(W4H_ERR_DEVICE, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+// ---------------------------------------------------------------------------------------------
+// f16 helpers (IEEE binary16, round to nearest even)
+
+float half_to_float(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16, exp = (h >> 10) & 0x1fu, man = h & 0x3ffu, bits;
+  if (exp == 0) {
+    if (man == 0) {
+      bits = sign;
+    } else {
+      int e = -1;
+      do {
+        man <<= 1;
+        e++;
+      } while ((man & 0x400u) == 0);
+      bits = sign | ((uint32_t)(127 - 15 - e) << 23) | ((man & 0x3ffu) << 13);
+    }
+  } else if (exp == 31) {
+    bits = sign | 0x7f800000u | (man << 13);
+  } else {
+    bits = sign | ((exp + 112) << 23) | (man << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+uint16_t float_to_half(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u));
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+  if (ax < 0x38800000u) {
+    if (ax < 0x33000000u) return (uint16_t)sign;
+    uint32_t e = ax >> 23, m = (ax & 0x7fffffu) | 0x800000u, sh = 126 - e;
+    uint32_t q = m >> sh, rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+  }
+  uint32_t q = (((ax >> 23) - 112) << 10) | ((ax & 0x7fffffu) >> 13), rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
+  return (uint16_t)(sign | q);
+}
+
+// GELU table indexed by f16 bits: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) evaluated in
+// float with the tanh taken in double and rounded, as main/tensor/Tensor.java:493-501 builds it.
+#pragma clang fp contract(off)
+void build_gelu_table(float* t) {
+  const float s = (float)std::sqrt(2.0 / 3.14159265358979323846);
+  for (int i = 0; i < 65536; i++) {
+    const float x = half_to_float((uint16_t)i);
+    const float inner = s * (x + 0.044715f * x * x * x);
+    t[i] = 0.5f * x * (1.0f + (float)std::tanh((double)inner));
+  }
+}
+#pragma clang fp contract(on)
+
+// ---------------------------------------------------------------------------------------------
+// device memory
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t n = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+  int alloc(size_t bytes) {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+    if (bytes == 0) return W4H_OK;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+      p = nullptr;
+      return fail(W4H_ERR_OOM, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    }
+    n = bytes;
+    return W4H_OK;
+  }
+  template <class T>
+  T* as() const {
+    return static_cast<T*>(p);
+  }
+};
+
+int upload(DevBuf& b, const void* src, size_t bytes) {
+  int rc = b.alloc(bytes);
+  if (rc) return rc;
+  if (bytes) HIPCHK(hipMemcpy(b.p, src, bytes, hipMemcpyHostToDevice));
+  return W4H_OK;
+}
+
+}  // namespace w4h
+
+using namespace w4h;
+
+struct w4h_model {
+  int device = 0;
+  w4h_dims dims{};
+  int wq8 = 0;
+  std::vector<std::unique_ptr<DevBuf>> bufs;
+  std::vector<LayerDev> layers;
+  DevBuf layers_dev;
+  const void* emb = nullptr;
+  const uint16_t* emb_s = nullptr;
+  const float *pos = nullptr, *lnf_g = nullptr, *lnf_b = nullptr, *gelu = nullptr;
+  std::atomic<int> refs{1};
+  std::atomic<bool> closed{false};
+};
+
+namespace {
+
+struct TensorTable {
+  std::map<std::string, const w4h_tensor*> by_name;
+  const w4h_tensor* get(const std::string& n) const {
+    auto it = by_name.find(n);
+    return it == by_name.end() ? nullptr : it->second;
+  }
+};
+
+int64_t numel(const w4h_tensor* t) {
+  int64_t n = 1;
+  for (int i = 0; i < t->n_dims; i++) n *= t->ne[i];
+  return n;
+}
+
+DevBuf* new_buf(w4h_model* m) {
+  m->bufs.push_back(std::make_unique<DevBuf>());
+  return m->bufs.back().get();
+}
+
+// 1-D f32 tensor (f16 accepted and widened).
+int load_vec(w4h_model* m, const TensorTable& tt, const std::string& name, int n, const float** out,
+             bool optional = false) {
+  const w4h_tensor* t = tt.get(name);
+  if (!t) {
+    if (optional) {
+      *out = nullptr;
+      return W4H_OK;
+    }
+    return fail(W4H_ERR_NOT_FOUND, "missing tensor: %s", name.c_str());
+  }
+  if (numel(t) != n) return fail(W4H_ERR_SHAPE, "tensor %s has %lld elements, expected %d", name.c_str(), (long long)numel(t), n);
+  std::vector<float> v(n);
+  if (t->type == W4H_TYPE_F32) {
+    memcpy(v.data(), t->data, sizeof(float) * n);
+  } else if (t->type == W4H_TYPE_F16) {
+    const uint16_t* h = static_cast<const uint16_t*>(t->data);
+    for (int i = 0; i < n; i++) v[i] = half_to_float(h[i]);
+  } else {
+    return fail(W4H_ERR_FORMAT, "tensor %s: type %d not supported for a vector", name.c_str(), t->type);
+  }
+  DevBuf* b = new_buf(m);
+  int rc = upload(*b, v.data(), sizeof(float) * n);
+  if (rc) return rc;
+  *out = b->as<float>();
+  return W4H_OK;
+}
+
+// Stack 2-D matrices [rows_i][K] (GGML ne = [K, rows_i]) into one device matrix.
+// f16 mode: halves [N][K] (f32 sources rounded to f16).  q8 mode: int8 [N][K] + f16 scales [N][K/32].
+int load_mat(w4h_model* m, const TensorTable& tt, const std::vector<std::string>& names, const std::vector<int>& rows,
+             int K, const void** w, const uint16_t** s) {
+  int N = 0;
+  for (int r : rows) N += r;
+  std::vector<const w4h_tensor*> ts;
+  for (size_t i = 0; i < names.size(); i++) {
+    const w4h_tensor* t = tt.get(names[i]);
+    if (!t) return fail(W4H_ERR_NOT_FOUND, "missing tensor: %s", names[i].c_str());
+    if (t->n_dims != 2 || t->ne[0] != K || t->ne[1] != rows[i])
+      return fail(W4H_ERR_SHAPE, "tensor %s: expected ne=[%d,%d], got n_dims=%d ne=[%lld,%lld]", names[i].c_str(), K, rows[i],
+                  t->n_dims, (long long)t->ne[0], (long long)(t->n_dims > 1 ? t->ne[1] : 1));
+    const bool q8 = t->type == W4H_TYPE_Q8_0;
+    if (q8 != (m->wq8 != 0))
+      return fail(W4H_ERR_FORMAT, "tensor %s: matrix type %d does not match the model's %s matrices", names[i].c_str(),
+                  t->type, m->wq8 ? "q8_0" : "f16/f32");
+    if (!q8 && t->type != W4H_TYPE_F16 && t->type != W4H_TYPE_F32)
+      return fail(W4H_ERR_FORMAT, "tensor %s: unsupported type %d", names[i].c_str(), t->type);
+    ts.push_back(t);
+  }
+  if (!m->wq8) {
+    std::vector<uint16_t> h((size_t)N * K);
+    size_t o = 0;
+    for (size_t i = 0; i < ts.size(); i++) {
+      const size_t n = (size_t)rows[i] * K;
+      if (ts[i]->type == W4H_TYPE_F16) {
+        memcpy(h.data() + o, ts[i]->data, n * 2);
+      } else {
+        const float* f = static_cast<const float*>(ts[i]->data);
+        for (size_t j = 0; j < n; j++) h[o + j] = float_to_half(f[j]);
+      }
+      o += n;
+    }
+    DevBuf* b = new_buf(m);
+    int rc = upload(*b, h.data(), h.size() * 2);
+    if (rc) return rc;
+    *w = b->p;
+    *s = nullptr;
+  } else {
+    if (K % 32) return fail(W4H_ERR_SHAPE, "q8_0 matrix needs K %% 32 == 0 (K=%d)", K);
+    std::vector<int8_t> q((size_t)N * K);
+    std::vector<uint16_t> sc((size_t)N * (K / 32));
+    size_t row = 0;
+    for (size_t i = 0; i < ts.size(); i++) {
+      const unsigned char* src = static_cast<const unsigned char*>(ts[i]->data);
+      for (int r = 0; r < rows[i]; r++, row++)
+        for (int b = 0; b < K / 32; b++) {
+          const unsigned char* blk = src + ((size_t)r * (K / 32) + b) * 34;
+          sc[row * (K / 32) + b] = (uint16_t)(blk[0] | (blk[1] << 8));
+          memcpy(q.data() + row * K + (size_t)b * 32, blk + 2, 32);
+        }
+    }
+    DevBuf* bw = new_buf(m);
+    int rc = upload(*bw, q.data(), q.size());
+    if (rc) return rc;
+    DevBuf* bs = new_buf(m);
+    rc = upload(*bs, sc.data(), sc.size() * 2);
+    if (rc) return rc;
+    *w = bw->p;
+    *s = bs->as<uint16_t>();
+  }
+  return W4H_OK;
+}
+
+int build_model(w4h_model* m, const w4h_dims* dims, const w4h_tensor* tensors, int n_tensors) {
+  TensorTable tt;
+  for (int i = 0; i < n_tensors; i++) {
+    if (!tensors[i].name) return fail(W4H_ERR_INVALID, "tensor %d has no name", i);
+    tt.by_name[tensors[i].name] = &tensors[i];
+  }
+  const int d = dims->n_text_state, V = dims->n_vocab, C = dims->n_text_ctx, L = dims->n_text_layer;
+  const w4h_tensor* te = tt.get("decoder.token_embedding.weight");
+  if (!te) return fail(W4H_ERR_NOT_FOUND, "missing tensor: decoder.token_embedding.weight");
+  m->wq8 = te->type == W4H_TYPE_Q8_0;
+  int rc;
+  if ((rc = load_mat(m, tt, {"decoder.token_embedding.weight"}, {V}, d, &m->emb, &m->emb_s))) return rc;
+  if ((rc = load_vec(m, tt, "decoder.positional_embedding", C * d, &m->pos))) return rc;
+  if ((rc = load_vec(m, tt, "decoder.ln.weight", d, &m->lnf_g))) return rc;
+  if ((rc = load_vec(m, tt, "decoder.ln.bias", d, &m->lnf_b))) return rc;
+  m->layers.resize(L);
+  for (int i = 0; i < L; i++) {
+    LayerDev& ld = m->layers[i];
+    const std::string b = "decoder.blocks." + std::to_string(i) + ".";
+    const void** ws[8] = {&ld.w_qkv, &ld.w_o, &ld.w_cq, &ld.w_co, &ld.w_1, &ld.w_2, &ld.w_ck, &ld.w_cv};
+    const uint16_t** ss[8] = {&ld.s_qkv, &ld.s_o, &ld.s_cq, &ld.s_co, &ld.s_1, &ld.s_2, &ld.s_ck, &ld.s_cv};
+    if ((rc = load_mat(m, tt, {b + "attn.query.weight", b + "attn.key.weight", b + "attn.value.weight"}, {d, d, d}, d, ws[0], ss[0])))
+      return rc;
+    if ((rc = load_mat(m, tt, {b + "attn.out.weight"}, {d}, d, ws[1], ss[1]))) return rc;
+    if ((rc = load_mat(m, tt, {b + "cross_attn.query.weight"}, {d}, d, ws[2], ss[2]))) return rc;
+    if ((rc = load_mat(m, tt, {b + "cross_attn.out.weight"}, {d}, d, ws[3], ss[3]))) return rc;
+    if ((rc = load_mat(m, tt, {b + "mlp.0.weight"}, {4 * d}, d, ws[4], ss[4]))) return rc;
+    if ((rc = load_mat(m, tt, {b + "mlp.2.weight"}, {d}, 4 * d, ws[5], ss[5]))) return rc;
+    if ((rc = load_mat(m, tt, {b + "cross_attn.key.weight"}, {d}, d, ws[6], ss[6]))) return rc;
+    if ((rc = load_mat(m, tt, {b + "cross_attn.value.weight"}, {d}, d, ws[7], ss[7]))) return rc;
+    // QKV bias: query and value biases, key bias if the checkpoint has one (else zeros)
+    {
+      std::vector<float> bq(3 * d, 0.0f);
+      const char* parts[3] = {"attn.query.bias", "attn.key.bias", "attn.value.bias"};
+      for (int p = 0; p < 3; p++) {
+        const w4h_tensor* t = tt.get(b + parts[p]);
+        if (!t) {
+          if (p == 1) continue;
+          return fail(W4H_ERR_NOT_FOUND, "missing tensor: %s%s", b.c_str(), parts[p]);
+        }
+        if (numel(t) != d || (t->type != W4H_TYPE_F32 && t->type != W4H_TYPE_F16))
+          return fail(W4H_ERR_SHAPE, "tensor %s%s: bad shape or type", b.c_str(), parts[p]);
+        for (int j = 0; j < d; j++)
+          bq[p * d + j] = t->type == W4H_TYPE_F32 ? static_cast<const float*>(t->data)[j]
+                                                  : half_to_float(static_cast<const uint16_t*>(t->data)[j]);
+      }
+      DevBuf* bb = new_buf(m);
+      if ((rc = upload(*bb, bq.data(), bq.size() * 4))) return rc;
+      ld.b_qkv = bb->as<float>();
+    }
+    if ((rc = load_vec(m, tt, b + "attn.out.bias", d, &ld.b_o))) return rc;
+    if ((rc = load_vec(m, tt, b + "cross_attn.query.bias", d, &ld.b_cq))) return rc;
+    if ((rc = load_vec(m, tt, b + "cross_attn.out.bias", d, &ld.b_co))) return rc;
+    if ((rc = load_vec(m, tt, b + "cross_attn.value.bias", d, &ld.b_cv))) return rc;
+    if ((rc = load_vec(m, tt, b + "mlp.0.bias", 4 * d, &ld.b_1))) return rc;
+    if ((rc = load_vec(m, tt, b + "mlp.2.bias", d, &ld.b_2))) return rc;
+    if ((rc = load_vec(m, tt, b + "attn_ln.weight", d, &ld.ln1_g))) return rc;
+    if ((rc = load_vec(m, tt, b + "attn_ln.bias", d, &ld.ln1_b))) return rc;
+    if ((rc = load_vec(m, tt, b + "cross_attn_ln.weight", d, &ld.ln2_g))) return rc;
+    if ((rc = load_vec(m, tt, b + "cross_attn_ln.bias", d, &ld.ln2_b))) return rc;
+    if ((rc = load_vec(m, tt, b + "mlp_ln.weight", d, &ld.ln3_g))) return rc;
+    if ((rc = load_vec(m, tt, b + "mlp_ln.bias", d, &ld.ln3_b))) return rc;
+  }
+  if ((rc = upload(m->layers_dev, m->layers.data(), sizeof(LayerDev) * L))) return rc;
+  std::vector<float> table(65536);
+  build_gelu_table(table.data());
+  DevBuf* gb = new_buf(m);
+  if ((rc = upload(*gb, table.data(), table.size() * 4))) return rc;
+  m->gelu = gb->as<float>();
+  return W4H_OK;
+}
+
+int set_device(int device) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(W4H_ERR_DEVICE, "no HIP device available");
+  if (device < 0 || device >= n) return fail(W4H_ERR_INVALID, "device %d out of range (%d devices)", device, n);
+  HIPCHK(hipSetDevice(device));
+  return W4H_OK;
+}
+
+}  // namespace
+
+void model_release(w4h_model* m) {
+  if (m && m->refs.fetch_sub(1) == 1) {
+    (void)hipSetDevice(m->device);
+    delete m;
+  }
+}
+
+extern "C" {
+
+const char* w4h_last_error(void) { return g_err.c_str(); }
+
+int w4h_device_count(int32_t* n) {
+  if (!n) return fail(W4H_ERR_INVALID, "null argument");
+  int c = 0;
+  if (hipGetDeviceCount(&c) != hipSuccess) c = 0;
+  *n = c;
+  return W4H_OK;
+}
+
+int w4h_model_create(const w4h_dims* dims, const w4h_tensor* tensors, int32_t n_tensors, int32_t device,
+                     w4h_model** out) {
+  if (!dims || !tensors || !out || n_tensors <= 0) return fail(W4H_ERR_INVALID, "null argument");
+  *out = nullptr;
+  const int d = dims->n_text_state;
+  if (d <= 0 || d % 64 || dims->n_text_head * 64 != d)
+    return fail(W4H_ERR_INVALID, "n_text_state (%d) must be 64 * n_text_head (%d)", d, dims->n_text_head);
+  if (dims->n_vocab <= 0 || dims->n_text_ctx <= 0 || dims->n_text_layer <= 0 || dims->n_audio_ctx <= 0)
+    return fail(W4H_ERR_INVALID, "dimensions must be positive");
+  if (d > 1280 * 2) return fail(W4H_ERR_INVALID, "n_text_state %d above the supported 2560", d);
+  int rc = set_device(device);
+  if (rc) return rc;
+  auto* m = new w4h_model();
+  m->device = device;
+  m->dims = *dims;
+  rc = build_model(m, dims, tensors, n_tensors);
+  if (rc) {
+    delete m;
+    return rc;
+  }
+  *out = m;
+  return W4H_OK;
+}
+
+int w4h_model_dims(const w4h_model* m, w4h_dims* out) {
+  if (!m || !out) return fail(W4H_ERR_INVALID, "null argument");
+  *out = m->dims;
+  return W4H_OK;
+}
+
+int w4h_model_destroy(w4h_model* m) {
+  if (!m) return fail(W4H_ERR_INVALID, "null argument");
+  if (m->closed.exchange(true)) return fail(W4H_ERR_CLOSED, "model already destroyed");
+  model_release(m);
+  return W4H_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------------------
+// sessions
+
+struct w4h_session {
+  w4h_model* m = nullptr;
+  int S = 1, X = 1, max_ctx = 0, grid = 0, ncs_max = 0, ncc = 0, chc = 0, rpw = 0, mw = 0;
+  size_t lds = 0;
+  hipStream_t stream = nullptr;
+  DevBuf kvk, kvv, xk, xv, slots, ll, err, out, toks, forced, mask, mask2, logits, xa_tmp;
+  u64 *qkv = nullptr, *sp = nullptr, *x1 = nullptr, *cq = nullptr, *cp = nullptr, *x2 = nullptr, *hm = nullptr,
+      *x3 = nullptr, *lp = nullptr, *lpa = nullptr;
+  int kv_len = 0;
+  uint32_t next_tag = 1;
+  int probe = -1;
+  bool has_mask = false;
+  std::vector<int32_t> slots_host;
+  bool slots_identity = true, slots_dirty = false;
+  bool closed = false;
+};
+
+namespace w4h {
+
+static StepParams base_params(w4h_session* s) {
+  w4h_model* m = s->m;
+  StepParams p{};
+  p.layers = m->layers_dev.as<LayerDev>();
+  p.L = m->dims.n_text_layer;
+  p.d = m->dims.n_text_state;
+  p.H = m->dims.n_text_head;
+  p.V = m->dims.n_vocab;
+  p.C = m->dims.n_text_ctx;
+  p.A = m->dims.n_audio_ctx;
+  p.wq8 = m->wq8;
+  p.emb = m->emb;
+  p.emb_s = m->emb_s;
+  p.pos = m->pos;
+  p.lnf_g = m->lnf_g;
+  p.lnf_b = m->lnf_b;
+  p.gelu = m->gelu;
+  p.S = s->S;
+  p.X = s->X;
+  p.max_ctx = s->max_ctx;
+  p.kv_k = s->kvk.as<uint16_t>();
+  p.kv_v = s->kvv.as<uint16_t>();
+  p.xk = s->xk.as<uint16_t>();
+  p.xv = s->xv.as<uint16_t>();
+  p.slots = s->slots_identity ? nullptr : s->slots.as<int32_t>();
+  p.qkv = s->qkv;
+  p.sp = s->sp;
+  p.x1 = s->x1;
+  p.cq = s->cq;
+  p.cp = s->cp;
+  p.x2 = s->x2;
+  p.hm = s->hm;
+  p.x3 = s->x3;
+  p.lp = s->lp;
+  p.lpa = s->lpa;
+  p.ncs_max = s->ncs_max;
+  p.ncc = s->ncc;
+  p.chc = s->chc;
+  p.mask = s->has_mask ? s->mask.as<uint32_t>() : nullptr;
+  p.mw = s->mw;
+  p.probe = s->probe;
+  p.err = s->err.as<unsigned>();
+  p.rows_per_wg = s->rpw;
+  return p;
+}
+
+static int ensure(DevBuf& b, size_t bytes) {
+  if (b.n >= bytes) return W4H_OK;
+  return b.alloc(bytes);
+}
+
+// Launch n_steps steps; tokens/forced are host arrays.  Results (if out) are copied back.
+int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int n_steps, const uint32_t* extra_mask,
+              int topk, w4h_step_out* out, float* logits, float* ms) {
+  if (s->closed) return fail(W4H_ERR_CLOSED, "session destroyed");
+  if (!tokens || n_steps <= 0) return fail(W4H_ERR_INVALID, "tokens and n_steps > 0 required");
+  if (topk < 0 || topk > W4H_TOPK_MAX) return fail(W4H_ERR_INVALID, "topk %d outside [0, %d]", topk, W4H_TOPK_MAX);
+  if (s->kv_len + n_steps > s->max_ctx)
+    return fail(W4H_ERR_CAPACITY, "self-KV capacity %d exceeded (kv_len %d + %d steps)", s->max_ctx, s->kv_len, n_steps);
+  const int V = s->m->dims.n_vocab;
+  for (int i = 0; i < s->S; i++)
+    if (tokens[i] < 0 || tokens[i] >= V) return fail(W4H_ERR_INVALID, "token %d out of range [0, %d)", tokens[i], V);
+  if (forced)
+    for (size_t i = 0; i < (size_t)(n_steps - 1) * s->S; i++)
+      if (forced[i] < 0 || forced[i] >= V) return fail(W4H_ERR_INVALID, "forced token %d out of range", forced[i]);
+  if ((uint64_t)s->next_tag + (uint64_t)n_steps >= 0xfffffff0ull) return fail(W4H_ERR_INVALID, "tag space exhausted; recreate the session");
+  HIPCHK(hipSetDevice(s->m->device));
+  int rc;
+  if ((rc = ensure(s->toks, sizeof(int32_t) * s->S))) return rc;
+  HIPCHK(hipMemcpyAsync(s->toks.p, tokens, sizeof(int32_t) * s->S, hipMemcpyHostToDevice, s->stream));
+  if (forced && n_steps > 1) {
+    if ((rc = ensure(s->forced, sizeof(int32_t) * (size_t)(n_steps - 1) * s->S))) return rc;
+    HIPCHK(hipMemcpyAsync(s->forced.p, forced, sizeof(int32_t) * (size_t)(n_steps - 1) * s->S, hipMemcpyHostToDevice, s->stream));
+  }
+  if (extra_mask) {
+    if ((rc = ensure(s->mask2, sizeof(uint32_t) * (size_t)s->S * s->mw))) return rc;
+    HIPCHK(hipMemcpyAsync(s->mask2.p, extra_mask, sizeof(uint32_t) * (size_t)s->S * s->mw, hipMemcpyHostToDevice, s->stream));
+  }
+  if (s->slots_dirty) {
+    HIPCHK(hipMemcpyAsync(s->slots.p, s->slots_host.data(), sizeof(int32_t) * s->slots_host.size(), hipMemcpyHostToDevice,
+                          s->stream));
+    s->slots_dirty = false;
+  }
+  if (out && (rc = ensure(s->out, sizeof(w4h_step_out) * (size_t)n_steps * s->S))) return rc;
+  if (logits && (rc = ensure(s->logits, sizeof(float) * (size_t)n_steps * s->S * V))) return rc;
+  HIPCHK(hipMemsetAsync(s->err.p, 0, sizeof(unsigned), s->stream));
+  StepParams p = base_params(s);
+  p.nsteps = n_steps;
+  p.kv_len0 = s->kv_len;
+  p.tag0 = s->next_tag;
+  p.tokens0 = s->toks.as<int32_t>();
+  p.forced = (forced && n_steps > 1) ? s->forced.as<int32_t>() : nullptr;
+  p.mask2 = extra_mask ? s->mask2.as<uint32_t>() : nullptr;
+  p.topk = topk;
+  p.out = out ? s->out.as<w4h_step_out>() : nullptr;
+  p.logits_out = logits ? s->logits.as<float>() : nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (ms) {
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    HIPCHK(hipEventRecord(e0, s->stream));
+  }
+  hipError_t le = launch_step(p, s->grid, s->lds, s->stream);
+  if (le != hipSuccess) return fail(W4H_ERR_DEVICE, "decoder step launch failed: %s", hipGetErrorString(le));
+  s->next_tag += (uint32_t)n_steps;
+  if (ms) HIPCHK(hipEventRecord(e1, s->stream));
+  unsigned herr = 0;
+  HIPCHK(hipMemcpyAsync(&herr, s->err.p, sizeof(unsigned), hipMemcpyDeviceToHost, s->stream));
+  if (out) HIPCHK(hipMemcpyAsync(out, s->out.p, sizeof(w4h_step_out) * (size_t)n_steps * s->S, hipMemcpyDeviceToHost, s->stream));
+  if (logits)
+    HIPCHK(hipMemcpyAsync(logits, s->logits.p, sizeof(float) * (size_t)n_steps * s->S * V, hipMemcpyDeviceToHost, s->stream));
+  HIPCHK(hipStreamSynchronize(s->stream));
+  if (ms) {
+    HIPCHK(hipEventElapsedTime(ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+  }
+  if (herr) return fail(W4H_ERR_TIMEOUT, "a device-side wait expired during the step (code %u); step aborted", herr);
+  s->kv_len += n_steps;
+  return W4H_OK;
+}
+
+}  // namespace w4h
+
+extern "C" {
+
+int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session** out) {
+  if (!m || !desc || !out) return fail(W4H_ERR_INVALID, "null argument");
+  *out = nullptr;
+  if (m->closed) return fail(W4H_ERR_CLOSED, "model destroyed");
+  const w4h_dims& D = m->dims;
+  if (desc->n_rows < 1 || desc->n_rows > kMaxRows)
+    return fail(W4H_ERR_INVALID, "n_rows %d outside [1, %d]", desc->n_rows, kMaxRows);
+  if (desc->n_encoders != 1 && desc->n_encoders != desc->n_rows)
+    return fail(W4H_ERR_INVALID, "n_encoders must be 1 or n_rows");
+  if (desc->max_ctx < 1 || desc->max_ctx > 8192) return fail(W4H_ERR_INVALID, "max_ctx %d outside [1, 8192]", desc->max_ctx);
+  int rc = set_device(m->device);
+  if (rc) return rc;
+  auto s = std::make_unique<w4h_session>();
+  s->m = m;
+  s->S = desc->n_rows;
+  s->X = desc->n_encoders;
+  s->max_ctx = desc->max_ctx;
+  const int L = D.n_text_layer, d = D.n_text_state, H = D.n_text_head, A = D.n_audio_ctx, V = D.n_vocab;
+  s->ncs_max = (s->max_ctx + kSelfChunk - 1) / kSelfChunk;
+  s->ncc = (A + kMaxChunk - 1) / kMaxChunk;
+  s->chc = (A + s->ncc - 1) / s->ncc;
+  s->mw = (V + 31) / 32;
+  hipDeviceProp_t prop;
+  HIPCHK(hipGetDeviceProperties(&prop, m->device));
+  s->grid = prop.multiProcessorCount;
+  s->rpw = (((V + 7) / 8 + s->grid - 1) / s->grid) * 8;
+  StepParams probe_p{};
+  probe_p.S = s->S;
+  probe_p.d = d;
+  probe_p.H = H;
+  probe_p.ncs_max = s->ncs_max;
+  probe_p.ncc = s->ncc;
+  probe_p.rows_per_wg = s->rpw;
+  s->lds = step_lds_bytes(probe_p, s->grid);
+  if (s->lds > (size_t)prop.sharedMemPerBlock)
+    return fail(W4H_ERR_INVALID, "n_rows %d x n_text_state %d needs %zu bytes of LDS per workgroup (max %zu)", s->S, d, s->lds,
+                (size_t)prop.sharedMemPerBlock);
+  const size_t kv_elems = (size_t)L * s->S * H * s->max_ctx * kHeadDim;
+  if ((rc = s->kvk.alloc(kv_elems * 2)) || (rc = s->kvv.alloc(kv_elems * 2))) return rc;
+  const size_t x_elems = (size_t)s->X * L * H * A * kHeadDim;
+  if ((rc = s->xk.alloc(x_elems * 2)) || (rc = s->xv.alloc(x_elems * 2))) return rc;
+  HIPCHK(hipMemset(s->xk.p, 0, x_elems * 2));
+  HIPCHK(hipMemset(s->xv.p, 0, x_elems * 2));
+  s->slots_host.resize((size_t)s->S * s->max_ctx);
+  for (int r = 0; r < s->S; r++)
+    for (int q = 0; q < s->max_ctx; q++) s->slots_host[(size_t)r * s->max_ctx + q] = r;
+  if ((rc = upload(s->slots, s->slots_host.data(), s->slots_host.size() * 4))) return rc;
+  // tagged exchange buffers, one allocation
+  const size_t n_qkv = (size_t)L * s->S * 3 * d, n_sp = (size_t)L * s->ncs_max * s->S * H * kPartWords,
+               n_vec = (size_t)L * s->S * d, n_cp = (size_t)L * s->ncc * s->S * H * kPartWords, n_hm = (size_t)L * s->S * 4 * d,
+               n_lp = (size_t)s->grid * s->S * kSelWords, n_lpa = (size_t)s->grid * s->S * 2;
+  const size_t total = n_qkv + n_sp + 4 * n_vec + n_cp + n_hm + n_lp + n_lpa;
+  if ((rc = s->ll.alloc(total * sizeof(u64)))) return rc;
+  u64* b = s->ll.as<u64>();
+  s->qkv = b; b += n_qkv;
+  s->sp = b; b += n_sp;
+  s->x1 = b; b += n_vec;
+  s->cq = b; b += n_vec;
+  s->cp = b; b += n_cp;
+  s->x2 = b; b += n_vec;
+  s->hm = b; b += n_hm;
+  s->x3 = b; b += n_vec;
+  s->lp = b; b += n_lp;
+  s->lpa = b;
+  HIPCHK(hipStreamCreate(&s->stream));
+  HIPCHK(launch_fill_u64(s->ll.as<u64>(), total, s->stream));
+  if ((rc = s->err.alloc(256))) return rc;
+  if ((rc = s->mask.alloc(sizeof(uint32_t) * (size_t)s->S * s->mw))) return rc;
+  HIPCHK(hipStreamSynchronize(s->stream));
+  m->refs.fetch_add(1);
+  *out = s.release();
+  return W4H_OK;
+}
+
+int w4h_session_destroy(w4h_session* s) {
+  if (!s) return fail(W4H_ERR_INVALID, "null argument");
+  w4h_model* m = s->m;
+  (void)hipSetDevice(m->device);
+  if (s->stream) {
+    (void)hipStreamSynchronize(s->stream);
+    (void)hipStreamDestroy(s->stream);
+  }
+  delete s;
+  model_release(m);
+  return W4H_OK;
+}
+
+int w4h_session_set_encoder(w4h_session* s, int32_t enc, const float* xa) {
+  if (!s || !xa) return fail(W4H_ERR_INVALID, "null argument");
+  if (enc < 0 || enc >= s->X) return fail(W4H_ERR_INVALID, "encoder %d outside [0, %d)", enc, s->X);
+  const w4h_dims& D = s->m->dims;
+  HIPCHK(hipSetDevice(s->m->device));
+  const size_t n = (size_t)D.n_audio_ctx * D.n_text_state;
+  int rc = ensure(s->xa_tmp, n * sizeof(float));
+  if (rc) return rc;
+  HIPCHK(hipMemcpyAsync(s->xa_tmp.p, xa, n * sizeof(float), hipMemcpyHostToDevice, s->stream));
+  const size_t off = (size_t)enc * D.n_text_layer * D.n_text_head * D.n_audio_ctx * kHeadDim;
+  HIPCHK(launch_cross_kv(s->m->layers_dev.as<LayerDev>(), D.n_text_layer, D.n_text_state, D.n_text_head, D.n_audio_ctx,
+                         s->m->wq8, s->xa_tmp.as<float>(), s->xk.as<uint16_t>() + off, s->xv.as<uint16_t>() + off, s->stream));
+  HIPCHK(hipStreamSynchronize(s->stream));
+  return W4H_OK;
+}
+
+int w4h_session_reset(w4h_session* s, int32_t kv_len) {
+  if (!s) return fail(W4H_ERR_INVALID, "null argument");
+  if (kv_len < 0 || kv_len > s->kv_len) return fail(W4H_ERR_INVALID, "kv_len %d outside [0, %d]", kv_len, s->kv_len);
+  s->kv_len = kv_len;
+  if (kv_len == 0 && !s->slots_identity) {
+    for (int r = 0; r < s->S; r++)
+      for (int q = 0; q < s->max_ctx; q++) s->slots_host[(size_t)r * s->max_ctx + q] = r;
+    s->slots_identity = true;
+    s->slots_dirty = true;
+  }
+  return W4H_OK;
+}
+
+int w4h_session_kv_len(const w4h_session* s, int32_t* kv_len) {
+  if (!s || !kv_len) return fail(W4H_ERR_INVALID, "null argument");
+  *kv_len = s->kv_len;
+  return W4H_OK;
+}
+
+int w4h_session_set_suppress(w4h_session* s, const int32_t* ids, int32_t n) {
+  if (!s || (n > 0 && !ids)) return fail(W4H_ERR_INVALID, "null argument");
+  std::vector<uint32_t> bits((size_t)s->S * s->mw, 0u);
+  const int V = s->m->dims.n_vocab;
+  for (int i = 0; i < n; i++)
+    if (ids[i] >= 0 && ids[i] < V)
+      for (int r = 0; r < s->S; r++) bits[(size_t)r * s->mw + (ids[i] >> 5)] |= 1u << (ids[i] & 31);
+  HIPCHK(hipSetDevice(s->m->device));
+  HIPCHK(hipMemcpy(s->mask.p, bits.data(), bits.size() * 4, hipMemcpyHostToDevice));
+  s->has_mask = n > 0;
+  return W4H_OK;
+}
+
+int w4h_session_set_probe(w4h_session* s, int32_t token) {
+  if (!s) return fail(W4H_ERR_INVALID, "null argument");
+  s->probe = (token >= 0 && token < s->m->dims.n_vocab) ? token : -1;
+  return W4H_OK;
+}
+
+int w4h_session_step(w4h_session* s, const int32_t* tokens, const uint32_t* extra_mask, int32_t topk, w4h_step_out* out,
+                     float* logits) {
+  if (!s) return fail(W4H_ERR_INVALID, "null argument");
+  return run_steps(s, tokens, nullptr, 1, extra_mask, topk, out, logits, nullptr);
+}
+
+int w4h_session_run(w4h_session* s, const int32_t* tokens, const int32_t* forced, int32_t n_steps, int32_t topk,
+                    w4h_step_out* out) {
+  if (!s) return fail(W4H_ERR_INVALID, "null argument");
+  return run_steps(s, tokens, forced, n_steps, nullptr, topk, out, nullptr, nullptr);
+}
+
+int w4h_session_reorder(w4h_session* s, const int32_t* parent) {
+  if (!s || !parent) return fail(W4H_ERR_INVALID, "null argument");
+  for (int r = 0; r < s->S; r++)
+    if (parent[r] < 0 || parent[r] >= s->S) return fail(W4H_ERR_INVALID, "parent[%d]=%d outside [0, %d)", r, parent[r], s->S);
+  std::vector<int32_t> old(s->slots_host);
+  for (int r = 0; r < s->S; r++)
+    memcpy(&s->slots_host[(size_t)r * s->max_ctx], &old[(size_t)parent[r] * s->max_ctx], sizeof(int32_t) * s->kv_len);
+  bool ident = true;
+  for (int r = 0; r < s->S && ident; r++)
+    for (int q = 0; q < s->kv_len; q++)
+      if (s->slots_host[(size_t)r * s->max_ctx + q] != r) {
+        ident = false;
+        break;
+      }
+  s->slots_identity = ident;
+  s->slots_dirty = true;
+  return W4H_OK;
+}
+
+int w4h_session_time_run(w4h_session* s, const int32_t* tokens, const int32_t* forced, int32_t n_steps, int32_t n_repeats,
+                         float* ms_out, w4h_step_out* out) {
+  if (!s || !ms_out || n_repeats < 1) return fail(W4H_ERR_INVALID, "bad argument");
+  const int kv0 = s->kv_len;
+  for (int r = 0; r < n_repeats; r++) {
+    s->kv_len = kv0;
+    int rc = run_steps(s, tokens, forced, n_steps, nullptr, 0, r + 1 == n_repeats ? out : nullptr, nullptr, &ms_out[r]);
+    if (rc) return rc;
+  }
+  return W4H_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// kernel-level entry points
+
+static int op_prepare() {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(W4H_ERR_DEVICE, "no HIP device available");
+  return W4H_OK;
+}
+
+int w4h_op_linear(const void* w, int32_t w_type, int32_t n, int32_t k, const float* bias, const float* x, int32_t m,
+                  float* y) {
+  if (!w || !x || !y || n <= 0 || k <= 0 || m <= 0 || m > kMaxRows) return fail(W4H_ERR_INVALID, "bad argument");
+  if (k % 32) return fail(W4H_ERR_SHAPE, "k must be a multiple of 32");
+  if (w_type != W4H_TYPE_F16 && w_type != W4H_TYPE_Q8_0) return fail(W4H_ERR_INVALID, "w_type must be f16 or q8_0");
+  int rc = op_prepare();
+  if (rc) return rc;
+  DevBuf dw, ds, db, dx, dy;
+  if (w_type == W4H_TYPE_F16) {
+    if ((rc = upload(dw, w, (size_t)n * k * 2))) return rc;
+  } else {
+    std::vector<int8_t> q((size_t)n * k);
+    std::vector<uint16_t> sc((size_t)n * (k / 32));
+    const unsigned char* src = static_cast<const unsigned char*>(w);
+    for (int r = 0; r < n; r++)
+      for (int b = 0; b < k / 32; b++) {
+        const unsigned char* blk = src + ((size_t)r * (k / 32) + b) * 34;
+        sc[(size_t)r * (k / 32) + b] = (uint16_t)(blk[0] | (blk[1] << 8));
+        memcpy(q.data() + (size_t)r * k + b * 32, blk + 2, 32);
+      }
+    if ((rc = upload(dw, q.data(), q.size())) || (rc = upload(ds, sc.data(), sc.size() * 2))) return rc;
+  }
+  if (bias && (rc = upload(db, bias, (size_t)n * 4))) return rc;
+  if ((rc = upload(dx, x, (size_t)m * k * 4)) || (rc = dy.alloc((size_t)m * n * 4))) return rc;
+  HIPCHK(launch_op_linear(dw.p, ds.as<uint16_t>(), w_type == W4H_TYPE_Q8_0, n, k, bias ? db.as<float>() : nullptr,
+                          dx.as<float>(), m, dy.as<float>(), nullptr));
+  HIPCHK(hipMemcpy(y, dy.p, (size_t)m * n * 4, hipMemcpyDeviceToHost));
+  return W4H_OK;
+}
+
+int w4h_op_layernorm(const float* x, int32_t rows, int32_t n, const float* gamma, const float* beta, float* y) {
+  if (!x || !gamma || !beta || !y || rows <= 0 || n <= 0) return fail(W4H_ERR_INVALID, "bad argument");
+  int rc = op_prepare();
+  if (rc) return rc;
+  DevBuf dx, dg, dbt, dy;
+  if ((rc = upload(dx, x, (size_t)rows * n * 4)) || (rc = upload(dg, gamma, (size_t)n * 4)) ||
+      (rc = upload(dbt, beta, (size_t)n * 4)) || (rc = dy.alloc((size_t)rows * n * 4)))
+    return rc;
+  HIPCHK(launch_op_layernorm(dx.as<float>(), rows, n, dg.as<float>(), dbt.as<float>(), dy.as<float>(), nullptr));
+  HIPCHK(hipMemcpy(y, dy.p, (size_t)rows * n * 4, hipMemcpyDeviceToHost));
+  return W4H_OK;
+}
+
+int w4h_op_gelu(const float* x, int32_t n, float* y) {
+  if (!x || !y || n <= 0) return fail(W4H_ERR_INVALID, "bad argument");
+  int rc = op_prepare();
+  if (rc) return rc;
+  std::vector<float> table(65536);
+  build_gelu_table(table.data());
+  DevBuf dt, dx, dy;
+  if ((rc = upload(dt, table.data(), table.size() * 4)) || (rc = upload(dx, x, (size_t)n * 4)) || (rc = dy.alloc((size_t)n * 4)))
+    return rc;
+  HIPCHK(launch_op_gelu(dx.as<float>(), n, dt.as<float>(), dy.as<float>(), nullptr));
+  HIPCHK(hipMemcpy(y, dy.p, (size_t)n * 4, hipMemcpyDeviceToHost));
+  return W4H_OK;
+}
+
+int w4h_op_attention(const float* q, const uint16_t* k, const uint16_t* v, int32_t n_heads, int32_t kv_len, float scale,
+                     float* out) {
+  if (!q || !k || !v || !out || n_heads <= 0 || kv_len <= 0 || kv_len > 8192) return fail(W4H_ERR_INVALID, "bad argument");
+  int rc = op_prepare();
+  if (rc) return rc;
+  DevBuf dq, dk, dv, dout;
+  const size_t kvn = (size_t)n_heads * kv_len * kHeadDim;
+  if ((rc = upload(dq, q, (size_t)n_heads * kHeadDim * 4)) || (rc = upload(dk, k, kvn * 2)) || (rc = upload(dv, v, kvn * 2)) ||
+      (rc = dout.alloc((size_t)n_heads * kHeadDim * 4)))
+    return rc;
+  HIPCHK(launch_op_attention(dq.as<float>(), dk.as<uint16_t>(), dv.as<uint16_t>(), n_heads, kv_len, scale, dout.as<float>(), nullptr));
+  HIPCHK(hipMemcpy(out, dout.p, (size_t)n_heads * kHeadDim * 4, hipMemcpyDeviceToHost));
+  return W4H_OK;
+}
+
+int w4h_op_select(const float* logits, int32_t rows, int32_t n, const uint32_t* mask, int32_t k, w4h_step_out* out) {
+  if (!logits || !out || rows <= 0 || n <= 0 || k < 0 || k > W4H_TOPK_MAX) return fail(W4H_ERR_INVALID, "bad argument");
+  int rc = op_prepare();
+  if (rc) return rc;
+  DevBuf dl, dm, dout;
+  const size_t mw = (size_t)(n + 31) / 32;
+  if ((rc = upload(dl, logits, (size_t)rows * n * 4))) return rc;
+  if (mask && (rc = upload(dm, mask, (size_t)rows * mw * 4))) return rc;
+  if ((rc = dout.alloc(sizeof(w4h_step_out) * rows))) return rc;
+  HIPCHK(launch_op_select(dl.as<float>(), rows, n, mask ? dm.as<uint32_t>() : nullptr, k, dout.as<w4h_step_out>(), nullptr));
+  HIPCHK(hipMemcpy(out, dout.p, sizeof(w4h_step_out) * rows, hipMemcpyDeviceToHost));
+  return W4H_OK;
+}
+
+}  // extern "C"
+
+namespace w4h {
+int session_rows(const w4h_session* s) { return s->S; }
+w4h_dims session_dims(const w4h_session* s) { return s->m->dims; }
+}  // namespace w4h

@@ -1,0 +1,81 @@
+// Internal interface between the host runtime (w4h_api.cpp, w4h_decode.cpp) and the device code
+// (w4h_device.hip).  Not part of the public C ABI.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#include "../../include/w4h.h"
+
+namespace w4h {
+
+constexpr int kHeadDim = 64;
+constexpr int kThreads = 256;  // threads per workgroup of every kernel
+constexpr int kMaxRows = 8;    // decoder rows per step handled by the persistent kernel
+constexpr int kSelfChunk = 128;  // self-attention keys per work item
+constexpr int kMaxChunk = 256;   // longest key chunk an attention work item may take
+constexpr int kPartWords = 2 + kHeadDim;            // (m, l, acc[64]) per attention partial
+constexpr int kSelWords = 6 + 2 * W4H_TOPK_MAX;     // per-workgroup selection partial
+
+// Device pointers of one decoder layer.  Matrices are [out][in] row-major; f16 matrices hold
+// halves, q8_0 matrices hold int8 with f16 scales [out][in/32] in the s_* pointer.
+struct LayerDev {
+  const void *w_qkv, *w_o, *w_cq, *w_co, *w_1, *w_2, *w_ck, *w_cv;
+  const uint16_t *s_qkv, *s_o, *s_cq, *s_co, *s_1, *s_2, *s_ck, *s_cv;
+  const float *b_qkv, *b_o, *b_cq, *b_co, *b_1, *b_2, *b_cv;
+  const float *ln1_g, *ln1_b, *ln2_g, *ln2_b, *ln3_g, *ln3_b;
+};
+
+typedef unsigned long long u64;
+
+struct StepParams {
+  // model
+  const LayerDev* layers;
+  int L, d, H, V, C, A;
+  int wq8;
+  const void* emb;
+  const uint16_t* emb_s;
+  const float* pos;
+  const float *lnf_g, *lnf_b;
+  const float* gelu;
+  // session
+  int S, X, max_ctx;
+  uint16_t *kv_k, *kv_v;        // [L][S][H][max_ctx][64]
+  const uint16_t *xk, *xv;      // [X][L][H][A][64]
+  const int32_t* slots;         // [S][max_ctx] or null (row r reads its own slot)
+  u64 *qkv, *sp, *x1, *cq, *cp, *x2, *hm, *x3, *lp, *lpa;  // tagged exchange buffers
+  int ncs_max, ncc, chc;        // self chunk capacity, cross chunk count, cross chunk length
+  // control
+  int nsteps, kv_len0;
+  uint32_t tag0;
+  const int32_t* tokens0;       // [S]
+  const int32_t* forced;        // [nsteps-1][S] or null (greedy feedback)
+  const uint32_t* mask;         // [S][mw] static suppress bitmask or null
+  const uint32_t* mask2;        // [S][mw] per-step extra bitmask or null
+  int mw, probe, topk;
+  w4h_step_out* out;            // [nsteps][S] or null
+  float* logits_out;            // [nsteps][S][V] or null
+  unsigned* err;
+  int rows_per_wg;              // vocab rows one workgroup keeps in LDS in the logits phase
+};
+
+// Launchers (return the HIP error of the launch).
+hipError_t launch_step(const StepParams& p, int grid, size_t lds_bytes, hipStream_t st);
+size_t step_lds_bytes(const StepParams& p, int grid);
+int step_max_grid(size_t lds_bytes);
+hipError_t launch_cross_kv(const LayerDev* layers_host, int L, int d, int H, int A, int wq8, const float* xa,
+                           uint16_t* xk, uint16_t* xv, hipStream_t st);
+hipError_t launch_fill_u64(u64* p, size_t n, hipStream_t st);
+
+// Standalone op launchers (device pointers).
+hipError_t launch_op_linear(const void* w, const uint16_t* ws, int wq8, int n, int k, const float* bias,
+                            const float* x, int m, float* y, hipStream_t st);
+hipError_t launch_op_layernorm(const float* x, int rows, int n, const float* g, const float* b, float* y,
+                               hipStream_t st);
+hipError_t launch_op_gelu(const float* x, int n, const float* table, float* y, hipStream_t st);
+hipError_t launch_op_attention(const float* q, const uint16_t* k, const uint16_t* v, int nh, int kv_len, float scale,
+                               float* out, hipStream_t st);
+hipError_t launch_op_select(const float* logits, int rows, int n, const uint32_t* mask, int k, w4h_step_out* out,
+                            hipStream_t st);
+
+}  // namespace w4h
