@@ -1,0 +1,152 @@
+"""Benchmark: greedy batch-1 decode tokens/s of a Whisper base.en-shaped text decoder on one MI355X.
+
+Workload (the configuration the headline metric is quoted on): d_model 512, 6 layers, 8 heads,
+vocab 51864, f16 weights N(0, 0.02), LayerNorm gamma 1 / beta 0, one fp32 [1500, 512] N(0, 1)
+encoder output, prompt [50257, 50258, 50359, 50363], then 444 teacher-forced single-token steps
+(uniform ids in [0, 50256]) to the full 448-token context.
+
+A bench "step" is one such 444-token decode sweep over device-resident weights, cross-attention
+K/V and a self-KV cache holding the prefilled 4-token prompt; each sweep rewinds the KV to the
+prompt.  Prefill and the cross-K/V projection are outside the timed region.  Every token step is
+a real single-token decoder step (the next token could be the previous argmax; the teacher-forced
+id is read from device memory instead).  The whole sweep is one launch of the persistent step
+kernel, timed with HIP events on the session stream.
+
+Prints ONE JSON line (see the keys below); ``--gpus N`` with N > 1 exits: this build runs on one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode tokens/s (greedy b=1 & beam 5) + % of HBM roofline, 1 MI355X"
+N_STEPS = 444
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_step_base.en_traffic.txt")
+
+
+def algorithmic_bytes_per_step(dims, kv_len, rows=1, encoders=1, w_b=2.0, kv_b=2.0):
+    """Bytes a decoder step must move: layer weights once, tied logits once, cross K/V of every
+    encoder, the self-KV read plus the appended row, biases, LayerNorm parameters, embedding rows."""
+    L, d, V, A = dims.n_text_layer, dims.n_text_state, dims.n_vocab, dims.n_audio_ctx
+    b = L * 14 * d * d * w_b + V * d * w_b
+    b += L * 2 * A * d * kv_b * encoders
+    b += rows * L * 2 * d * kv_b * (kv_len + 1)
+    b += L * 10 * d * 4 + (3 * L + 1) * 2 * d * 4 + rows * (d * w_b + d * 4)
+    return b
+
+
+def read_traffic():
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline(dims, T, xa, prompt, forced, n_steps):
+    """The oracle (single-threaded C restatement of the reference's Linux decode path) on a bounded
+    sample of the same workload: prefill untimed, then n_steps teacher-forced steps."""
+    from oracle import oracle as orc
+
+    m = orc.Model(dims, T)
+    c = m.new_cache()
+    m.forward(prompt, xa, c)
+    t0 = time.perf_counter()
+    for i in range(n_steps):
+        m.forward([int(forced[i])], xa, c)
+    dt = time.perf_counter() - t0
+    m.close()
+    return n_steps / dt, dt
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10, help="timed 444-token decode sweeps")
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--cpu-steps", type=int, default=60, help="oracle steps timed for the CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}); this build has no multi-GPU path.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import whisper4j_amd as w4h
+    from whisper4j_amd import synth
+
+    dims = synth.SHAPES["base.en"]
+    T = synth.make_decoder(dims, seed=0, wtype="f16")
+    xa = synth.encoder_output(dims, 0)
+    prompt = list(synth.BENCH_PREFIX)
+    forced = synth.forced_tokens(N_STEPS, 0)
+
+    model = w4h.Model.from_tensors(dims, T)
+    sess = model.session(n_rows=1, max_ctx=dims.n_text_ctx)
+    sess.set_encoder(xa)
+    sess.run([prompt[0]], forced=prompt[1:], n_steps=len(prompt))  # prefill (untimed)
+    kv0 = sess.kv_len
+    # sweep: forced[i] at position 4 + i for i < 444 (kv_len 4 -> 448)
+    tok0 = [int(forced[0])]
+    fwd = forced[1:N_STEPS]
+    if args.warmup:
+        sess.time_run(tok0, fwd, N_STEPS, args.warmup)
+    t0 = time.perf_counter()
+    ms, outs = sess.time_run(tok0, fwd, N_STEPS, args.steps)
+    wall = time.perf_counter() - t0
+    sess.close()
+    model.close()
+
+    ms_mean = float(np.mean(ms))
+    tok_s = N_STEPS * args.steps / wall
+    bytes_launch = sum(algorithmic_bytes_per_step(dims, kv0 + i) for i in range(N_STEPS))
+    achieved = bytes_launch / (ms_mean * 1e-3) / 1e9
+    traffic = read_traffic()
+
+    cpu = None
+    if not args.no_cpu:
+        cps, dt = cpu_baseline(dims, T, xa, prompt, forced, args.cpu_steps)
+        cpu = {"value": round(cps, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"base.en decoder, {args.cpu_steps} teacher-forced steps at positions 4..{3 + args.cpu_steps} "
+                         f"after an untimed 4-token prefill, one thread ({dt:.1f} s)"}
+
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 weights / fp32 compute / f16 KV",
+        "data": "synthetic (seeded random-init weights, N(0,1) encoder output, uniform teacher-forced ids)",
+        "config": {"workload": "whisper base.en-shaped decoder, greedy batch 1, 4-token prefix + 444 teacher-forced "
+                               "steps to the 448-token context (one step = one 444-token sweep)",
+                   "d_model": 512, "layers": 6, "heads": 8, "vocab": 51864, "tokens_per_step": N_STEPS,
+                   "kernel_ms_per_step": round(ms_mean, 4),
+                   "us_per_token": round(ms_mean * 1e3 / N_STEPS, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "w4h::k_step<1,0> (persistent decoder step, whole sweep per launch)",
+                     "algorithmic_bytes_per_launch": int(bytes_launch)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
