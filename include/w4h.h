@@ -146,6 +146,15 @@ int w4h_session_reorder(w4h_session* s, const int32_t* parent);
 int w4h_session_time_run(w4h_session* s, const int32_t* tokens, const int32_t* forced, int32_t n_steps,
                          int32_t n_repeats, float* ms_out, w4h_step_out* out);
 
+/* Diagnostics: run n_steps teacher-forced steps (kv_len restored afterwards) and record, for every
+ * step, phase, point and workgroup the device wall-clock (100 MHz) tick: points are 0 phase entered,
+ * 1 inputs arrived, 2 work computed, 3 phase left (0 where a workgroup had no work):
+ * trace[((step * (6 * n_text_layer + 2) + phase) * 4 + point) * n_workgroups + workgroup].  Phases per
+ * layer: self-attention (with the q/k/v projection), self out-proj, cross-attention (with the q
+ * projection), cross out-proj, mlp1, mlp2; then logits and selection. */
+int w4h_session_trace_run(w4h_session* s, const int32_t* tokens, const int32_t* forced, int32_t n_steps,
+                          uint64_t* trace, int64_t trace_len, int32_t* n_workgroups);
+
 /* ============================ decode drivers ============================ */
 
 typedef struct {

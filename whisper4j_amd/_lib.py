@@ -32,6 +32,7 @@ EXPORTS = (
     "w4h_model_destroy", "w4h_ggml_inspect", "w4h_ggml_read_tensor", "w4h_session_create", "w4h_session_destroy",
     "w4h_session_set_encoder", "w4h_session_reset", "w4h_session_kv_len", "w4h_session_set_suppress",
     "w4h_session_set_probe", "w4h_session_step", "w4h_session_run", "w4h_session_reorder", "w4h_session_time_run",
+    "w4h_session_trace_run",
     "w4h_decode", "w4h_decode_beam", "w4h_decode_with_fallback", "w4h_compression_ratio", "w4h_op_linear",
     "w4h_op_layernorm", "w4h_op_gelu", "w4h_op_attention", "w4h_op_select",
 )
@@ -110,6 +111,7 @@ def lib():
         "w4h_session_run": (i32, [vp, i32p, i32p, i32, i32, ctypes.POINTER(StepOut)]),
         "w4h_session_reorder": (i32, [vp, i32p]),
         "w4h_session_time_run": (i32, [vp, i32p, i32p, i32, i32, f32p, ctypes.POINTER(StepOut)]),
+        "w4h_session_trace_run": (i32, [vp, i32p, i32p, i32, ctypes.POINTER(ctypes.c_uint64), ctypes.c_int64, i32p]),
         "w4h_decode": (i32, [vp, ctypes.POINTER(DecodeOpts), ctypes.POINTER(DecodeResult)]),
         "w4h_decode_beam": (i32, [vp, ctypes.POINTER(DecodeOpts), ctypes.POINTER(DecodeResult)]),
         "w4h_decode_with_fallback": (i32, [vp, ctypes.POINTER(DecodeOpts), ctypes.POINTER(DecodeResult)]),

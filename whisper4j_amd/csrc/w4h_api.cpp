@@ -415,7 +415,7 @@ struct w4h_session {
   int S = 1, X = 1, max_ctx = 0, grid = 0, ncs_max = 0, ncc = 0, chc = 0, rpw = 0, mw = 0;
   size_t lds = 0;
   hipStream_t stream = nullptr;
-  DevBuf kvk, kvv, xk, xv, slots, ll, err, out, toks, forced, mask, mask2, logits, xa_tmp;
+  DevBuf kvk, kvv, xk, xv, slots, ll, err, out, toks, forced, mask, mask2, logits, xa_tmp, trace;
   u64 *qkv = nullptr, *sp = nullptr, *x1 = nullptr, *cq = nullptr, *cp = nullptr, *x2 = nullptr, *hm = nullptr,
       *x3 = nullptr, *lp = nullptr, *lpa = nullptr;
   int kv_len = 0;
@@ -482,7 +482,7 @@ static int ensure(DevBuf& b, size_t bytes) {
 
 // Launch n_steps steps; tokens/forced are host arrays.  Results (if out) are copied back.
 int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int n_steps, const uint32_t* extra_mask,
-              int topk, w4h_step_out* out, float* logits, float* ms) {
+              int topk, w4h_step_out* out, float* logits, float* ms, uint64_t* trace = nullptr) {
   if (s->closed) return fail(W4H_ERR_CLOSED, "session destroyed");
   if (!tokens || n_steps <= 0) return fail(W4H_ERR_INVALID, "tokens and n_steps > 0 required");
   if (topk < 0 || topk > W4H_TOPK_MAX) return fail(W4H_ERR_INVALID, "topk %d outside [0, %d]", topk, W4H_TOPK_MAX);
@@ -514,6 +514,8 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
   }
   if (out && (rc = ensure(s->out, sizeof(w4h_step_out) * (size_t)n_steps * s->S))) return rc;
   if (logits && (rc = ensure(s->logits, sizeof(float) * (size_t)n_steps * s->S * V))) return rc;
+  const size_t trace_n = (size_t)n_steps * (6 * s->m->dims.n_text_layer + 2) * 4 * s->grid;
+  if (trace && (rc = ensure(s->trace, trace_n * sizeof(uint64_t)))) return rc;
   HIPCHK(hipMemsetAsync(s->err.p, 0, sizeof(unsigned), s->stream));
   StepParams p = base_params(s);
   p.nsteps = n_steps;
@@ -525,6 +527,7 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
   p.topk = topk;
   p.out = out ? s->out.as<w4h_step_out>() : nullptr;
   p.logits_out = logits ? s->logits.as<float>() : nullptr;
+  p.trace = trace ? s->trace.as<unsigned long long>() : nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   if (ms) {
     HIPCHK(hipEventCreate(&e0));
@@ -540,6 +543,7 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
   if (out) HIPCHK(hipMemcpyAsync(out, s->out.p, sizeof(w4h_step_out) * (size_t)n_steps * s->S, hipMemcpyDeviceToHost, s->stream));
   if (logits)
     HIPCHK(hipMemcpyAsync(logits, s->logits.p, sizeof(float) * (size_t)n_steps * s->S * V, hipMemcpyDeviceToHost, s->stream));
+  if (trace) HIPCHK(hipMemcpyAsync(trace, s->trace.p, trace_n * sizeof(uint64_t), hipMemcpyDeviceToHost, s->stream));
   HIPCHK(hipStreamSynchronize(s->stream));
   if (ms) {
     HIPCHK(hipEventElapsedTime(ms, e0, e1));
@@ -573,7 +577,7 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   s->X = desc->n_encoders;
   s->max_ctx = desc->max_ctx;
   const int L = D.n_text_layer, d = D.n_text_state, H = D.n_text_head, A = D.n_audio_ctx, V = D.n_vocab;
-  s->ncs_max = (s->max_ctx + kSelfChunk - 1) / kSelfChunk;
+  s->ncs_max = (s->max_ctx + kSelfChunk - 1) / kSelfChunk + 1;  // cached-key chunks + the current key
   s->ncc = (A + kMaxChunk - 1) / kMaxChunk;
   s->chc = (A + s->ncc - 1) / s->ncc;
   s->mw = (V + 31) / 32;
@@ -734,9 +738,25 @@ int w4h_session_time_run(w4h_session* s, const int32_t* tokens, const int32_t* f
   for (int r = 0; r < n_repeats; r++) {
     s->kv_len = kv0;
     int rc = run_steps(s, tokens, forced, n_steps, nullptr, 0, r + 1 == n_repeats ? out : nullptr, nullptr, &ms_out[r]);
-    if (rc) return rc;
+    if (rc) {
+      s->kv_len = kv0;
+      return rc;
+    }
   }
+  s->kv_len = kv0;
   return W4H_OK;
+}
+
+int w4h_session_trace_run(w4h_session* s, const int32_t* tokens, const int32_t* forced, int32_t n_steps, uint64_t* trace,
+                          int64_t trace_len, int32_t* n_workgroups) {
+  if (!s || !trace || !n_workgroups) return fail(W4H_ERR_INVALID, "null argument");
+  const int64_t need = (int64_t)n_steps * (6 * s->m->dims.n_text_layer + 2) * 4 * s->grid;
+  *n_workgroups = s->grid;
+  if (trace_len < need) return fail(W4H_ERR_INVALID, "trace needs %lld entries", (long long)need);
+  const int kv0 = s->kv_len;
+  int rc = run_steps(s, tokens, forced, n_steps, nullptr, 0, nullptr, nullptr, nullptr, trace);
+  s->kv_len = kv0;
+  return rc;
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -26,7 +26,6 @@ namespace w4h {
 
 constexpr unsigned kSpinLimit = 1u << 20;  // polls before a wait is declared expired (~1 s)
 constexpr int PFR = 8;  // 16-byte weight chunks per lane kept in registers (prefetched) per item
-constexpr int PFL = 8;  // the same for the logits phase (rows of the tied embedding)
 constexpr int KPT_SELF = kSelfChunk / 32;   // keys per thread, self-attention chunk
 constexpr int KPT_CROSS = kMaxChunk / 32;   // keys per thread, cross-attention chunk
 constexpr int kPollBatch = 8;  // tagged words each thread loads before checking tags
@@ -43,6 +42,30 @@ DEV float2 h2x2(uint32_t u) {
   return __half22float2(h);
 }
 
+// Raw buffer loads: the descriptor carries the buffer size, and the hardware returns zero for any
+// access past it, so disabled lanes load from kOOB instead of branching around the load.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kOOB = 0x80000000u;  // beyond every buffer this library creates (< 2 GiB)
+DEV __amdgpu_buffer_rsrc_t brsrc(const void* base, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)(bytes > 0x7fffffffu ? 0x7fffffffu : bytes),
+                                           0x00020000);
+}
+DEV uint4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+DEV uint16_t bld2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+
+// Self-KV rows: written with device-coherent (sc1, write-through) stores and read back with sc1
+// loads by other workgroups at later steps of the same launch.  kv_drain() waits until this
+// wave's stores have completed before it publishes anything that comes after them.
+DEV void kv_store(uint16_t* base, size_t bytes, size_t elem, uint16_t v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, brsrc(base, bytes), (int)(elem * 2), 0, 16);
+}
+DEV void kv_drain() { __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0), expcnt and lgkmcnt untouched */ }
+
 DEV u64 ll_ld(const u64* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 DEV void ll_st(u64* p, float v, uint32_t tag) {
   __hip_atomic_store(p, ((u64)tag << 32) | (u64)__float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -54,15 +77,41 @@ DEV void raise_err(unsigned* err, unsigned code) {
   __hip_atomic_fetch_or(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+// DPP lane moves (gfx9 dpp_ctrl encodings): quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E,
+// row_half_mirror = 0x141 (lane i <-> 7-i within 8), row_mirror = 0x140 (i <-> 15-i within 16),
+// row_ror:8 = 0x128, row_bcast:15 = 0x142, row_bcast:31 = 0x143.
+template <int CTRL, int ROWMASK = 0xF, bool BC = true>
+DEV float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWMASK, 0xF, BC));
+}
+// Sum over each aligned group of 8 lanes; every lane of the group gets it.
+DEV float sum8(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
   return v;
 }
-DEV float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+// Sum over each row of 16 lanes.
+DEV float sum16(float v) {
+  v = sum8(v);
+  v += dpp<0x140>(v);
   return v;
+}
+DEV float wave_sum(float v) {
+  v = sum16(v);
+  // rows -> lane 63: row_bcast:15 adds row r's lane 15 into row r+1, row_bcast:31 lane 31 into rows 2-3
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+DEV float wave_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), 0x142, 0xA, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), 0x143, 0xC, 0xF, false)));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 // (value, index) maximum; equal values keep the lower index.  NaN never wins.
 DEV void wave_argmax(float& v, int& i) {
@@ -144,6 +193,46 @@ DEV bool ll_poll1(const u64* src, int n, float* dst, uint32_t tag, unsigned* err
   return ll_poll2(src, n, dst, nullptr, 0, nullptr, tag, err);
 }
 
+// Cheap readiness wait before a full read: one wave polls the words k*stride + off1 (and + off2
+// when off2 >= 0) for k < nrec with a short sleep between rounds.  These are the last words each
+// producer writes, so the full read that follows normally finds every tag in place on its first
+// round (it still verifies every word).  Keeps the number of polling loads in flight low.
+DEV bool ll_wait_sparse(const u64* src, int nrec, int stride, int off1, int off2, uint32_t tag, unsigned* err) {
+  bool fail = false;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int per = off2 >= 0 ? 2 : 1;
+    const int total = nrec * per;
+    for (int base = 0; base < total && !fail; base += 64 * kPollBatch) {
+      unsigned spins = 0;
+      while (true) {
+        bool ok = true;
+#pragma unroll
+        for (int u = 0; u < kPollBatch; ++u) {
+          const int i = base + u * 64 + lane;
+          if (i < total) {
+            const int k = i / per, w = (per == 2 && (i & 1)) ? off2 : off1;
+            ok &= (uint32_t)(ll_ld(src + (size_t)k * stride + w) >> 32) == tag;
+          }
+        }
+        if (__all(ok)) break;
+        ++spins;
+        if (spins > kSpinLimit) {
+          raise_err(err, 1u);
+          fail = true;
+          break;
+        }
+        if ((spins & 63u) == 0 && aborted(err)) {
+          fail = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+  }
+  return !__syncthreads_or(fail);
+}
+
 // ------------------------------------------------------------------------------------------------
 // GEMV over one item of 8 weight rows, for up to SM activation rows held in LDS.
 //
@@ -162,26 +251,27 @@ template <int R, int WQ8>
 DEV void gemv_prefetch(const void* W, const uint16_t* Ws, int N, int K, int r0, WRegs<R>& wr) {
   const int tid = threadIdx.x, lane = tid & 63, row = lane >> 3, slot = ((tid >> 6) << 3) | (lane & 7);
   const int gr = r0 + row;
-  if (gr >= N) return;
+  const bool rok = gr < N;
   if (!WQ8) {
     const int nch = K >> 3;
-    const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(W) + (size_t)gr * K);
+    const auto rs = brsrc(W, (size_t)N * K * 2);
+    const uint32_t base = (uint32_t)gr * (uint32_t)K * 2u;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      int c = slot + 32 * r;
-      if (c < nch) wr.w[r] = src[c];
+      const int c = slot + 32 * r;
+      wr.w[r] = bld16(rs, (rok && c < nch) ? base + (uint32_t)c * 16u : kOOB);
     }
   } else {
     const int nch = K >> 4;
-    const uint4* src = reinterpret_cast<const uint4*>(static_cast<const int8_t*>(W) + (size_t)gr * K);
-    const uint16_t* ss = Ws + (size_t)gr * (K >> 5);
+    const auto rs = brsrc(W, (size_t)N * K);
+    const auto ss = brsrc(Ws, (size_t)N * (K >> 5) * 2);
+    const uint32_t base = (uint32_t)gr * (uint32_t)K, sbase = (uint32_t)gr * (uint32_t)(K >> 5) * 2u;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      int c = slot + 32 * r;
-      if (c < nch) {
-        wr.w[r] = src[c];
-        wr.s[r] = ss[c >> 1];
-      }
+      const int c = slot + 32 * r;
+      const bool ok = rok && c < nch;
+      wr.w[r] = bld16(rs, ok ? base + (uint32_t)c * 16u : kOOB);
+      wr.s[r] = bld2(ss, ok ? sbase + (uint32_t)(c >> 1) * 2u : kOOB);
     }
   }
 }
@@ -215,6 +305,44 @@ DEV float dot16_q8(const uint4& w, const float* x) {
   return s;
 }
 
+// Chunks of a row beyond the R prefetched rounds: loaded here, four rounds at a time, with a
+// round count that is uniform across the wave (disabled lanes load zeros).
+template <int R, int WQ8, int SM>
+DEV void stream_rest(const void* W, const uint16_t* Ws, int N, int K, int gr, int slot, int S, const float* x,
+                     float (&acc)[SM]) {
+  const int nch = WQ8 ? (K >> 4) : (K >> 3);
+  const int extra = nch - 32 * R;  // chunks not prefetched (per row)
+  if (extra <= 0) return;
+  const auto rs = brsrc(W, (size_t)N * K * (WQ8 ? 1 : 2));
+  const auto ss = brsrc(Ws, WQ8 ? (size_t)N * (K >> 5) * 2 : 0);
+  const uint32_t base = (uint32_t)gr * (uint32_t)K * (WQ8 ? 1u : 2u);
+  const uint32_t sbase = (uint32_t)gr * (uint32_t)(K >> 5) * 2u;
+  for (int c0 = 32 * R; c0 < nch; c0 += 32 * 4) {
+    uint4 t[4];
+    uint16_t ts[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = c0 + slot + 32 * u;
+      t[u] = bld16(rs, c < nch ? base + (uint32_t)c * 16u : kOOB);
+      if (WQ8) ts[u] = bld2(ss, c < nch ? sbase + (uint32_t)(c >> 1) * 2u : kOOB);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = c0 + slot + 32 * u;
+      if (c < nch) {
+#pragma unroll
+        for (int s = 0; s < SM; ++s)
+          if (s < S) {
+            if (WQ8)
+              acc[s] = fmaf(h2f(ts[u]), dot16_q8(t[u], x + s * K + c * 16), acc[s]);
+            else
+              acc[s] += dot8_f16(t[u], x + s * K + c * 8);
+          }
+      }
+    }
+  }
+}
+
 // out[s*8 + r] = sum_k W[r0 + r][k] * x[s*K + k] for s < S (LDS in, LDS out).  Chunks of the
 // prefetched rounds come from registers; later rounds of long rows are loaded here.
 template <int R, int WQ8, int SM>
@@ -238,20 +366,7 @@ DEV void gemv_compute(const WRegs<R>& wr, const void* W, const uint16_t* Ws, int
             if (s < S) acc[s] += dot8_f16(wr.w[r], x + s * K + c * 8);
         }
       }
-      const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(W) + (size_t)gr * K);
-      for (int c = slot + 32 * R; c < nch; c += 32 * 4) {
-        uint4 t[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          if (c + 32 * u < nch) t[u] = src[c + 32 * u];
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          if (c + 32 * u < nch) {
-#pragma unroll
-            for (int s = 0; s < SM; ++s)
-              if (s < S) acc[s] += dot8_f16(t[u], x + s * K + (c + 32 * u) * 8);
-          }
-      }
+      stream_rest<R, 0, SM>(W, Ws, N, K, gr, slot, S, x, acc);
     } else {
       const int nch = K >> 4;
 #pragma unroll
@@ -264,34 +379,11 @@ DEV void gemv_compute(const WRegs<R>& wr, const void* W, const uint16_t* Ws, int
             if (s < S) acc[s] = fmaf(sc, dot16_q8(wr.w[r], x + s * K + c * 16), acc[s]);
         }
       }
-      const uint4* src = reinterpret_cast<const uint4*>(static_cast<const int8_t*>(W) + (size_t)gr * K);
-      const uint16_t* ss = Ws + (size_t)gr * (K >> 5);
-      for (int c = slot + 32 * R; c < nch; c += 32 * 4) {
-        uint4 t[4];
-        uint16_t ts[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          if (c + 32 * u < nch) {
-            t[u] = src[c + 32 * u];
-            ts[u] = ss[(c + 32 * u) >> 1];
-          }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          if (c + 32 * u < nch) {
-            const float sc = h2f(ts[u]);
-#pragma unroll
-            for (int s = 0; s < SM; ++s)
-              if (s < S) acc[s] = fmaf(sc, dot16_q8(t[u], x + s * K + (c + 32 * u) * 16), acc[s]);
-          }
-      }
+      stream_rest<R, 1, SM>(W, Ws, N, K, gr, slot, S, x, acc);
     }
   }
 #pragma unroll
-  for (int s = 0; s < SM; ++s) {
-    acc[s] += __shfl_xor(acc[s], 1);
-    acc[s] += __shfl_xor(acc[s], 2);
-    acc[s] += __shfl_xor(acc[s], 4);
-  }
+  for (int s = 0; s < SM; ++s) acc[s] = sum8(acc[s]);
   if (sub == 0) {
 #pragma unroll
     for (int s = 0; s < SM; ++s)
@@ -301,6 +393,92 @@ DEV void gemv_compute(const WRegs<R>& wr, const void* W, const uint16_t* Ws, int
   if (tid < 8 * S) {
     const int s = tid >> 3, rr = tid & 7;
     out[s * 8 + rr] = (red[rr * SM + s] + red[(8 + rr) * SM + s]) + (red[(16 + rr) * SM + s] + red[(24 + rr) * SM + s]);
+  }
+  __syncthreads();
+}
+
+// Batched GEMV: NB items of 8 rows (item i covers rows (it0 + i * istr) * 8 .. + 8, i < nit) with
+// one cross-wave reduction for the whole batch.  Same lane layout as above.
+template <int R, int NB>
+struct WBatch {
+  uint4 w[NB][R];
+  uint16_t s[NB][R];
+};
+
+template <int R, int NB, int WQ8>
+DEV void gemvb_prefetch(const void* W, const uint16_t* Ws, int N, int K, int it0, int istr, int nit,
+                        WBatch<R, NB>& wb) {
+  const int tid = threadIdx.x, lane = tid & 63, row = lane >> 3, slot = ((tid >> 6) << 3) | (lane & 7);
+  const int nch = WQ8 ? (K >> 4) : (K >> 3);
+  const auto rs = brsrc(W, (size_t)N * K * (WQ8 ? 1 : 2));
+  const auto ss = brsrc(Ws, WQ8 ? (size_t)N * (K >> 5) * 2 : 0);
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int gr = (it0 + i * istr) * 8 + row;
+    const bool rok = i < nit && gr < N;
+    const uint32_t base = (uint32_t)gr * (uint32_t)K * (WQ8 ? 1u : 2u);
+    const uint32_t sbase = (uint32_t)gr * (uint32_t)(K >> 5) * 2u;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int c = slot + 32 * r;
+      const bool ok = rok && c < nch;
+      wb.w[i][r] = bld16(rs, ok ? base + (uint32_t)c * 16u : kOOB);
+      if (WQ8) wb.s[i][r] = bld2(ss, ok ? sbase + (uint32_t)(c >> 1) * 2u : kOOB);
+    }
+  }
+}
+
+// One row of an item: dot of the lane's chunks (prefetched rounds, then streamed ones).
+template <int R, int WQ8, int SM>
+DEV void row_dots(const uint4 (&w)[R], const uint16_t (&sc)[R], const void* W, const uint16_t* Ws, int N, int gr,
+                  int K, int slot, int S, const float* x, float (&acc)[SM]) {
+  const int nch = WQ8 ? (K >> 4) : (K >> 3);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int c = slot + 32 * r;
+    if (c < nch) {
+#pragma unroll
+      for (int s = 0; s < SM; ++s)
+        if (s < S) {
+          if (WQ8)
+            acc[s] = fmaf(h2f(sc[r]), dot16_q8(w[r], x + s * K + c * 16), acc[s]);
+          else
+            acc[s] += dot8_f16(w[r], x + s * K + c * 8);
+        }
+    }
+  }
+  stream_rest<R, WQ8, SM>(W, Ws, N, K, gr, slot, S, x, acc);
+}
+
+// out[(i * SM + s) * 8 + r] = sum_k W[(it0 + i * istr) * 8 + r][k] * x[s * K + k]
+// red: LDS [NB][32][SM], out: LDS [NB][SM][8].
+template <int R, int NB, int WQ8, int SM>
+DEV void gemvb_compute(const WBatch<R, NB>& wb, const void* W, const uint16_t* Ws, int N, int K, int it0, int istr,
+                       int nit, int S, const float* x, float* red, float* out) {
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, row = lane >> 3, sub = lane & 7;
+  const int slot = (w << 3) | sub;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    if (i < nit) {
+      float acc[SM];
+#pragma unroll
+      for (int s = 0; s < SM; ++s) acc[s] = 0.f;
+      const int gr = (it0 + i * istr) * 8 + row;
+      if (gr < N) row_dots<R, WQ8, SM>(wb.w[i], wb.s[i], W, Ws, N, gr, K, slot, S, x, acc);
+#pragma unroll
+      for (int s = 0; s < SM; ++s) acc[s] = sum8(acc[s]);
+      if (sub == 0) {
+#pragma unroll
+        for (int s = 0; s < SM; ++s)
+          if (s < S) red[(i * 32 + (w << 3) + row) * SM + s] = acc[s];
+      }
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < nit * S * 8; idx += kThreads) {
+    const int i = idx / (S * 8), rem = idx - i * S * 8, s = rem >> 3, rr = rem & 7;
+    const float* rp = red + i * 32 * SM;
+    out[(i * SM + s) * 8 + rr] = (rp[rr * SM + s] + rp[(8 + rr) * SM + s]) + (rp[(16 + rr) * SM + s] + rp[(24 + rr) * SM + s]);
   }
   __syncthreads();
 }
@@ -340,17 +518,20 @@ struct KVRegs {
   uint4 v[KPT];
 };
 
-template <int KPT, class Off>
-DEV void attn_prefetch(const uint16_t* kb, const uint16_t* vb, Off off, int n, KVRegs<KPT>& r) {
+// AUX 16 (sc1) makes the loads coherent at device scope: used for the self-KV cache, whose rows
+// are appended by other workgroups earlier in the same launch.
+template <int KPT, int AUX, class Off>
+DEV void attn_prefetch(const uint16_t* kb, const uint16_t* vb, size_t kv_bytes, Off off, int n, KVRegs<KPT>& r) {
   const int sub = threadIdx.x & 7, kg = threadIdx.x >> 3;
+  const auto rk = brsrc(kb, kv_bytes), rv = brsrc(vb, kv_bytes);
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
-    int j = kg + 32 * i;
-    if (j < n) {
-      size_t o = off(j) + (size_t)sub * 8;
-      r.k[i] = *reinterpret_cast<const uint4*>(kb + o);
-      r.v[i] = *reinterpret_cast<const uint4*>(vb + o);
-    }
+    const int j = kg + 32 * i;
+    const uint32_t o = j < n ? (uint32_t)((off(j) + (size_t)sub * 8) * 2) : kOOB;
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)o, 0, AUX);
+    const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rv, (int)o, 0, AUX);
+    r.k[i] = make_uint4(a.x, a.y, a.z, a.w);
+    r.v[i] = make_uint4(b.x, b.y, b.z, b.w);
   }
 }
 
@@ -371,11 +552,7 @@ DEV void attn_compute(const KVRegs<KPT>& r, int n, int ns, const float* q, const
         if (s < ns) part[s] = dot8_f16(r.k[i], q + s * kHeadDim + sub * 8);
     }
 #pragma unroll
-    for (int s = 0; s < SM; ++s) {
-      part[s] += __shfl_xor(part[s], 1);
-      part[s] += __shfl_xor(part[s], 2);
-      part[s] += __shfl_xor(part[s], 4);
-    }
+    for (int s = 0; s < SM; ++s) part[s] = sum8(part[s]);
     if (sub == 0 && j < n) {
 #pragma unroll
       for (int s = 0; s < SM; ++s)
@@ -437,23 +614,22 @@ DEV void attn_compute(const KVRegs<KPT>& r, int n, int ns, const float* q, const
 #pragma unroll
   for (int s = 0; s < SM; ++s)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      a[s][e] += __shfl_xor(a[s][e], 8);
-      a[s][e] += __shfl_xor(a[s][e], 16);
-      a[s][e] += __shfl_xor(a[s][e], 32);
-    }
-  if (lane < 8) {
+    for (int e = 0; e < 8; ++e) a[s][e] += dpp<0x128>(a[s][e]);  // + lane ^ 8
+  // lanes 0..7 of each 16-lane row now hold the row's partial: 4 rows x 4 waves -> LDS
+  if ((lane & 15) < 8) {
+    const int rw = w * 4 + (lane >> 4);
 #pragma unroll
     for (int s = 0; s < SM; ++s)
       if (s < ns)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) red[(w * SM + s) * kHeadDim + sub * 8 + e] = a[s][e];
+        for (int e = 0; e < 8; ++e) red[(rw * SM + s) * kHeadDim + sub * 8 + e] = a[s][e];
   }
   __syncthreads();
   for (int i = tid; i < ns * kHeadDim; i += kThreads) {
     const int s = i >> 6, e = i & 63;
-    float o = (red[(0 * SM + s) * kHeadDim + e] + red[(1 * SM + s) * kHeadDim + e]) +
-              (red[(2 * SM + s) * kHeadDim + e] + red[(3 * SM + s) * kHeadDim + e]);
+    float o = 0.f;
+#pragma unroll
+    for (int rw = 0; rw < 16; ++rw) o += red[(rw * SM + s) * kHeadDim + e];
     if (kx != nullptr) o = fmaf(sc[s * scs + n], vx[e], o);
     acc_out[i] = o;
   }
@@ -647,24 +823,45 @@ DEV bool masked(const uint32_t* m, int mw, int s, int v) {
 // The persistent decoder-step kernel.
 
 struct Lds {
-  float* xin;   // [S][4d]   polled activations
-  float* xn;    // [S][d]    LayerNorm output / merged attention output
-  float* red;   // [32][SM]
-  float* gout;  // [SM][8]
+  float* xin;   // [S][4d]        polled activations
+  float* xn;    // [S][d]         LayerNorm output / merged attention output
+  float* red;   // [kNB][32][SM]  GEMV cross-wave partials
+  float* gout;  // [kNB][SM][8]   GEMV results
   float* scr;   // [8]
-  int* toks;    // [kMaxRows] tokens of the current step
+  int* toks;    // [kMaxRows]     tokens of the current step
   float* big;   // phase scratch
 };
 
-// First work item of workgroup g for a phase with `off` rotation, G workgroups.
-DEV int first_item(int g, int off, int G) { return (g - off % G + G) % G; }
+constexpr int kNB = 8;  // items per GEMV batch (64 rows)
+
+// Workgroup group of a phase.  Consecutive phases run on disjoint quarters of the grid (phase q on
+// quarter q % 4), so a workgroup has three phases of idle time to prefetch the weights of its next
+// item, and only a quarter of the grid polls any one exchange buffer.
+struct Grp {
+  int base, size;
+};
+DEV Grp phase_group(int q, int G) {
+  const int ng = G >= 64 ? 4 : 1;
+  const int sz = G / ng;
+  return Grp{(q % ng) * sz, sz};
+}
+// First item of this workgroup in the group (items i, i + size, ...), or a value past any item count.
+DEV int grp_first(Grp gr) {
+  const int g = blockIdx.x;
+  return (g >= gr.base && g < gr.base + gr.size) ? g - gr.base : 0x7fffffff;
+}
 
 struct StepCtx {
   uint32_t tag;
-  int st, kv, pe, ncs;
+  int st, kv, pe, ph, nph;
 };
 
-#define NOINL __device__ __noinline__
+// Diagnostics: sub-phase timestamps (0 start, 1 inputs arrived, 2 computed, 3 end).
+#define STAMP(sub)                                                                                            \
+  do {                                                                                                        \
+    if (p.trace != nullptr && threadIdx.x == 0)                                                               \
+      p.trace[(((size_t)c.st * c.nph + c.ph) * 4 + (sub)) * gridDim.x + blockIdx.x] = wall_clock64();         \
+  } while (0)
 
 // x of layer 0 = token embedding + positional embedding (exact dequant, one rounding)
 template <int WQ8>
@@ -685,163 +882,181 @@ DEV void embed(const StepParams& p, const Lds& m, const StepCtx& c, float* dst) 
   __syncthreads();
 }
 
-// LN1 + QKV; k and v are also appended to the self-KV cache at position c.kv.
+// Layer input x: the embedding at layer 0, else the previous layer's output.
+template <int WQ8>
+DEV bool layer_input(const StepParams& p, const Lds& m, const StepCtx& c, int l, float* dst) {
+  if (l == 0) {
+    embed<WQ8>(p, m, c, dst);
+    return true;
+  }
+  return ll_poll1(p.x3 + (size_t)(l - 1) * p.S * p.d, p.S * p.d, dst, c.tag, p.err);
+}
+
+// Self-attention with the q/k/v projection folded in.  Per (row s, head h) the items are:
+//   j <  nold : cached-key chunk j (keys [j*C, min((j+1)*C, kv)));  projects q_h, attends, writes a
+//               partial (m, l, acc[64]) to chunk slot j;
+//   j == nold : projects q_h and k_h, appends k_h to the cache, writes the current key's score as
+//               (m = q.k * scale, l = 1) into chunk slot nold;
+//   j == nold+1: projects v_h, appends it to the cache, writes it as acc[64] of chunk slot nold.
+// All items depend only on the layer input, so the projection costs no extra hand-over.
 template <int SM, int WQ8>
-NOINL bool phase_qkv(const StepParams& p, Lds m, StepCtx c, int l, int rot) {
+DEV bool phase_self(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
   const int G = gridDim.x, tid = threadIdx.x, S = p.S, d = p.d, H = p.H, d3 = 3 * d;
   const LayerDev& lw = p.layers[l];
-  const int nitems = (d3 + 7) / 8;
-  const int it0 = first_item(blockIdx.x, rot, G);
-  if (it0 >= nitems) return true;
-  WRegs<PFR> wr;
-  gemv_prefetch<PFR, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, it0 * 8, wr);
-  if (l == 0) {
-    embed<WQ8>(p, m, c, m.xin);
-  } else {
-    if (!ll_poll1(p.x3 + (size_t)(l - 1) * S * d, S * d, m.xin, c.tag, p.err)) return false;
-  }
-  wg_layernorm(m.xin, m.xn, S, d, lw.ln1_g, lw.ln1_b, m.scr);
-  for (int it = it0; it < nitems; it += G) {
-    if (it != it0) gemv_prefetch<PFR, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, it * 8, wr);
-    gemv_compute<PFR, WQ8, SM>(wr, lw.w_qkv, lw.s_qkv, d3, d, it * 8, S, m.xn, m.red, m.gout);
-    if (tid < 8 * S) {
-      const int s = tid >> 3, row = it * 8 + (tid & 7);
-      if (row < d3) {
-        const float y = m.gout[tid] + lw.b_qkv[row];
-        const int part = row / d, e = row - part * d, h = e >> 6;
-        if (part > 0) {
-          uint16_t* dstkv = part == 1 ? p.kv_k : p.kv_v;
-          dstkv[((((size_t)l * S + s) * H + h) * p.max_ctx + c.kv) * kHeadDim + (e & 63)] = f2h(y);
-          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  const int nold = (c.kv + kSelfChunk - 1) / kSelfChunk;
+  const int per = nold + 2;
+  const int nitems = S * H * per;
+  bool have_x = false;
+  STAMP(0);
+  for (int it = grp_first(gr); it < nitems; it += gr.size) {
+    const int j = it % per, sh = it / per, h = sh % H, s = sh / H;
+    const int kind = j < nold ? 0 : (j == nold ? 1 : 2);
+    const int rowA = (kind == 2 ? 2 * d : 0) + h * kHeadDim;  // q rows, or v rows for the value item
+    WBatch<2, kNB> wa, wb;
+    gemvb_prefetch<2, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, wa);
+    if (kind == 1) gemvb_prefetch<2, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, (d + h * kHeadDim) >> 3, 1, kNB, wb);
+    const int k0 = j * kSelfChunk;
+    const int n = kind == 0 ? min(kSelfChunk, c.kv - k0) : 0;
+    const int32_t* slots = p.slots ? p.slots + (size_t)s * p.max_ctx : nullptr;
+    const size_t lb = (size_t)l * S;
+    const int mc = p.max_ctx;
+    auto off = [=](int jj) -> size_t {
+      const int pos = k0 + jj;
+      const int slot = slots ? slots[pos] : s;
+      return (((lb + slot) * H + h) * mc + pos) * kHeadDim;
+    };
+    KVRegs<KPT_SELF> kr;
+    if (kind == 0)
+      attn_prefetch<KPT_SELF, 16>(p.kv_k, p.kv_v, (size_t)p.L * S * H * p.max_ctx * kHeadDim * 2, off, n, kr);
+    if (!have_x) {
+      if (!layer_input<WQ8>(p, m, c, l, m.xin)) return false;
+      STAMP(1);
+      wg_layernorm(m.xin, m.xn, S, d, lw.ln1_g, lw.ln1_b, m.scr);
+      have_x = true;
+    }
+    float* va = m.big;              // [64] q (or v)
+    float* vb = va + kHeadDim;      // [64] k
+    float* pmv = vb + kHeadDim;     // [8]
+    float* plv = pmv + 8;           // [8]
+    float* acc = plv + 8;           // [64]
+    float* sc = acc + kHeadDim;     // [kSelfChunk + 4]
+    float* red = sc + kSelfChunk + 4;  // [16][64]
+    gemvb_compute<2, kNB, WQ8, SM>(wa, lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, 1, m.xn + s * d, m.red, m.gout);
+    if (tid < kHeadDim) va[tid] = m.gout[((tid >> 3) * SM) * 8 + (tid & 7)] + lw.b_qkv[rowA + tid];
+    if (kind == 1) {
+      gemvb_compute<2, kNB, WQ8, SM>(wb, lw.w_qkv, lw.s_qkv, d3, d, (d + h * kHeadDim) >> 3, 1, kNB, 1, m.xn + s * d,
+                                     m.red, m.gout);
+      if (tid < kHeadDim) vb[tid] = m.gout[((tid >> 3) * SM) * 8 + (tid & 7)] + lw.b_qkv[d + h * kHeadDim + tid];
+    }
+    __syncthreads();
+    u64* dst = p.sp + ((((size_t)l * p.ncs_max + (kind == 0 ? j : nold)) * S + s) * H + h) * kPartWords;
+    const size_t kvrow = ((((size_t)l * S + s) * H + h) * p.max_ctx + c.kv) * kHeadDim;
+    const size_t kv_bytes = (size_t)p.L * S * H * p.max_ctx * kHeadDim * 2;
+    if (kind == 0) {
+      attn_compute<KPT_SELF, 1>(kr, n, 1, va, nullptr, nullptr, 0.125f, sc, kSelfChunk + 4, red, pmv, plv, acc);
+      STAMP(2);
+      for (int i = tid; i < kPartWords; i += kThreads) ll_st(dst + i, i == 0 ? pmv[0] : (i == 1 ? plv[0] : acc[i - 2]), c.tag);
+    } else if (kind == 1) {
+      if (tid < 64) {
+        kv_store(p.kv_k, kv_bytes, kvrow + tid, f2h(vb[tid]));
+        const float t = wave_sum(va[tid] * vb[tid]);
+        kv_drain();
+        if (tid == 0) {
+          ll_st(dst + 0, t * 0.125f, c.tag);
+          ll_st(dst + 1, 1.0f, c.tag);
         }
-        ll_st(p.qkv + (((size_t)l * S + s) * H + h) * 3 * kHeadDim + part * kHeadDim + (e & 63), y, c.tag);
+      }
+    } else {
+      if (tid < 64) {
+        kv_store(p.kv_v, kv_bytes, kvrow + tid, f2h(va[tid]));
+        kv_drain();
+        ll_st(dst + 2 + tid, va[tid], c.tag);
       }
     }
   }
   return true;
 }
 
-// Self-attention: one item per (row, head, chunk of kSelfChunk keys); the current token's key and
-// value come from the tagged QKV words, earlier keys from the f16 cache.
-NOINL bool phase_self_attn(const StepParams& p, Lds m, StepCtx c, int l, int rot) {
-  const int G = gridDim.x, tid = threadIdx.x, S = p.S, H = p.H;
-  const int nitems = S * H * c.ncs;
-  for (int it = first_item(blockIdx.x, rot, G); it < nitems; it += G) {
-    const int ch = it % c.ncs, sh = it / c.ncs, h = sh % H, s = sh / H;
-    const int k0 = ch * kSelfChunk;
-    const int k1 = min(k0 + kSelfChunk, c.kv + 1);
-    const int ncache = min(k1, c.kv) - k0;
-    const bool cur = (k1 == c.kv + 1);
-    const int32_t* slots = p.slots ? p.slots + (size_t)s * p.max_ctx : nullptr;
-    const size_t lb = (size_t)l * S;
-    const int H_ = H, mc = p.max_ctx;
-    auto off = [=](int j) -> size_t {
-      const int pos = k0 + j;
-      const int slot = slots ? slots[pos] : s;
-      return (((lb + slot) * H_ + h) * mc + pos) * kHeadDim;
-    };
-    KVRegs<KPT_SELF> kr;
-    attn_prefetch<KPT_SELF>(p.kv_k, p.kv_v, off, ncache, kr);
-    float* q = m.big;  // q, k_cur, v_cur contiguous: [3][64]
-    float* kx = q + kHeadDim;
-    float* vx = kx + kHeadDim;
-    float* pmv = vx + kHeadDim;
-    float* plv = pmv + 8;
-    float* acc = plv + 8;
-    float* sc = acc + kHeadDim;
-    float* red = sc + kSelfChunk + 4;
-    const u64* qb = p.qkv + (((size_t)l * S + s) * H + h) * 3 * kHeadDim;
-    if (!ll_poll1(qb, cur ? 3 * kHeadDim : kHeadDim, q, c.tag, p.err)) return false;
-    attn_compute<KPT_SELF, 1>(kr, ncache, 1, q, cur ? kx : nullptr, vx, 0.125f, sc, kSelfChunk + 4, red, pmv, plv, acc);
-    u64* dst = p.sp + ((((size_t)l * p.ncs_max + ch) * S + s) * H + h) * kPartWords;
-    for (int i = tid; i < kPartWords; i += kThreads) ll_st(dst + i, i == 0 ? pmv[0] : (i == 1 ? plv[0] : acc[i - 2]), c.tag);
-  }
-  return true;
-}
-
 // Merge attention partials, out-projection, bias and residual:  xout = xres + (Wo . o + b).
 template <int SM, int WQ8>
-NOINL bool phase_out(const StepParams& p, Lds m, StepCtx c, int l, int rot, bool cross) {
+DEV bool phase_out(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr, bool cross) {
   const int G = gridDim.x, tid = threadIdx.x, S = p.S, d = p.d, H = p.H;
   const LayerDev& lw = p.layers[l];
   const void* W = cross ? lw.w_co : lw.w_o;
   const uint16_t* Ws = cross ? lw.s_co : lw.s_o;
   const float* bias = cross ? lw.b_co : lw.b_o;
   const int nitems = (d + 7) / 8;
-  const int it0 = first_item(blockIdx.x, rot, G);
+  const int it0 = grp_first(gr);
   if (it0 >= nitems) return true;
   WRegs<PFR> wr;
   gemv_prefetch<PFR, WQ8>(W, Ws, d, d, it0 * 8, wr);
   float* part = m.big;
-  const int nc = cross ? p.ncc : c.ncs;
+  const int nc = cross ? p.ncc : (c.kv + kSelfChunk - 1) / kSelfChunk + 1;
   const u64* psrc = cross ? p.cp + (size_t)l * p.ncc * S * H * kPartWords : p.sp + (size_t)l * p.ncs_max * S * H * kPartWords;
-  // residual input: x1 for the cross block, the layer input for the self block (layer 0: embedding)
+  // residual: x1 for the cross block, the layer input for the self block (layer 0: embedding)
   const u64* rsrc = cross ? p.x1 + (size_t)l * S * d : p.x3 + (size_t)(l > 0 ? l - 1 : 0) * S * d;
   const int rn = (cross || l > 0) ? S * d : 0;
+  STAMP(0);
   if (!ll_poll2(psrc, nc * S * H * kPartWords, part, rsrc, rn, m.xin, c.tag, p.err)) return false;
+  STAMP(1);
   if (rn == 0) embed<WQ8>(p, m, c, m.xin);
   attn_merge(part, nc, S * H, m.xn);
   u64* xout = (cross ? p.x2 : p.x1) + (size_t)l * S * d;
-  for (int it = it0; it < nitems; it += G) {
+  for (int it = it0; it < nitems; it += gr.size) {
     if (it != it0) gemv_prefetch<PFR, WQ8>(W, Ws, d, d, it * 8, wr);
     gemv_compute<PFR, WQ8, SM>(wr, W, Ws, d, d, it * 8, S, m.xn, m.red, m.gout);
     if (tid < 8 * S) {
       const int s = tid >> 3, row = it * 8 + (tid & 7);
       if (row < d) ll_st(xout + (size_t)s * d + row, m.xin[s * d + row] + (m.gout[tid] + bias[row]), c.tag);
     }
+    STAMP(2);
   }
   return true;
 }
 
-// LN2 + cross q, published head-major [H][S][64] so a head's rows are contiguous.
+// Cross-attention with the q projection folded in: one item per (encoder group, head, key chunk);
+// the item projects q_h for its rows from LN2(x1), then attends over its chunk of encoder keys.
+// Rows sharing an encoder output are processed together so the chunk's K/V is read once.
 template <int SM, int WQ8>
-NOINL bool phase_cq(const StepParams& p, Lds m, StepCtx c, int l, int rot) {
-  const int G = gridDim.x, tid = threadIdx.x, S = p.S, d = p.d, H = p.H;
+DEV bool phase_cross(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
+  const int G = gridDim.x, tid = threadIdx.x, S = p.S, d = p.d, H = p.H, L = p.L;
   const LayerDev& lw = p.layers[l];
-  const int nitems = (d + 7) / 8;
-  const int it0 = first_item(blockIdx.x, rot, G);
-  if (it0 >= nitems) return true;
-  WRegs<PFR> wr;
-  gemv_prefetch<PFR, WQ8>(lw.w_cq, lw.s_cq, d, d, it0 * 8, wr);
-  if (!ll_poll1(p.x1 + (size_t)l * S * d, S * d, m.xin, c.tag, p.err)) return false;
-  wg_layernorm(m.xin, m.xn, S, d, lw.ln2_g, lw.ln2_b, m.scr);
-  for (int it = it0; it < nitems; it += G) {
-    if (it != it0) gemv_prefetch<PFR, WQ8>(lw.w_cq, lw.s_cq, d, d, it * 8, wr);
-    gemv_compute<PFR, WQ8, SM>(wr, lw.w_cq, lw.s_cq, d, d, it * 8, S, m.xn, m.red, m.gout);
-    if (tid < 8 * S) {
-      const int s = tid >> 3, row = it * 8 + (tid & 7);
-      if (row < d)
-        ll_st(p.cq + (((size_t)l * H + (row >> 6)) * S + s) * kHeadDim + (row & 63), m.gout[tid] + lw.b_cq[row], c.tag);
-    }
-  }
-  return true;
-}
-
-// Cross-attention: one item per (encoder group, head, key chunk); rows sharing an encoder output
-// are processed together so the chunk's K/V is read once.
-template <int SM>
-NOINL bool phase_cross_attn(const StepParams& p, Lds m, StepCtx c, int l, int rot) {
-  const int G = gridDim.x, tid = threadIdx.x, S = p.S, H = p.H, L = p.L;
   const int ngrp = p.X == 1 ? 1 : S;
   const int ns = p.X == 1 ? S : 1;
   const int nitems = ngrp * H * p.ncc;
-  for (int it = first_item(blockIdx.x, rot, G); it < nitems; it += G) {
+  bool have_x = false;
+  STAMP(0);
+  for (int it = grp_first(gr); it < nitems; it += gr.size) {
     const int ch = it % p.ncc, gh = it / p.ncc, h = gh % H, grp = gh / H;
     const int k0 = ch * p.chc;
     const int n = min(p.chc, p.A - k0);
     const size_t base = ((((size_t)grp * L + l) * H + h) * p.A + k0) * kHeadDim;
     auto off = [=](int j) -> size_t { return base + (size_t)j * kHeadDim; };
+    WBatch<2, kNB> wq;
+    gemvb_prefetch<2, kNB, WQ8>(lw.w_cq, lw.s_cq, d, d, (h * kHeadDim) >> 3, 1, kNB, wq);
     KVRegs<KPT_CROSS> kr;
-    attn_prefetch<KPT_CROSS>(p.xk, p.xv, off, n, kr);
-    float* q = m.big;                     // [ns][64]
-    float* pmv = q + SM * kHeadDim;       // [8]
-    float* plv = pmv + 8;                 // [8]
-    float* acc = plv + 8;                 // [ns][64]
-    float* red = acc + SM * kHeadDim;     // [4][SM][64]
-    float* sc = red + 4 * SM * kHeadDim;  // [ns][kMaxChunk + 4]
-    const u64* qsrc = p.cq + (((size_t)l * H + h) * S + (p.X == 1 ? 0 : grp)) * kHeadDim;
-    if (!ll_poll1(qsrc, ns * kHeadDim, q, c.tag, p.err)) return false;
+    attn_prefetch<KPT_CROSS, 0>(p.xk, p.xv, (size_t)p.X * L * H * p.A * kHeadDim * 2, off, n, kr);
+    if (!have_x) {
+      if (!ll_poll1(p.x1 + (size_t)l * S * d, S * d, m.xin, c.tag, p.err)) return false;
+      STAMP(1);
+      wg_layernorm(m.xin, m.xn, S, d, lw.ln2_g, lw.ln2_b, m.scr);
+      have_x = true;
+    }
+    float* q = m.big;                      // [ns][64]
+    float* pmv = q + SM * kHeadDim;        // [8]
+    float* plv = pmv + 8;                  // [8]
+    float* acc = plv + 8;                  // [ns][64]
+    float* red = acc + SM * kHeadDim;      // [4][SM][64]
+    float* sc = red + 4 * SM * kHeadDim;   // [ns][kMaxChunk + 4]
+    const float* xs = m.xn + (p.X == 1 ? 0 : grp) * d;
+    gemvb_compute<2, kNB, WQ8, SM>(wq, lw.w_cq, lw.s_cq, d, d, (h * kHeadDim) >> 3, 1, kNB, ns, xs, m.red, m.gout);
+    for (int i = tid; i < ns * kHeadDim; i += kThreads) {
+      const int s = i >> 6, e = i & 63;
+      q[i] = m.gout[((e >> 3) * SM + s) * 8 + (e & 7)] + lw.b_cq[h * kHeadDim + e];
+    }
+    __syncthreads();
     attn_compute<KPT_CROSS, SM>(kr, n, ns, q, nullptr, nullptr, 0.125f, sc, kMaxChunk + 4, red, pmv, plv, acc);
+    STAMP(2);
     for (int i = tid; i < ns * kPartWords; i += kThreads) {
       const int s = i / kPartWords, w = i - s * kPartWords;
       const int row = p.X == 1 ? s : grp;
@@ -854,84 +1069,113 @@ NOINL bool phase_cross_attn(const StepParams& p, Lds m, StepCtx c, int l, int ro
 
 // LN3 + MLP1 + GELU table lookup.
 template <int SM, int WQ8>
-NOINL bool phase_mlp1(const StepParams& p, Lds m, StepCtx c, int l, int rot) {
+DEV bool phase_mlp1(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
   const int G = gridDim.x, tid = threadIdx.x, S = p.S, d = p.d, d4 = 4 * d;
   const LayerDev& lw = p.layers[l];
   const int nitems = (d4 + 7) / 8;
-  const int it0 = first_item(blockIdx.x, rot, G);
+  const int it0 = grp_first(gr);
   if (it0 >= nitems) return true;
   WRegs<PFR> wr;
+  STAMP(0);
   gemv_prefetch<PFR, WQ8>(lw.w_1, lw.s_1, d4, d, it0 * 8, wr);
   if (!ll_poll1(p.x2 + (size_t)l * S * d, S * d, m.xin, c.tag, p.err)) return false;
+  STAMP(1);
   wg_layernorm(m.xin, m.xn, S, d, lw.ln3_g, lw.ln3_b, m.scr);
-  for (int it = it0; it < nitems; it += G) {
+  for (int it = it0; it < nitems; it += gr.size) {
     if (it != it0) gemv_prefetch<PFR, WQ8>(lw.w_1, lw.s_1, d4, d, it * 8, wr);
     gemv_compute<PFR, WQ8, SM>(wr, lw.w_1, lw.s_1, d4, d, it * 8, S, m.xn, m.red, m.gout);
     if (tid < 8 * S) {
       const int s = tid >> 3, row = it * 8 + (tid & 7);
       if (row < d4) ll_st(p.hm + ((size_t)l * S + s) * d4 + row, p.gelu[f2h(m.gout[tid] + lw.b_1[row])], c.tag);
     }
+    STAMP(2);
   }
   return true;
 }
 
 // MLP2 + bias + residual.
 template <int SM, int WQ8>
-NOINL bool phase_mlp2(const StepParams& p, Lds m, StepCtx c, int l, int rot) {
+DEV bool phase_mlp2(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
   const int G = gridDim.x, tid = threadIdx.x, S = p.S, d = p.d, d4 = 4 * d;
   const LayerDev& lw = p.layers[l];
   const int nitems = (d + 7) / 8;
-  const int it0 = first_item(blockIdx.x, rot, G);
+  const int it0 = grp_first(gr);
   if (it0 >= nitems) return true;
   WRegs<PFR> wr;
+  STAMP(0);
   gemv_prefetch<PFR, WQ8>(lw.w_2, lw.s_2, d, d4, it0 * 8, wr);
   if (!ll_poll2(p.hm + (size_t)l * S * d4, S * d4, m.xin, p.x2 + (size_t)l * S * d, S * d, m.xn, c.tag, p.err))
     return false;
-  for (int it = it0; it < nitems; it += G) {
+  STAMP(1);
+  for (int it = it0; it < nitems; it += gr.size) {
     if (it != it0) gemv_prefetch<PFR, WQ8>(lw.w_2, lw.s_2, d, d4, it * 8, wr);
     gemv_compute<PFR, WQ8, SM>(wr, lw.w_2, lw.s_2, d, d4, it * 8, S, m.xin, m.red, m.gout);
     if (tid < 8 * S) {
       const int s = tid >> 3, row = it * 8 + (tid & 7);
       if (row < d) ll_st(p.x3 + ((size_t)l * S + s) * d + row, m.xn[s * d + row] + (m.gout[tid] + lw.b_2[row]), c.tag);
     }
+    STAMP(2);
   }
   return true;
 }
 
-// Final LN + tied-embedding logits over this workgroup's 8-row vocabulary groups, masks, and
-// the workgroup's selection partial (full record and a (max, argmax) pair).
+// Final LN + tied-embedding logits over this workgroup's 8-row vocabulary items (items g, g+G, ...,
+// taken kNB at a time with the next batch's weights in flight), masks, and the workgroup's
+// selection partial (a full record and a (max, argmax) pair).
 template <int SM, int WQ8>
-NOINL bool phase_logits(const StepParams& p, Lds m, StepCtx c) {
+DEV void logits_batch(const StepParams& p, const Lds& m, const StepCtx& c, const WBatch<2, kNB>& wb, int b,
+                      int nmine, float* lg, float* rw, int* lidx, int rpw) {
+  const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x, S = p.S, V = p.V, d = p.d;
+  const int nit = min(kNB, nmine - b * kNB);
+  gemvb_compute<2, kNB, WQ8, SM>(wb, p.emb, p.emb_s, V, d, g + b * kNB * G, G, nit, S, m.xn, m.red, m.gout);
+  for (int idx = tid; idx < nit * S * 8; idx += kThreads) {
+    const int i = idx / (S * 8), rem = idx - i * S * 8, s = rem >> 3, rr = rem & 7;
+    const int row = (g + (b * kNB + i) * G) * 8 + rr, li = (b * kNB + i) * 8 + rr;
+    if (row < V) {
+      const float v = m.gout[(i * SM + s) * 8 + rr];
+      rw[s * rpw + li] = v;
+      lg[s * rpw + li] = (masked(p.mask, p.mw, s, row) || masked(p.mask2, p.mw, s, row)) ? -INFINITY : v;
+      if (s == 0) lidx[li] = row;
+      if (p.logits_out) p.logits_out[((size_t)c.st * S + s) * V + row] = v;
+    } else if (s == 0) {
+      lidx[li] = -1;
+    }
+  }
+}
+
+template <int SM, int WQ8>
+DEV bool phase_logits(const StepParams& p, const Lds& m, const StepCtx& c) {
   const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x, S = p.S, d = p.d, V = p.V;
   const int nitems = (V + 7) / 8;
+  const int nmine = g < nitems ? (nitems - g + G - 1) / G : 0;
+  const int nb = (nmine + kNB - 1) / kNB;
   const int rpw = p.rows_per_wg;
   float* lg = m.big;                                  // [S][rpw] masked
   float* rw = lg + S * rpw;                           // [S][rpw] raw
   int* lidx = reinterpret_cast<int*>(rw + S * rpw);   // [rpw]
   float* rec = reinterpret_cast<float*>(lidx + rpw);  // [S][kSelWords]
-  WRegs<PFL> wa, wb;
-  if (g < nitems) gemv_prefetch<PFL, WQ8>(p.emb, p.emb_s, V, d, g * 8, wa);
+  WBatch<2, kNB> wa, wb;
+  STAMP(0);
+  if (nb > 0) gemvb_prefetch<2, kNB, WQ8>(p.emb, p.emb_s, V, d, g, G, min(kNB, nmine), wa);
   if (!ll_poll1(p.x3 + (size_t)(p.L - 1) * S * d, S * d, m.xin, c.tag, p.err)) return false;
+  STAMP(1);
   wg_layernorm(m.xin, m.xn, S, d, p.lnf_g, p.lnf_b, m.scr);
-  int nl = 0;
-  for (int it = g; it < nitems; it += G) {
-    const int nx = it + G;
-    if (nx < nitems) gemv_prefetch<PFL, WQ8>(p.emb, p.emb_s, V, d, nx * 8, wb);
-    gemv_compute<PFL, WQ8, SM>(wa, p.emb, p.emb_s, V, d, it * 8, S, m.xn, m.red, m.gout);
-    if (tid < 8 * S) {
-      const int s = tid >> 3, rr = tid & 7, row = it * 8 + rr, li = nl + rr;
-      if (row < V) {
-        const float v = m.gout[tid];
-        rw[s * rpw + li] = v;
-        lg[s * rpw + li] = (masked(p.mask, p.mw, s, row) || masked(p.mask2, p.mw, s, row)) ? -INFINITY : v;
-        if (s == 0) lidx[li] = row;
-        if (p.logits_out) p.logits_out[((size_t)c.st * S + s) * V + row] = v;
-      }
+  for (int b = 0; b < nb; b += 2) {
+    if (b + 1 < nb) gemvb_prefetch<2, kNB, WQ8>(p.emb, p.emb_s, V, d, g + (b + 1) * kNB * G, G, min(kNB, nmine - (b + 1) * kNB), wb);
+    logits_batch<SM, WQ8>(p, m, c, wa, b, nmine, lg, rw, lidx, rpw);
+    if (b + 1 < nb) {
+      if (b + 2 < nb) gemvb_prefetch<2, kNB, WQ8>(p.emb, p.emb_s, V, d, g + (b + 2) * kNB * G, G, min(kNB, nmine - (b + 2) * kNB), wa);
+      logits_batch<SM, WQ8>(p, m, c, wb, b + 1, nmine, lg, rw, lidx, rpw);
     }
-    nl += min(8, V - it * 8);
-    wa = wb;
   }
   __syncthreads();
+  STAMP(2);
+  // compact: rows beyond V (only in the last item) carry lidx -1 and sit at the end
+  int nl = nmine * 8;
+  if (nmine > 0) {
+    const int last_row0 = (g + (nmine - 1) * G) * 8;
+    nl = (nmine - 1) * 8 + min(8, V - last_row0);
+  }
   for (int s = tid >> 6; s < S; s += 4)
     sel_partial(lg + s * rpw, rw + s * rpw, lidx, nl, p.probe, p.topk, rec + s * kSelWords);
   __syncthreads();
@@ -943,24 +1187,38 @@ NOINL bool phase_logits(const StepParams& p, Lds m, StepCtx c) {
 // Selection reduction.  Every workgroup reduces the (max, argmax) pairs to get the next token;
 // the last workgroup also merges the full partials (blocks of kRedBlock workgroups) into the
 // step outputs.
-NOINL bool phase_reduce(const StepParams& p, Lds m, StepCtx c) {
+DEV bool phase_reduce(const StepParams& p, const Lds& m, const StepCtx& c) {
   const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x, S = p.S;
-  float* pairs = m.big;  // [G][S][2]
-  if (!ll_poll1(p.lpa, G * S * 2, pairs, c.tag, p.err)) return false;
   const bool last_step = c.st + 1 == p.nsteps;
-  for (int s = tid >> 6; s < S; s += 4) {
-    const int am = sel_argmax(pairs + 2 * s, G, 2 * S);
-    if ((tid & 63) == 0 && !last_step)
-      m.toks[s] = p.forced ? p.forced[(size_t)c.st * S + s] : (am == 0x7fffffff ? 0 : am);
+  // Only the workgroups of the first two phases of the next step (layer 0 self-attention and
+  // out-projection, which embed the next token) need the token; the output writer needs the
+  // records.  Everyone else goes straight to its next phase, whose inputs depend on these.
+  const Grp g0 = phase_group(0, G), g1 = phase_group(1, G);
+  const int writer = phase_group(2, G).base;
+  const bool need_tok = !last_step && ((g >= g0.base && g < g0.base + g0.size) || (g >= g1.base && g < g1.base + g1.size));
+  const bool is_writer = g == writer && p.out != nullptr;
+  if (!need_tok && !is_writer) return true;
+  float* pairs = m.big;  // [G][S][2]
+  STAMP(0);
+  if (need_tok) {
+    if (!ll_poll1(p.lpa, G * S * 2, pairs, c.tag, p.err)) return false;
   }
-  __syncthreads();
-  if (g == G - 1 && p.out != nullptr) {
+  STAMP(1);
+  if (need_tok) {
+    for (int s = tid >> 6; s < S; s += 4) {
+      const int am = sel_argmax(pairs + 2 * s, G, 2 * S);
+      if ((tid & 63) == 0) m.toks[s] = p.forced ? p.forced[(size_t)c.st * S + s] : (am == 0x7fffffff ? 0 : am);
+    }
+    __syncthreads();
+  }
+  if (is_writer) {
     const int nblk = (G + kRedBlock - 1) / kRedBlock;
     float* blk = m.big;                                     // [kRedBlock][S][kSelWords]
     float* brec = blk + (size_t)kRedBlock * S * kSelWords;  // [nblk][S][kSelWords]
     for (int b = 0; b < nblk; ++b) {
-      const int g0 = b * kRedBlock, ng = min(kRedBlock, G - g0);
-      if (!ll_poll1(p.lp + (size_t)g0 * S * kSelWords, ng * S * kSelWords, blk, c.tag, p.err)) return false;
+      const int gb = b * kRedBlock, ng = min(kRedBlock, G - gb);
+      if (!ll_wait_sparse(p.lp + (size_t)gb * S * kSelWords, ng, S * kSelWords, S * kSelWords - 1, -1, c.tag, p.err)) return false;
+      if (!ll_poll1(p.lp + (size_t)gb * S * kSelWords, ng * S * kSelWords, blk, c.tag, p.err)) return false;
       for (int s = tid >> 6; s < S; s += 4)
         sel_merge(blk + s * kSelWords, ng, S * kSelWords, p.topk, brec + ((size_t)b * S + s) * kSelWords);
       __syncthreads();
@@ -982,40 +1240,49 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
   m.xin = lds_raw;
   m.xn = m.xin + S * 4 * d;
   m.red = m.xn + S * d;
-  m.gout = m.red + 32 * SM;
-  m.scr = m.gout + 8 * SM;
+  m.gout = m.red + kNB * 32 * SM;
+  m.scr = m.gout + kNB * SM * 8;
   m.toks = reinterpret_cast<int*>(m.scr + 8);
   m.big = m.scr + 8 + kMaxRows;
   if (tid < S) m.toks[tid] = p.tokens0[tid];
   __syncthreads();
+  const int nph = 6 * p.L + 2;
   for (int st = 0; st < p.nsteps; ++st) {
     StepCtx c;
     c.tag = p.tag0 + (uint32_t)st;
     c.st = st;
-    c.kv = p.kv_len0 + st;                         // keys already cached; this token is key c.kv
-    c.pe = c.kv < p.C - 1 ? c.kv : p.C - 1;        // positional row (clamped as the reference)
-    c.ncs = (c.kv + 1 + kSelfChunk - 1) / kSelfChunk;
-    int rot = 0;
+    c.kv = p.kv_len0 + st;                   // keys already cached; this token is key c.kv
+    c.pe = c.kv < p.C - 1 ? c.kv : p.C - 1;  // positional row (clamped as the reference)
+    c.nph = nph;
+    c.ph = 0;
+    const int G = gridDim.x;
     for (int l = 0; l < p.L; ++l) {
-      if (!phase_qkv<SM, WQ8>(p, m, c, l, rot)) return;
-      rot += 37;
-      if (!phase_self_attn(p, m, c, l, rot)) return;
-      rot += 37;
-      if (!phase_out<SM, WQ8>(p, m, c, l, rot, false)) return;
-      rot += 37;
-      if (!phase_cq<SM, WQ8>(p, m, c, l, rot)) return;
-      rot += 37;
-      if (!phase_cross_attn<SM>(p, m, c, l, rot)) return;
-      rot += 37;
-      if (!phase_out<SM, WQ8>(p, m, c, l, rot, true)) return;
-      rot += 37;
-      if (!phase_mlp1<SM, WQ8>(p, m, c, l, rot)) return;
-      rot += 37;
-      if (!phase_mlp2<SM, WQ8>(p, m, c, l, rot)) return;
-      rot += 37;
+      const int q = 6 * l;
+      if (!phase_self<SM, WQ8>(p, m, c, l, phase_group(q, G))) return;
+      STAMP(3);
+      ++c.ph;
+      if (!phase_out<SM, WQ8>(p, m, c, l, phase_group(q + 1, G), false)) return;
+      STAMP(3);
+      ++c.ph;
+      if (!phase_cross<SM, WQ8>(p, m, c, l, phase_group(q + 2, G))) return;
+      STAMP(3);
+      ++c.ph;
+      if (!phase_out<SM, WQ8>(p, m, c, l, phase_group(q + 3, G), true)) return;
+      STAMP(3);
+      ++c.ph;
+      if (!phase_mlp1<SM, WQ8>(p, m, c, l, phase_group(q + 4, G))) return;
+      STAMP(3);
+      ++c.ph;
+      if (!phase_mlp2<SM, WQ8>(p, m, c, l, phase_group(q + 5, G))) return;
+      STAMP(3);
+      ++c.ph;
     }
     if (!phase_logits<SM, WQ8>(p, m, c)) return;
+    STAMP(3);
+    ++c.ph;
     if (!phase_reduce(p, m, c)) return;
+    STAMP(3);
+    ++c.ph;
   }
 }
 
@@ -1137,8 +1404,8 @@ __global__ void __launch_bounds__(kThreads) k_op_attention(const float* q, const
   float* plv = pmv + 8;
   float* acc = plv + 8;                     // [64]
   float* sc = acc + kHeadDim;               // [kSelfChunk + 4]
-  float* red = sc + kSelfChunk + 4;         // [4][1][64]
-  float* part = red + 4 * kHeadDim;         // [nc][kPartWords]
+  float* red = sc + kSelfChunk + 4;         // [16][1][64]
+  float* part = red + 16 * kHeadDim;        // [nc][kPartWords]
   for (int i = threadIdx.x; i < kHeadDim; i += kThreads) qs[i] = q[h * kHeadDim + i];
   __syncthreads();
   const uint16_t* kb = k + (size_t)h * kv_len * kHeadDim;
@@ -1147,7 +1414,7 @@ __global__ void __launch_bounds__(kThreads) k_op_attention(const float* q, const
     const int k0 = c * kSelfChunk, n = min(kSelfChunk, kv_len - k0);
     auto off = [&](int j) -> size_t { return (size_t)(k0 + j) * kHeadDim; };
     KVRegs<KPT_SELF> kr;
-    attn_prefetch<KPT_SELF>(kb, vb, off, n, kr);
+    attn_prefetch<KPT_SELF, 0>(kb, vb, (size_t)kv_len * kHeadDim * 2, off, n, kr);
     attn_compute<KPT_SELF, 1>(kr, n, 1, qs, nullptr, nullptr, scale, sc, kSelfChunk + 4, red, pmv, plv, acc);
     for (int i = threadIdx.x; i < kPartWords; i += kThreads)
       part[c * kPartWords + i] = i == 0 ? pmv[0] : (i == 1 ? plv[0] : acc[i - 2]);
@@ -1199,9 +1466,9 @@ __global__ void __launch_bounds__(64) k_op_select_final(const float* parts, int 
 
 size_t step_lds_bytes(const StepParams& p, int grid) {
   const int S = p.S, d = p.d, SM = S > 1 ? kMaxRows : 1;
-  size_t fixed = (size_t)S * 4 * d + (size_t)S * d + 32 * SM + 8 * SM + 8 + kMaxRows;
-  const size_t self_attn = 3 * kHeadDim + 16 + kHeadDim + kSelfChunk + 4 + 4 * kHeadDim;
-  const size_t cross_attn = SM * kHeadDim + 16 + SM * kHeadDim + 4 * SM * kHeadDim + (size_t)SM * (kMaxChunk + 4);
+  const size_t fixed = (size_t)S * 4 * d + (size_t)S * d + kNB * 32 * SM + kNB * SM * 8 + 8 + kMaxRows;
+  const size_t self_attn = 2 * kHeadDim + 16 + kHeadDim + kSelfChunk + 4 + 16 * kHeadDim;
+  const size_t cross_attn = SM * kHeadDim + 16 + SM * kHeadDim + 16 * SM * kHeadDim + (size_t)SM * (kMaxChunk + 4);
   const size_t merge_self = (size_t)p.ncs_max * S * p.H * kPartWords;
   const size_t merge_cross = (size_t)p.ncc * S * p.H * kPartWords;
   const size_t logits = (size_t)2 * S * p.rows_per_wg + p.rows_per_wg + (size_t)S * kSelWords;
@@ -1303,7 +1570,7 @@ hipError_t launch_op_gelu(const float* x, int n, const float* table, float* y, h
 hipError_t launch_op_attention(const float* q, const uint16_t* k, const uint16_t* v, int nh, int kv_len, float scale,
                                float* out, hipStream_t st) {
   const int nc = (kv_len + kSelfChunk - 1) / kSelfChunk;
-  size_t lds = ((size_t)kHeadDim + 16 + kHeadDim + kSelfChunk + 4 + 4 * kHeadDim + (size_t)nc * kPartWords) * sizeof(float);
+  size_t lds = ((size_t)kHeadDim + 16 + kHeadDim + kSelfChunk + 4 + 16 * kHeadDim + (size_t)nc * kPartWords) * sizeof(float);
   hipError_t e = hipFuncSetAttribute((const void*)k_op_attention, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_op_attention, dim3(nh), dim3(kThreads), lds, st, q, k, v, kv_len, scale, out);

@@ -44,7 +44,7 @@ struct StepParams {
   const uint16_t *xk, *xv;      // [X][L][H][A][64]
   const int32_t* slots;         // [S][max_ctx] or null (row r reads its own slot)
   u64 *qkv, *sp, *x1, *cq, *cp, *x2, *hm, *x3, *lp, *lpa;  // tagged exchange buffers
-  int ncs_max, ncc, chc;        // self chunk capacity, cross chunk count, cross chunk length
+  int ncs_max, ncc, chc;        // self partial slots (cached chunks + current key), cross chunks, cross chunk length
   // control
   int nsteps, kv_len0;
   uint32_t tag0;
@@ -57,6 +57,7 @@ struct StepParams {
   float* logits_out;            // [nsteps][S][V] or null
   unsigned* err;
   int rows_per_wg;              // vocab rows one workgroup keeps in LDS in the logits phase
+  unsigned long long* trace;    // [nsteps][6L+2][grid] phase-end timestamps (wall clock) or null
 };
 
 // Launchers (return the HIP error of the launch).

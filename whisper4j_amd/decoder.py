@@ -183,6 +183,27 @@ class Session:
         return ms, [[StepResult._from(out[i * self.n_rows + r], 0) for r in range(self.n_rows)] for i in range(n_steps)]
 
 
+def _phase_names(L):
+    per = ["self_attn", "self_out", "cross_attn", "cross_out", "mlp1", "mlp2"]
+    return [f"l{l}.{p}" for l in range(L) for p in per] + ["logits", "select"]
+
+
+def trace_run(session: "Session", tokens, forced, n_steps: int):
+    """Device timestamps -> (names, ticks[n_steps][n_phases][4][n_workgroups]); points per phase:
+    0 entered, 1 inputs arrived, 2 computed, 3 left (0 where the workgroup had no work)."""
+    t = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
+    f = np.ascontiguousarray(forced, dtype=np.int32).reshape(-1) if forced is not None else None
+    L = session.model.dims.n_text_layer
+    nph = 6 * L + 2
+    g = ctypes.c_int32()
+    n = n_steps * nph * 4 * 1024
+    buf = np.zeros(n, np.uint64)
+    check(lib().w4h_session_trace_run(session._h, _ptr(t, _i32p), _ptr(f, _i32p), n_steps,
+                                      buf.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)), n, ctypes.byref(g)))
+    G = g.value
+    return _phase_names(L), buf[: n_steps * nph * 4 * G].reshape(n_steps, nph, 4, G)
+
+
 class WhisperDecoder:
     """Mirror of com.sparrowlogic.whisper4j.nn.WhisperDecoder running on the device."""
 
