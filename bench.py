@@ -54,20 +54,78 @@ def read_traffic():
     return None
 
 
-def cpu_baseline(dims, T, xa, prompt, forced, n_steps):
+def cpu_baseline(dims, T, xa, prompt, forced, min_seconds, max_sweeps):
     """The oracle (single-threaded C restatement of the reference's Linux decode path) on a bounded
-    sample of the same workload: prefill untimed, then n_steps teacher-forced steps."""
+    sample of the same workload: whole 444-step teacher-forced sweeps, each after an untimed 4-token
+    prefill into a fresh cache, repeated until min_seconds of timed CPU work (at most max_sweeps)."""
     from oracle import oracle as orc
 
     m = orc.Model(dims, T)
-    c = m.new_cache()
-    m.forward(prompt, xa, c)
-    t0 = time.perf_counter()
-    for i in range(n_steps):
-        m.forward([int(forced[i])], xa, c)
-    dt = time.perf_counter() - t0
+    dt, sweeps = 0.0, 0
+    while sweeps < max_sweeps and (sweeps == 0 or dt < min_seconds):
+        c = m.new_cache()
+        m.forward(prompt, xa, c)
+        t0 = time.perf_counter()
+        for i in range(N_STEPS):
+            m.forward([int(forced[i])], xa, c)
+        dt += time.perf_counter() - t0
+        c.close()
+        sweeps += 1
     m.close()
-    return n_steps / dt, dt
+    return N_STEPS * sweeps / dt, dt, sweeps
+
+
+def copy_calibration(mib):
+    """A plain device-to-device copy of `mib` MiB (reads mib, writes mib), run three times so that a
+    counter pass over this process sees a kernel of known traffic beside the decoder kernel."""
+    import torch
+
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def traffic_from(fetch_csv, write_csv, copy_mib, out_path):
+    """Reduce two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE pass, WRITE_SIZE pass; both
+    in KiB per dispatch) to HBM bytes per sweep launch of the decoder kernel.  The copy kernel of the
+    same process (copy_mib read + copy_mib written) calibrates each counter: factor = known bytes /
+    counted bytes."""
+    import csv
+
+    def per_kernel(path, counter):
+        rows = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] != counter:
+                continue
+            key = (r["Kernel_Name"], r["Dispatch_Id"])
+            rows[key] = rows.get(key, 0.0) + float(r["Counter_Value"])
+        return rows
+
+    res = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = per_kernel(path, counter)
+        step = [v for (k, _), v in rows.items() if "k_step" in k]
+        copy = [v for (k, _), v in rows.items() if "copy" in k.lower() or "elementwise" in k.lower()]
+        if not step or not copy:
+            raise SystemExit(f"{path}: no decoder or copy dispatch with {counter}")
+        counted_copy = max(copy) * 1024.0
+        factor = (copy_mib << 20) / counted_copy
+        counted_step = max(step) * 1024.0  # the sweep launch is the largest decoder dispatch
+        res[counter] = (counted_step, counted_copy, factor)
+    fetch = res["FETCH_SIZE"][0] * res["FETCH_SIZE"][2]
+    write = res["WRITE_SIZE"][0] * res["WRITE_SIZE"][2]
+    with open(out_path, "w") as f:
+        for counter, (cs, cc, fac) in res.items():
+            f.write(f"{counter}: decoder sweep dispatch {cs:.6e} B counted; copy of {copy_mib} MiB counted "
+                    f"{cc:.6e} B -> factor {fac:.4f}\n")
+        f.write(f"fetch_bytes_per_launch: {fetch:.6e}\n")
+        f.write(f"write_bytes_per_launch: {write:.6e}\n")
+        f.write(f"traffic_bytes_per_launch: {fetch + write:.6e}\n")
+    print(open(out_path).read())
 
 
 def main():
@@ -75,9 +133,17 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10, help="timed 444-token decode sweeps")
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--cpu-steps", type=int, default=60, help="oracle steps timed for the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum timed oracle work for the CPU baseline")
+    ap.add_argument("--cpu-max-sweeps", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="also run a plain copy of this many MiB (counter calibration for rocprofv3 --pmc)")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="reduce two --pmc counter CSVs to the traffic file and exit (no GPU work)")
     args = ap.parse_args()
+    if args.traffic_from:
+        traffic_from(args.traffic_from[0], args.traffic_from[1], args.copy_mib or 256, TRAFFIC_FILE)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); this build has no multi-GPU path.",
               file=sys.stderr)
@@ -107,6 +173,8 @@ def main():
     wall = time.perf_counter() - t0
     sess.close()
     model.close()
+    if args.copy_mib:
+        copy_calibration(args.copy_mib)
 
     ms_mean = float(np.mean(ms))
     tok_s = N_STEPS * args.steps / wall
@@ -116,10 +184,11 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cps, dt = cpu_baseline(dims, T, xa, prompt, forced, args.cpu_steps)
+        cps, dt, sweeps = cpu_baseline(dims, T, xa, prompt, forced, args.cpu_seconds, args.cpu_max_sweeps)
         cpu = {"value": round(cps, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
-               "sample": f"base.en decoder, {args.cpu_steps} teacher-forced steps at positions 4..{3 + args.cpu_steps} "
-                         f"after an untimed 4-token prefill, one thread ({dt:.1f} s)"}
+               "sample": f"the same base.en workload on the oracle: {sweeps} whole {N_STEPS}-step teacher-forced "
+                         f"sweeps (positions 4..447, each after an untimed 4-token prefill), one thread, "
+                         f"{dt:.1f} s timed"}
 
     line = {
         "metric": METRIC,
