@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -84,18 +85,6 @@ uint16_t float_to_half(float f) {
   return (uint16_t)(sign | q);
 }
 
-// GELU table indexed by f16 bits: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) evaluated in
-// float with the tanh taken in double and rounded, as main/tensor/Tensor.java:493-501 builds it.
-#pragma clang fp contract(off)
-void build_gelu_table(float* t) {
-  const float s = (float)std::sqrt(2.0 / 3.14159265358979323846);
-  for (int i = 0; i < 65536; i++) {
-    const float x = half_to_float((uint16_t)i);
-    const float inner = s * (x + 0.044715f * x * x * x);
-    t[i] = 0.5f * x * (1.0f + (float)std::tanh((double)inner));
-  }
-}
-#pragma clang fp contract(on)
 
 // ---------------------------------------------------------------------------------------------
 // device memory
@@ -148,7 +137,7 @@ struct w4h_model {
   DevBuf layers_dev;
   const void* emb = nullptr;
   const uint16_t* emb_s = nullptr;
-  const float *pos = nullptr, *lnf_g = nullptr, *lnf_b = nullptr, *gelu = nullptr;
+  const float *pos = nullptr, *lnf_g = nullptr, *lnf_b = nullptr;
   std::atomic<int> refs{1};
   std::atomic<bool> closed{false};
 };
@@ -331,11 +320,6 @@ int build_model(w4h_model* m, const w4h_dims* dims, const w4h_tensor* tensors, i
     if ((rc = load_vec(m, tt, b + "mlp_ln.bias", d, &ld.ln3_b))) return rc;
   }
   if ((rc = upload(m->layers_dev, m->layers.data(), sizeof(LayerDev) * L))) return rc;
-  std::vector<float> table(65536);
-  build_gelu_table(table.data());
-  DevBuf* gb = new_buf(m);
-  if ((rc = upload(*gb, table.data(), table.size() * 4))) return rc;
-  m->gelu = gb->as<float>();
   return W4H_OK;
 }
 
@@ -412,7 +396,7 @@ int w4h_model_destroy(w4h_model* m) {
 
 struct w4h_session {
   w4h_model* m = nullptr;
-  int S = 1, X = 1, max_ctx = 0, grid = 0, ncs_max = 0, ncc = 0, chc = 0, rpw = 0, mw = 0;
+  int S = 1, X = 1, max_ctx = 0, grid = 0, ngroups = 2, ncs_max = 0, ncc = 0, chc = 0, rpw = 0, mw = 0;
   size_t lds = 0;
   hipStream_t stream = nullptr;
   DevBuf kvk, kvv, xk, xv, slots, ll, err, out, toks, forced, mask, mask2, logits, xa_tmp, trace;
@@ -445,7 +429,6 @@ static StepParams base_params(w4h_session* s) {
   p.pos = m->pos;
   p.lnf_g = m->lnf_g;
   p.lnf_b = m->lnf_b;
-  p.gelu = m->gelu;
   p.S = s->S;
   p.X = s->X;
   p.max_ctx = s->max_ctx;
@@ -472,6 +455,7 @@ static StepParams base_params(w4h_session* s) {
   p.probe = s->probe;
   p.err = s->err.as<unsigned>();
   p.rows_per_wg = s->rpw;
+  p.ngroups = s->ngroups;
   return p;
 }
 
@@ -584,6 +568,16 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   hipDeviceProp_t prop;
   HIPCHK(hipGetDeviceProperties(&prop, m->device));
   s->grid = prop.multiProcessorCount;
+  // Phase groups (phase q runs on workgroup group q % ngroups, 1 or 2); W4H_NGROUPS overrides the
+  // default of 2 for tuning.  A workgroup owns at most kResItems of the d/8 residual-row items.
+  if (const char* e = getenv("W4H_NGROUPS")) {
+    const int v = atoi(e);
+    if (v == 1 || v == 2) s->ngroups = v;
+  }
+  if (s->grid < 2 * s->ngroups) s->ngroups = 1;
+  if ((d / 8 + s->grid / s->ngroups - 1) / (s->grid / s->ngroups) > kResItems) s->ngroups = 1;
+  if ((d / 8 + s->grid - 1) / s->grid > kResItems)
+    return fail(W4H_ERR_INVALID, "n_text_state %d needs more than %d compute units", d, d / (8 * kResItems));
   s->rpw = (((V + 7) / 8 + s->grid - 1) / s->grid) * 8;
   StepParams probe_p{};
   probe_p.S = s->S;
@@ -815,12 +809,9 @@ int w4h_op_gelu(const float* x, int32_t n, float* y) {
   if (!x || !y || n <= 0) return fail(W4H_ERR_INVALID, "bad argument");
   int rc = op_prepare();
   if (rc) return rc;
-  std::vector<float> table(65536);
-  build_gelu_table(table.data());
-  DevBuf dt, dx, dy;
-  if ((rc = upload(dt, table.data(), table.size() * 4)) || (rc = upload(dx, x, (size_t)n * 4)) || (rc = dy.alloc((size_t)n * 4)))
-    return rc;
-  HIPCHK(launch_op_gelu(dx.as<float>(), n, dt.as<float>(), dy.as<float>(), nullptr));
+  DevBuf dx, dy;
+  if ((rc = upload(dx, x, (size_t)n * 4)) || (rc = dy.alloc((size_t)n * 4))) return rc;
+  HIPCHK(launch_op_gelu(dx.as<float>(), n, dy.as<float>(), nullptr));
   HIPCHK(hipMemcpy(y, dy.p, (size_t)n * 4, hipMemcpyDeviceToHost));
   return W4H_OK;
 }

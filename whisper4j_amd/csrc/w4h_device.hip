@@ -28,7 +28,7 @@ constexpr unsigned kSpinLimit = 1u << 20;  // polls before a wait is declared ex
 constexpr int PFR = 8;  // 16-byte weight chunks per lane kept in registers (prefetched) per item
 constexpr int KPT_SELF = kSelfChunk / 32;   // keys per thread, self-attention chunk
 constexpr int KPT_CROSS = kMaxChunk / 32;   // keys per thread, cross-attention chunk
-constexpr int kPollBatch = 8;  // tagged words each thread loads before checking tags
+constexpr int kPollBatch = 8;   // tagged words a polling lane keeps in flight (sparse waits)
 constexpr int kRedBlock = 64;   // selection partials merged per block by the output workgroup
 
 // ------------------------------------------------------------------------------------------------
@@ -126,12 +126,34 @@ DEV void wave_argmax(float& v, int& i) {
   }
 }
 
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations (lgkmcnt), not for
+// its global loads and stores, so weight and key/value prefetches stay in flight across it.  No
+// phase needs global memory written by one wave to be read by another wave of the same workgroup
+// (workgroups exchange data only through tagged words), so every barrier in the step is this one.
+DEV void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// OR of `pred` over the workgroup through LDS (LDS-only barriers); the second barrier keeps the
+// vote words from being rewritten by a later call before every wave has read them.
+DEV bool wg_any(bool pred) {
+  __shared__ int votes[4];
+  const bool any = __any(pred);
+  if ((threadIdx.x & 63) == 0) votes[threadIdx.x >> 6] = any ? 1 : 0;
+  lds_barrier();
+  const bool r = (votes[0] | votes[1] | votes[2] | votes[3]) != 0;
+  lds_barrier();
+  return r;
+}
+
 // Sum over the workgroup; every thread receives the result.  scratch: 4 floats of LDS.
 DEV float wg_sum(float v, float* scratch) {
   v = wave_sum(v);
-  __syncthreads();
+  lds_barrier();
   if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-  __syncthreads();
+  lds_barrier();
   return scratch[0] + scratch[1] + scratch[2] + scratch[3];
 }
 
@@ -139,16 +161,18 @@ DEV float wg_sum(float v, float* scratch) {
 // tagged-word polling
 
 // Poll words [0, n0) of src0 and [0, n1) of src1 until every word carries `tag`, then copy the
-// values into dst0 / dst1 (LDS).  Returns false (uniformly across the workgroup) when the wait
-// expired or another workgroup aborted.
+// values into dst0 / dst1 (LDS).  Each thread keeps PB words in flight per round (a round covers
+// PB * kThreads words).  Returns false (uniformly across the workgroup) when the wait expired or
+// another workgroup aborted.
+template <int PB>
 DEV bool ll_poll2(const u64* src0, int n0, float* dst0, const u64* src1, int n1, float* dst1, uint32_t tag,
                   unsigned* err) {
   const int total = n0 + n1;
   bool fail = false;
-  for (int base = 0; base < total && !fail; base += kThreads * kPollBatch) {
-    u64 v[kPollBatch];
+  for (int base = 0; base < total && !fail; base += kThreads * PB) {
+    u64 v[PB];
 #pragma unroll
-    for (int u = 0; u < kPollBatch; ++u) {
+    for (int u = 0; u < PB; ++u) {
       const int i = base + u * kThreads + (int)threadIdx.x;
       v[u] = i < n0 ? ll_ld(src0 + i) : (i < total ? ll_ld(src1 + (i - n0)) : ((u64)tag << 32));
     }
@@ -156,7 +180,7 @@ DEV bool ll_poll2(const u64* src0, int n0, float* dst0, const u64* src1, int n1,
     while (true) {
       bool ok = true;
 #pragma unroll
-      for (int u = 0; u < kPollBatch; ++u)
+      for (int u = 0; u < PB; ++u)
         if ((uint32_t)(v[u] >> 32) != tag) {
           const int i = base + u * kThreads + (int)threadIdx.x;
           ok = false;
@@ -177,7 +201,7 @@ DEV bool ll_poll2(const u64* src0, int n0, float* dst0, const u64* src1, int n1,
     }
     if (!fail) {
 #pragma unroll
-      for (int u = 0; u < kPollBatch; ++u) {
+      for (int u = 0; u < PB; ++u) {
         const int i = base + u * kThreads + (int)threadIdx.x;
         if (i < n0)
           dst0[i] = __uint_as_float((uint32_t)v[u]);
@@ -186,11 +210,12 @@ DEV bool ll_poll2(const u64* src0, int n0, float* dst0, const u64* src1, int n1,
       }
     }
   }
-  return !__syncthreads_or(fail);
+  return !wg_any(fail);
 }
 
+template <int PB>
 DEV bool ll_poll1(const u64* src, int n, float* dst, uint32_t tag, unsigned* err) {
-  return ll_poll2(src, n, dst, nullptr, 0, nullptr, tag, err);
+  return ll_poll2<PB>(src, n, dst, nullptr, 0, nullptr, tag, err);
 }
 
 // Cheap readiness wait before a full read: one wave polls the words k*stride + off1 (and + off2
@@ -230,7 +255,7 @@ DEV bool ll_wait_sparse(const u64* src, int nrec, int stride, int off1, int off2
       }
     }
   }
-  return !__syncthreads_or(fail);
+  return !wg_any(fail);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -389,12 +414,12 @@ DEV void gemv_compute(const WRegs<R>& wr, const void* W, const uint16_t* Ws, int
     for (int s = 0; s < SM; ++s)
       if (s < S) red[((w << 3) + row) * SM + s] = acc[s];
   }
-  __syncthreads();
+  lds_barrier();
   if (tid < 8 * S) {
     const int s = tid >> 3, rr = tid & 7;
     out[s * 8 + rr] = (red[rr * SM + s] + red[(8 + rr) * SM + s]) + (red[(16 + rr) * SM + s] + red[(24 + rr) * SM + s]);
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // Batched GEMV: NB items of 8 rows (item i covers rows (it0 + i * istr) * 8 .. + 8, i < nit) with
@@ -474,13 +499,13 @@ DEV void gemvb_compute(const WBatch<R, NB>& wb, const void* W, const uint16_t* W
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   for (int idx = tid; idx < nit * S * 8; idx += kThreads) {
     const int i = idx / (S * 8), rem = idx - i * S * 8, s = rem >> 3, rr = rem & 7;
     const float* rp = red + i * 32 * SM;
     out[(i * SM + s) * 8 + rr] = (rp[rr * SM + s] + rp[(8 + rr) * SM + s]) + (rp[(16 + rr) * SM + s] + rp[(24 + rr) * SM + s]);
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -501,7 +526,7 @@ DEV void wg_layernorm(const float* x, float* y, int S, int d, const float* g, co
     const float inv = 1.0f / sqrtf(var + 1e-5f);
     for (int i = threadIdx.x; i < d; i += kThreads) y[s * d + i] = (xs[i] - mean) * inv * g[i] + b[i];
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -565,7 +590,7 @@ DEV void attn_compute(const KVRegs<KPT>& r, int n, int ns, const float* q, const
       if (lane == 0) sc[s * scs + n] = t * scale;
     }
   }
-  __syncthreads();
+  lds_barrier();
   const int nt = n + (kx != nullptr ? 1 : 0);
   // softmax statistics, one wave per query row
   for (int s = w; s < ns; s += 4) {
@@ -584,7 +609,7 @@ DEV void attn_compute(const KVRegs<KPT>& r, int n, int ns, const float* q, const
       pl[s] = l;
     }
   }
-  __syncthreads();
+  lds_barrier();
   // AV
   float a[SM][8];
 #pragma unroll
@@ -624,7 +649,7 @@ DEV void attn_compute(const KVRegs<KPT>& r, int n, int ns, const float* q, const
 #pragma unroll
         for (int e = 0; e < 8; ++e) red[(rw * SM + s) * kHeadDim + sub * 8 + e] = a[s][e];
   }
-  __syncthreads();
+  lds_barrier();
   for (int i = tid; i < ns * kHeadDim; i += kThreads) {
     const int s = i >> 6, e = i & 63;
     float o = 0.f;
@@ -633,7 +658,7 @@ DEV void attn_compute(const KVRegs<KPT>& r, int n, int ns, const float* q, const
     if (kx != nullptr) o = fmaf(sc[s * scs + n], vx[e], o);
     acc_out[i] = o;
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // Merge attention partials: part[(c * nrow + row) * kPartWords + w] for c < nc -> o[row*64 + e].
@@ -651,7 +676,7 @@ DEV void attn_merge(const float* part, int nc, int nrow, float* o) {
     }
     o[i] = acc / Lsum;
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -829,19 +854,69 @@ struct Lds {
   float* gout;  // [kNB][SM][8]   GEMV results
   float* scr;   // [8]
   int* toks;    // [kMaxRows]     tokens of the current step
+  float* res;   // [kResItems][S][8] residual rows of this workgroup's d-row items
   float* big;   // phase scratch
 };
 
-constexpr int kNB = 8;  // items per GEMV batch (64 rows)
+constexpr int kNB = 8;        // items per GEMV batch (64 rows)
+constexpr int kVecRegs = 10;  // elements of a d-vector per thread (d <= 2560)
 
-// Workgroup group of a phase.  Consecutive phases run on disjoint quarters of the grid (phase q on
-// quarter q % 4), so a workgroup has three phases of idle time to prefetch the weights of its next
-// item, and only a quarter of the grid polls any one exchange buffer.
+// A d-vector parameter (LayerNorm gamma/beta, positional row) held in registers: thread t keeps
+// elements t + kThreads * i.  Loaded before a phase polls its inputs, so no parameter load sits
+// between the inputs' arrival and the phase's results.
+struct VecRegs {
+  float v[kVecRegs];
+};
+DEV void vec_prefetch(const float* src, int d, VecRegs& r) {
+  const auto rs = brsrc(src, (size_t)d * 4);
+#pragma unroll
+  for (int i = 0; i < kVecRegs; ++i) {
+    const int j = threadIdx.x + kThreads * i;
+    r.v[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, j < d ? j * 4 : (int)kOOB, 0, 0));
+  }
+}
+
+// LayerNorm of S rows of d (LDS in, LDS out) with gamma/beta in registers; two passes, eps 1e-5.
+DEV void wg_layernorm_r(const float* x, float* y, int S, int d, const VecRegs& g, const VecRegs& b, float* scratch) {
+  for (int s = 0; s < S; ++s) {
+    const float* xs = x + s * d;
+    float xv[kVecRegs];
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < kVecRegs; ++i) {
+      const int j = threadIdx.x + kThreads * i;
+      xv[i] = j < d ? xs[j] : 0.f;
+      a += xv[i];
+    }
+    const float mean = wg_sum(a, scratch) / (float)d;
+    float v = 0.f;
+#pragma unroll
+    for (int i = 0; i < kVecRegs; ++i) {
+      const int j = threadIdx.x + kThreads * i;
+      if (j < d) {
+        const float t = xv[i] - mean;
+        v = fmaf(t, t, v);
+      }
+    }
+    const float var = wg_sum(v, scratch + 4) / (float)d;
+    const float inv = 1.0f / sqrtf(var + 1e-5f);
+#pragma unroll
+    for (int i = 0; i < kVecRegs; ++i) {
+      const int j = threadIdx.x + kThreads * i;
+      if (j < d) y[s * d + j] = (xv[i] - mean) * inv * g.v[i] + b.v[i];
+    }
+  }
+  lds_barrier();
+}
+
+// Workgroup group of a phase.  Consecutive phases run on different groups (phase q on group
+// q % ngroups), so a workgroup has ngroups - 1 phases of idle time in which the weights, key/value
+// rows and parameters of its next phase arrive, while the polling load on any one exchange buffer
+// is spread over fewer workgroups.
 struct Grp {
   int base, size;
 };
-DEV Grp phase_group(int q, int G) {
-  const int ng = G >= 64 ? 4 : 1;
+DEV Grp phase_group(int q, int G, int ng) {
   const int sz = G / ng;
   return Grp{(q % ng) * sz, sz};
 }
@@ -863,33 +938,52 @@ struct StepCtx {
       p.trace[(((size_t)c.st * c.nph + c.ph) * 4 + (sub)) * gridDim.x + blockIdx.x] = wall_clock64();         \
   } while (0)
 
-// x of layer 0 = token embedding + positional embedding (exact dequant, one rounding)
+// x of layer 0 = token embedding + positional embedding (exact dequant, one rounding); the
+// positional row was prefetched into registers.
 template <int WQ8>
-DEV void embed(const StepParams& p, const Lds& m, const StepCtx& c, float* dst) {
+DEV void embed_r(const StepParams& p, const Lds& m, const VecRegs& pe, float* dst) {
   const int d = p.d;
   for (int s = 0; s < p.S; ++s) {
     const int tk = m.toks[s];
-    for (int j = threadIdx.x; j < d; j += kThreads) {
-      float e;
-      if (!WQ8) {
-        e = h2f(static_cast<const uint16_t*>(p.emb)[(size_t)tk * d + j]);
-      } else {
-        e = (float)static_cast<const int8_t*>(p.emb)[(size_t)tk * d + j] * h2f(p.emb_s[(size_t)tk * (d >> 5) + (j >> 5)]);
+#pragma unroll
+    for (int i = 0; i < kVecRegs; ++i) {
+      const int j = threadIdx.x + kThreads * i;
+      if (j < d) {
+        float e;
+        if (!WQ8) {
+          e = h2f(static_cast<const uint16_t*>(p.emb)[(size_t)tk * d + j]);
+        } else {
+          e = (float)static_cast<const int8_t*>(p.emb)[(size_t)tk * d + j] * h2f(p.emb_s[(size_t)tk * (d >> 5) + (j >> 5)]);
+        }
+        dst[s * d + j] = e + pe.v[i];
       }
-      dst[s * d + j] = e + p.pos[(size_t)c.pe * d + j];
     }
   }
-  __syncthreads();
+  lds_barrier();
 }
 
-// Layer input x: the embedding at layer 0, else the previous layer's output.
-template <int WQ8>
-DEV bool layer_input(const StepParams& p, const Lds& m, const StepCtx& c, int l, float* dst) {
-  if (l == 0) {
-    embed<WQ8>(p, m, c, dst);
-    return true;
+// GELU of the f16-rounded input, as the reference's 65 536-entry table defines it
+// (main/tensor/Tensor.java:493-501, 524-538): x = f32(f16(v)),
+//   y = fl(fl(0.5 x) * fl(1 + (float)tanh((double) fl(s * fl(x + fl(fl(fl(0.044715 x) x) x))))))
+// with s = (float)sqrt(2/pi), every float operation rounded on its own (contraction off) and tanh
+// taken in double.  Computed instead of looked up, so no table load waits on the GEMV result.
+DEV float gelu_f16(float v) {
+#pragma clang fp contract(off)
+  const float x = h2f(f2h(v));
+  const float s = (float)sqrt(2.0 / 3.14159265358979323846);
+  const float c = ((0.044715f * x) * x) * x;
+  const float inner = s * (x + c);
+  // tanh in double as (e^{2z} - 1) / (e^{2z} + 1) from expm1 (a few double ulps), then rounded
+  // to float: equal to the correctly rounded double tanh rounded to float on every f16 input.
+  const double z = (double)inner;
+  double t;
+  if (fabs(z) > 20.0) {
+    t = z > 0.0 ? 1.0 : -1.0;
+  } else {
+    const double e = expm1(2.0 * z);
+    t = e / (e + 2.0);
   }
-  return ll_poll1(p.x3 + (size_t)(l - 1) * p.S * p.d, p.S * p.d, dst, c.tag, p.err);
+  return (0.5f * x) * (1.0f + (float)t);
 }
 
 // Self-attention with the q/k/v projection folded in.  Per (row s, head h) the items are:
@@ -898,89 +992,133 @@ DEV bool layer_input(const StepParams& p, const Lds& m, const StepCtx& c, int l,
 //   j == nold : projects q_h and k_h, appends k_h to the cache, writes the current key's score as
 //               (m = q.k * scale, l = 1) into chunk slot nold;
 //   j == nold+1: projects v_h, appends it to the cache, writes it as acc[64] of chunk slot nold.
-// All items depend only on the layer input, so the projection costs no extra hand-over.
+// All items depend only on the layer input, so the projection costs no extra hand-over.  The
+// appended rows are read only by later steps; the logits phase drains every workgroup's stores
+// before it publishes, which orders them before any later step reads the cache.
 template <int SM, int WQ8>
 DEV bool phase_self(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
-  const int G = gridDim.x, tid = threadIdx.x, S = p.S, d = p.d, H = p.H, d3 = 3 * d;
+  const int tid = threadIdx.x, S = p.S, d = p.d, H = p.H, d3 = 3 * d;
   const LayerDev& lw = p.layers[l];
   const int nold = (c.kv + kSelfChunk - 1) / kSelfChunk;
   const int per = nold + 2;
   const int nitems = S * H * per;
-  bool have_x = false;
+  int it = grp_first(gr);
+  if (it >= nitems) return true;
   STAMP(0);
-  for (int it = grp_first(gr); it < nitems; it += gr.size) {
+  VecRegs g1, b1, pe;
+  vec_prefetch(lw.ln1_g, d, g1);
+  vec_prefetch(lw.ln1_b, d, b1);
+  if (l == 0) vec_prefetch(p.pos + (size_t)c.pe * d, d, pe);
+  const size_t kv_bytes = (size_t)p.L * S * H * p.max_ctx * kHeadDim * 2;
+  const int mc = p.max_ctx;
+  bool have_x = false;
+  // Layer input and LN1 (once per phase, before the first item's compute).
+  auto ensure_x = [&]() -> bool {
+    if (have_x) return true;
+    if (l == 0) {
+      embed_r<WQ8>(p, m, pe, m.xin);
+    } else if (!ll_poll1<8>(p.x3 + (size_t)(l - 1) * S * d, S * d, m.xin, c.tag, p.err)) {
+      return false;
+    }
+    STAMP(1);
+    wg_layernorm_r(m.xin, m.xn, S, d, g1, b1, m.scr);
+    have_x = true;
+    return true;
+  };
+  float* va = m.big;                 // [64] q (or v)
+  float* vb = va + kHeadDim;         // [64] k
+  float* pmv = vb + kHeadDim;        // [8]
+  float* plv = pmv + 8;              // [8]
+  float* acc = plv + 8;              // [64]
+  float* sc = acc + kHeadDim;        // [kSelfChunk + 4]
+  float* red = sc + kSelfChunk + 4;  // [16][64]
+  for (; it < nitems; it += gr.size) {
     const int j = it % per, sh = it / per, h = sh % H, s = sh / H;
     const int kind = j < nold ? 0 : (j == nold ? 1 : 2);
     const int rowA = (kind == 2 ? 2 * d : 0) + h * kHeadDim;  // q rows, or v rows for the value item
-    WBatch<2, kNB> wa, wb;
-    gemvb_prefetch<2, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, wa);
-    if (kind == 1) gemvb_prefetch<2, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, (d + h * kHeadDim) >> 3, 1, kNB, wb);
-    const int k0 = j * kSelfChunk;
-    const int n = kind == 0 ? min(kSelfChunk, c.kv - k0) : 0;
-    const int32_t* slots = p.slots ? p.slots + (size_t)s * p.max_ctx : nullptr;
-    const size_t lb = (size_t)l * S;
-    const int mc = p.max_ctx;
-    auto off = [=](int jj) -> size_t {
-      const int pos = k0 + jj;
-      const int slot = slots ? slots[pos] : s;
-      return (((lb + slot) * H + h) * mc + pos) * kHeadDim;
-    };
-    KVRegs<KPT_SELF> kr;
-    if (kind == 0)
-      attn_prefetch<KPT_SELF, 16>(p.kv_k, p.kv_v, (size_t)p.L * S * H * p.max_ctx * kHeadDim * 2, off, n, kr);
-    if (!have_x) {
-      if (!layer_input<WQ8>(p, m, c, l, m.xin)) return false;
-      STAMP(1);
-      wg_layernorm(m.xin, m.xn, S, d, lw.ln1_g, lw.ln1_b, m.scr);
-      have_x = true;
-    }
-    float* va = m.big;              // [64] q (or v)
-    float* vb = va + kHeadDim;      // [64] k
-    float* pmv = vb + kHeadDim;     // [8]
-    float* plv = pmv + 8;           // [8]
-    float* acc = plv + 8;           // [64]
-    float* sc = acc + kHeadDim;     // [kSelfChunk + 4]
-    float* red = sc + kSelfChunk + 4;  // [16][64]
-    gemvb_compute<2, kNB, WQ8, SM>(wa, lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, 1, m.xn + s * d, m.red, m.gout);
-    if (tid < kHeadDim) va[tid] = m.gout[((tid >> 3) * SM) * 8 + (tid & 7)] + lw.b_qkv[rowA + tid];
-    if (kind == 1) {
-      gemvb_compute<2, kNB, WQ8, SM>(wb, lw.w_qkv, lw.s_qkv, d3, d, (d + h * kHeadDim) >> 3, 1, kNB, 1, m.xn + s * d,
-                                     m.red, m.gout);
-      if (tid < kHeadDim) vb[tid] = m.gout[((tid >> 3) * SM) * 8 + (tid & 7)] + lw.b_qkv[d + h * kHeadDim + tid];
-    }
-    __syncthreads();
+    const int rowB = d + h * kHeadDim;                         // k rows
+    const float biasA = tid < kHeadDim ? lw.b_qkv[rowA + tid] : 0.f;
     u64* dst = p.sp + ((((size_t)l * p.ncs_max + (kind == 0 ? j : nold)) * S + s) * H + h) * kPartWords;
-    const size_t kvrow = ((((size_t)l * S + s) * H + h) * p.max_ctx + c.kv) * kHeadDim;
-    const size_t kv_bytes = (size_t)p.L * S * H * p.max_ctx * kHeadDim * 2;
     if (kind == 0) {
+      // cached keys: q projection + attention over this chunk
+      WBatch<2, kNB> wa;
+      gemvb_prefetch<2, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, wa);
+      const int k0 = j * kSelfChunk;
+      const int n = min(kSelfChunk, c.kv - k0);
+      const int32_t* slots = p.slots ? p.slots + (size_t)s * mc : nullptr;
+      const size_t lb = (size_t)l * S;
+      auto off = [=](int jj) -> size_t {
+        const int pos = k0 + jj;
+        const int slot = slots ? slots[pos] : s;
+        return (((lb + slot) * H + h) * mc + pos) * kHeadDim;
+      };
+      KVRegs<KPT_SELF> kr;
+      attn_prefetch<KPT_SELF, 16>(p.kv_k, p.kv_v, kv_bytes, off, n, kr);
+      if (!ensure_x()) return false;
+      gemvb_compute<2, kNB, WQ8, SM>(wa, lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, 1, m.xn + s * d, m.red, m.gout);
+      if (tid < kHeadDim) va[tid] = m.gout[((tid >> 3) * SM) * 8 + (tid & 7)] + biasA;
+      lds_barrier();
       attn_compute<KPT_SELF, 1>(kr, n, 1, va, nullptr, nullptr, 0.125f, sc, kSelfChunk + 4, red, pmv, plv, acc);
       STAMP(2);
       for (int i = tid; i < kPartWords; i += kThreads) ll_st(dst + i, i == 0 ? pmv[0] : (i == 1 ? plv[0] : acc[i - 2]), c.tag);
-    } else if (kind == 1) {
+    } else {
+      // the current token: (q, k) score and k append, or v append
+      WBatch<2, kNB> wa, wb;
+      gemvb_prefetch<2, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, wa);
+      if (kind == 1) gemvb_prefetch<2, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, rowB >> 3, 1, kNB, wb);
+      const float biasB = (kind == 1 && tid < kHeadDim) ? lw.b_qkv[rowB + tid] : 0.f;
+      if (!ensure_x()) return false;
+      gemvb_compute<2, kNB, WQ8, SM>(wa, lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, 1, m.xn + s * d, m.red, m.gout);
+      if (tid < kHeadDim) va[tid] = m.gout[((tid >> 3) * SM) * 8 + (tid & 7)] + biasA;
+      if (kind == 1) {
+        gemvb_compute<2, kNB, WQ8, SM>(wb, lw.w_qkv, lw.s_qkv, d3, d, rowB >> 3, 1, kNB, 1, m.xn + s * d, m.red, m.gout);
+        if (tid < kHeadDim) vb[tid] = m.gout[((tid >> 3) * SM) * 8 + (tid & 7)] + biasB;
+      }
+      lds_barrier();
+      STAMP(2);
+      const size_t kvrow = ((((size_t)l * S + s) * H + h) * mc + c.kv) * kHeadDim;
       if (tid < 64) {
-        kv_store(p.kv_k, kv_bytes, kvrow + tid, f2h(vb[tid]));
-        const float t = wave_sum(va[tid] * vb[tid]);
-        kv_drain();
-        if (tid == 0) {
-          ll_st(dst + 0, t * 0.125f, c.tag);
-          ll_st(dst + 1, 1.0f, c.tag);
+        if (kind == 1) {
+          const float t = wave_sum(va[tid] * vb[tid]);
+          if (tid == 0) {
+            ll_st(dst + 0, t * 0.125f, c.tag);
+            ll_st(dst + 1, 1.0f, c.tag);
+          }
+          kv_store(p.kv_k, kv_bytes, kvrow + tid, f2h(vb[tid]));
+        } else {
+          ll_st(dst + 2 + tid, va[tid], c.tag);
+          kv_store(p.kv_v, kv_bytes, kvrow + tid, f2h(va[tid]));
         }
       }
-    } else {
-      if (tid < 64) {
-        kv_store(p.kv_v, kv_bytes, kvrow + tid, f2h(va[tid]));
-        kv_drain();
-        ll_st(dst + 2 + tid, va[tid], c.tag);
-      }
     }
+    lds_barrier();
   }
   return true;
+}
+
+// Residual rows.  The out-projection, cross-out and MLP2 phases all produce d rows in 8-row
+// items, run on the same workgroup group and give item i to the same workgroup, so each workgroup
+// adds the residual to exactly the rows it produced in the previous such phase: those rows stay
+// in LDS (m.res[(item * S + s) * 8 + r]) and the residual stream is never polled.  Layer 0's
+// self block starts from the embedding of the workgroup's rows.
+template <int WQ8>
+DEV float resid_embed(const StepParams& p, const Lds& m, int s, int row, float pos) {
+  const int tk = m.toks[s], d = p.d;
+  float e;
+  if (!WQ8) {
+    e = h2f(static_cast<const uint16_t*>(p.emb)[(size_t)tk * d + row]);
+  } else {
+    e = (float)static_cast<const int8_t*>(p.emb)[(size_t)tk * d + row] * h2f(p.emb_s[(size_t)tk * (d >> 5) + (row >> 5)]);
+  }
+  return e + pos;
 }
 
 // Merge attention partials, out-projection, bias and residual:  xout = xres + (Wo . o + b).
 template <int SM, int WQ8>
 DEV bool phase_out(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr, bool cross) {
-  const int G = gridDim.x, tid = threadIdx.x, S = p.S, d = p.d, H = p.H;
+  constexpr int NBO = 1;            // items whose weights are prefetched before the poll
+  constexpr int RO = WQ8 ? 2 : 4;   // 16-byte chunks per lane and row kept in registers
+  const int tid = threadIdx.x, S = p.S, d = p.d, H = p.H;
   const LayerDev& lw = p.layers[l];
   const void* W = cross ? lw.w_co : lw.w_o;
   const uint16_t* Ws = cross ? lw.s_co : lw.s_o;
@@ -988,26 +1126,47 @@ DEV bool phase_out(const StepParams& p, const Lds& m, const StepCtx& c, int l, G
   const int nitems = (d + 7) / 8;
   const int it0 = grp_first(gr);
   if (it0 >= nitems) return true;
-  WRegs<PFR> wr;
-  gemv_prefetch<PFR, WQ8>(W, Ws, d, d, it0 * 8, wr);
+  STAMP(0);
+  const int nmine = (nitems - it0 + gr.size - 1) / gr.size;
+  WBatch<RO, NBO> wr;
+  gemvb_prefetch<RO, NBO, WQ8>(W, Ws, d, d, it0, gr.size, min(NBO, nmine), wr);
+  // the output this thread publishes in batch b: item b + tid / (S * 8), row s, row-in-item rr
+  auto row_of = [&](int b) -> int { return (it0 + (b + tid / (S * 8)) * gr.size) * 8 + (tid & 7); };
+  auto bias_of = [&](int b) -> float {
+    const int nit = min(NBO, nmine - b), row = row_of(b);
+    return (tid < nit * S * 8 && row < d) ? bias[row] : 0.f;
+  };
+  const bool emb_res = !cross && l == 0;
+  auto pos_of = [&](int b) -> float {
+    const int nit = min(NBO, nmine - b), row = row_of(b);
+    return (emb_res && tid < nit * S * 8 && row < d) ? p.pos[(size_t)c.pe * d + row] : 0.f;
+  };
+  float bv = bias_of(0), pv = pos_of(0);
   float* part = m.big;
   const int nc = cross ? p.ncc : (c.kv + kSelfChunk - 1) / kSelfChunk + 1;
   const u64* psrc = cross ? p.cp + (size_t)l * p.ncc * S * H * kPartWords : p.sp + (size_t)l * p.ncs_max * S * H * kPartWords;
-  // residual: x1 for the cross block, the layer input for the self block (layer 0: embedding)
-  const u64* rsrc = cross ? p.x1 + (size_t)l * S * d : p.x3 + (size_t)(l > 0 ? l - 1 : 0) * S * d;
-  const int rn = (cross || l > 0) ? S * d : 0;
-  STAMP(0);
-  if (!ll_poll2(psrc, nc * S * H * kPartWords, part, rsrc, rn, m.xin, c.tag, p.err)) return false;
+  if (!ll_poll1<16>(psrc, nc * S * H * kPartWords, part, c.tag, p.err)) return false;
   STAMP(1);
-  if (rn == 0) embed<WQ8>(p, m, c, m.xin);
   attn_merge(part, nc, S * H, m.xn);
   u64* xout = (cross ? p.x2 : p.x1) + (size_t)l * S * d;
-  for (int it = it0; it < nitems; it += gr.size) {
-    if (it != it0) gemv_prefetch<PFR, WQ8>(W, Ws, d, d, it * 8, wr);
-    gemv_compute<PFR, WQ8, SM>(wr, W, Ws, d, d, it * 8, S, m.xn, m.red, m.gout);
-    if (tid < 8 * S) {
-      const int s = tid >> 3, row = it * 8 + (tid & 7);
-      if (row < d) ll_st(xout + (size_t)s * d + row, m.xin[s * d + row] + (m.gout[tid] + bias[row]), c.tag);
+  for (int b = 0; b < nmine; b += NBO) {
+    const int nit = min(NBO, nmine - b);
+    if (b > 0) {
+      gemvb_prefetch<RO, NBO, WQ8>(W, Ws, d, d, it0 + b * gr.size, gr.size, nit, wr);
+      bv = bias_of(b);
+      pv = pos_of(b);
+    }
+    gemvb_compute<RO, NBO, WQ8, SM>(wr, W, Ws, d, d, it0 + b * gr.size, gr.size, nit, S, m.xn, m.red, m.gout);
+    if (tid < nit * S * 8) {
+      const int i = tid / (S * 8), rem = tid - i * S * 8, s = rem >> 3, rr = rem & 7;
+      const int row = row_of(b);
+      if (row < d) {
+        float* rs = m.res + ((b + i) * S + s) * 8 + rr;
+        const float xr = emb_res ? resid_embed<WQ8>(p, m, s, row, pv) : *rs;
+        const float y = xr + (m.gout[(i * SM + s) * 8 + rr] + bv);
+        *rs = y;
+        ll_st(xout + (size_t)s * d + row, y, c.tag);
+      }
     }
     STAMP(2);
   }
@@ -1019,14 +1178,19 @@ DEV bool phase_out(const StepParams& p, const Lds& m, const StepCtx& c, int l, G
 // Rows sharing an encoder output are processed together so the chunk's K/V is read once.
 template <int SM, int WQ8>
 DEV bool phase_cross(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
-  const int G = gridDim.x, tid = threadIdx.x, S = p.S, d = p.d, H = p.H, L = p.L;
+  const int tid = threadIdx.x, S = p.S, d = p.d, H = p.H, L = p.L;
   const LayerDev& lw = p.layers[l];
   const int ngrp = p.X == 1 ? 1 : S;
   const int ns = p.X == 1 ? S : 1;
   const int nitems = ngrp * H * p.ncc;
-  bool have_x = false;
+  int it = grp_first(gr);
+  if (it >= nitems) return true;
   STAMP(0);
-  for (int it = grp_first(gr); it < nitems; it += gr.size) {
+  VecRegs g2, b2;
+  vec_prefetch(lw.ln2_g, d, g2);
+  vec_prefetch(lw.ln2_b, d, b2);
+  bool have_x = false;
+  for (; it < nitems; it += gr.size) {
     const int ch = it % p.ncc, gh = it / p.ncc, h = gh % H, grp = gh / H;
     const int k0 = ch * p.chc;
     const int n = min(p.chc, p.A - k0);
@@ -1034,12 +1198,13 @@ DEV bool phase_cross(const StepParams& p, const Lds& m, const StepCtx& c, int l,
     auto off = [=](int j) -> size_t { return base + (size_t)j * kHeadDim; };
     WBatch<2, kNB> wq;
     gemvb_prefetch<2, kNB, WQ8>(lw.w_cq, lw.s_cq, d, d, (h * kHeadDim) >> 3, 1, kNB, wq);
+    const float bq = tid < kHeadDim ? lw.b_cq[h * kHeadDim + tid] : 0.f;
     KVRegs<KPT_CROSS> kr;
     attn_prefetch<KPT_CROSS, 0>(p.xk, p.xv, (size_t)p.X * L * H * p.A * kHeadDim * 2, off, n, kr);
     if (!have_x) {
-      if (!ll_poll1(p.x1 + (size_t)l * S * d, S * d, m.xin, c.tag, p.err)) return false;
+      if (!ll_poll1<8>(p.x1 + (size_t)l * S * d, S * d, m.xin, c.tag, p.err)) return false;
       STAMP(1);
-      wg_layernorm(m.xin, m.xn, S, d, lw.ln2_g, lw.ln2_b, m.scr);
+      wg_layernorm_r(m.xin, m.xn, S, d, g2, b2, m.scr);
       have_x = true;
     }
     float* q = m.big;                      // [ns][64]
@@ -1050,11 +1215,10 @@ DEV bool phase_cross(const StepParams& p, const Lds& m, const StepCtx& c, int l,
     float* sc = red + 4 * SM * kHeadDim;   // [ns][kMaxChunk + 4]
     const float* xs = m.xn + (p.X == 1 ? 0 : grp) * d;
     gemvb_compute<2, kNB, WQ8, SM>(wq, lw.w_cq, lw.s_cq, d, d, (h * kHeadDim) >> 3, 1, kNB, ns, xs, m.red, m.gout);
-    for (int i = tid; i < ns * kHeadDim; i += kThreads) {
-      const int s = i >> 6, e = i & 63;
-      q[i] = m.gout[((e >> 3) * SM + s) * 8 + (e & 7)] + lw.b_cq[h * kHeadDim + e];
+    if (tid < kHeadDim) {
+      for (int s = 0; s < ns; ++s) q[s * kHeadDim + tid] = m.gout[((tid >> 3) * SM + s) * 8 + (tid & 7)] + bq;
     }
-    __syncthreads();
+    lds_barrier();
     attn_compute<KPT_CROSS, SM>(kr, n, ns, q, nullptr, nullptr, 0.125f, sc, kMaxChunk + 4, red, pmv, plv, acc);
     STAMP(2);
     for (int i = tid; i < ns * kPartWords; i += kThreads) {
@@ -1067,52 +1231,87 @@ DEV bool phase_cross(const StepParams& p, const Lds& m, const StepCtx& c, int l,
   return true;
 }
 
-// LN3 + MLP1 + GELU table lookup.
+// LN3 + MLP1 + GELU.
 template <int SM, int WQ8>
 DEV bool phase_mlp1(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
-  const int G = gridDim.x, tid = threadIdx.x, S = p.S, d = p.d, d4 = 4 * d;
+  constexpr int NBM = 4;            // items whose weights are prefetched before the poll
+  constexpr int RM = WQ8 ? 2 : 4;   // 16-byte chunks per lane and row kept in registers
+  const int tid = threadIdx.x, S = p.S, d = p.d, d4 = 4 * d;
   const LayerDev& lw = p.layers[l];
   const int nitems = (d4 + 7) / 8;
   const int it0 = grp_first(gr);
   if (it0 >= nitems) return true;
-  WRegs<PFR> wr;
   STAMP(0);
-  gemv_prefetch<PFR, WQ8>(lw.w_1, lw.s_1, d4, d, it0 * 8, wr);
-  if (!ll_poll1(p.x2 + (size_t)l * S * d, S * d, m.xin, c.tag, p.err)) return false;
+  const int nmine = (nitems - it0 + gr.size - 1) / gr.size;
+  WBatch<RM, NBM> wr;
+  gemvb_prefetch<RM, NBM, WQ8>(lw.w_1, lw.s_1, d4, d, it0, gr.size, min(NBM, nmine), wr);
+  auto bias_of = [&](int b) -> float {
+    const int nit = min(NBM, nmine - b);
+    if (tid >= nit * S * 8) return 0.f;
+    const int i = tid / (S * 8), row = (it0 + (b + i) * gr.size) * 8 + (tid & 7);
+    return row < d4 ? lw.b_1[row] : 0.f;
+  };
+  float bv = bias_of(0);
+  VecRegs g3, b3;
+  vec_prefetch(lw.ln3_g, d, g3);
+  vec_prefetch(lw.ln3_b, d, b3);
+  if (!ll_poll1<8>(p.x2 + (size_t)l * S * d, S * d, m.xin, c.tag, p.err)) return false;
   STAMP(1);
-  wg_layernorm(m.xin, m.xn, S, d, lw.ln3_g, lw.ln3_b, m.scr);
-  for (int it = it0; it < nitems; it += gr.size) {
-    if (it != it0) gemv_prefetch<PFR, WQ8>(lw.w_1, lw.s_1, d4, d, it * 8, wr);
-    gemv_compute<PFR, WQ8, SM>(wr, lw.w_1, lw.s_1, d4, d, it * 8, S, m.xn, m.red, m.gout);
-    if (tid < 8 * S) {
-      const int s = tid >> 3, row = it * 8 + (tid & 7);
-      if (row < d4) ll_st(p.hm + ((size_t)l * S + s) * d4 + row, p.gelu[f2h(m.gout[tid] + lw.b_1[row])], c.tag);
+  wg_layernorm_r(m.xin, m.xn, S, d, g3, b3, m.scr);
+  for (int b = 0; b < nmine; b += NBM) {
+    const int nit = min(NBM, nmine - b);
+    if (b > 0) {
+      gemvb_prefetch<RM, NBM, WQ8>(lw.w_1, lw.s_1, d4, d, it0 + b * gr.size, gr.size, nit, wr);
+      bv = bias_of(b);
+    }
+    gemvb_compute<RM, NBM, WQ8, SM>(wr, lw.w_1, lw.s_1, d4, d, it0 + b * gr.size, gr.size, nit, S, m.xn, m.red, m.gout);
+    if (tid < nit * S * 8) {
+      const int i = tid / (S * 8), rem = tid - i * S * 8, s = rem >> 3, rr = rem & 7;
+      const int row = (it0 + (b + i) * gr.size) * 8 + rr;
+      if (row < d4) ll_st(p.hm + ((size_t)l * S + s) * d4 + row, gelu_f16(m.gout[(i * SM + s) * 8 + rr] + bv), c.tag);
     }
     STAMP(2);
   }
   return true;
 }
 
-// MLP2 + bias + residual.
+// MLP2 + bias + residual (the workgroup's own x2 rows, kept in LDS by the cross-out phase).
 template <int SM, int WQ8>
 DEV bool phase_mlp2(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
-  const int G = gridDim.x, tid = threadIdx.x, S = p.S, d = p.d, d4 = 4 * d;
+  constexpr int NBM = 1;  // items whose weights are prefetched before the poll (8 chunks per lane and row)
+  const int tid = threadIdx.x, S = p.S, d = p.d, d4 = 4 * d;
   const LayerDev& lw = p.layers[l];
   const int nitems = (d + 7) / 8;
   const int it0 = grp_first(gr);
   if (it0 >= nitems) return true;
-  WRegs<PFR> wr;
   STAMP(0);
-  gemv_prefetch<PFR, WQ8>(lw.w_2, lw.s_2, d, d4, it0 * 8, wr);
-  if (!ll_poll2(p.hm + (size_t)l * S * d4, S * d4, m.xin, p.x2 + (size_t)l * S * d, S * d, m.xn, c.tag, p.err))
-    return false;
+  const int nmine = (nitems - it0 + gr.size - 1) / gr.size;
+  WBatch<8, NBM> wr;
+  gemvb_prefetch<8, NBM, WQ8>(lw.w_2, lw.s_2, d, d4, it0, gr.size, min(NBM, nmine), wr);
+  auto row_of = [&](int b) -> int { return (it0 + (b + tid / (S * 8)) * gr.size) * 8 + (tid & 7); };
+  auto bias_of = [&](int b) -> float {
+    const int nit = min(NBM, nmine - b), row = row_of(b);
+    return (tid < nit * S * 8 && row < d) ? lw.b_2[row] : 0.f;
+  };
+  float bv = bias_of(0);
+  if (!ll_poll1<16>(p.hm + (size_t)l * S * d4, S * d4, m.xin, c.tag, p.err)) return false;
   STAMP(1);
-  for (int it = it0; it < nitems; it += gr.size) {
-    if (it != it0) gemv_prefetch<PFR, WQ8>(lw.w_2, lw.s_2, d, d4, it * 8, wr);
-    gemv_compute<PFR, WQ8, SM>(wr, lw.w_2, lw.s_2, d, d4, it * 8, S, m.xin, m.red, m.gout);
-    if (tid < 8 * S) {
-      const int s = tid >> 3, row = it * 8 + (tid & 7);
-      if (row < d) ll_st(p.x3 + ((size_t)l * S + s) * d + row, m.xn[s * d + row] + (m.gout[tid] + lw.b_2[row]), c.tag);
+  for (int b = 0; b < nmine; b += NBM) {
+    const int nit = min(NBM, nmine - b);
+    if (b > 0) {
+      gemvb_prefetch<8, NBM, WQ8>(lw.w_2, lw.s_2, d, d4, it0 + b * gr.size, gr.size, nit, wr);
+      bv = bias_of(b);
+    }
+    gemvb_compute<8, NBM, WQ8, SM>(wr, lw.w_2, lw.s_2, d, d4, it0 + b * gr.size, gr.size, nit, S, m.xin, m.red, m.gout);
+    if (tid < nit * S * 8) {
+      const int i = tid / (S * 8), rem = tid - i * S * 8, s = rem >> 3, rr = rem & 7;
+      const int row = row_of(b);
+      if (row < d) {
+        float* rs = m.res + ((b + i) * S + s) * 8 + rr;
+        const float y = *rs + (m.gout[(i * SM + s) * 8 + rr] + bv);
+        *rs = y;
+        ll_st(p.x3 + ((size_t)l * S + s) * d + row, y, c.tag);
+      }
     }
     STAMP(2);
   }
@@ -1157,9 +1356,12 @@ DEV bool phase_logits(const StepParams& p, const Lds& m, const StepCtx& c) {
   WBatch<2, kNB> wa, wb;
   STAMP(0);
   if (nb > 0) gemvb_prefetch<2, kNB, WQ8>(p.emb, p.emb_s, V, d, g, G, min(kNB, nmine), wa);
-  if (!ll_poll1(p.x3 + (size_t)(p.L - 1) * S * d, S * d, m.xin, c.tag, p.err)) return false;
+  VecRegs gf, bf;
+  vec_prefetch(p.lnf_g, d, gf);
+  vec_prefetch(p.lnf_b, d, bf);
+  if (!ll_poll1<8>(p.x3 + (size_t)(p.L - 1) * S * d, S * d, m.xin, c.tag, p.err)) return false;
   STAMP(1);
-  wg_layernorm(m.xin, m.xn, S, d, p.lnf_g, p.lnf_b, m.scr);
+  wg_layernorm_r(m.xin, m.xn, S, d, gf, bf, m.scr);
   for (int b = 0; b < nb; b += 2) {
     if (b + 1 < nb) gemvb_prefetch<2, kNB, WQ8>(p.emb, p.emb_s, V, d, g + (b + 1) * kNB * G, G, min(kNB, nmine - (b + 1) * kNB), wb);
     logits_batch<SM, WQ8>(p, m, c, wa, b, nmine, lg, rw, lidx, rpw);
@@ -1168,7 +1370,7 @@ DEV bool phase_logits(const StepParams& p, const Lds& m, const StepCtx& c) {
       logits_batch<SM, WQ8>(p, m, c, wb, b + 1, nmine, lg, rw, lidx, rpw);
     }
   }
-  __syncthreads();
+  lds_barrier();
   STAMP(2);
   // compact: rows beyond V (only in the last item) carry lidx -1 and sit at the end
   int nl = nmine * 8;
@@ -1178,30 +1380,34 @@ DEV bool phase_logits(const StepParams& p, const Lds& m, const StepCtx& c) {
   }
   for (int s = tid >> 6; s < S; s += 4)
     sel_partial(lg + s * rpw, rw + s * rpw, lidx, nl, p.probe, p.topk, rec + s * kSelWords);
-  __syncthreads();
+  lds_barrier();
+  // Self-KV rows this workgroup appended in this step are complete before its partial is visible:
+  // every workgroup of the next step's phases waits (directly or through other phases) on the
+  // selection, which waits on every workgroup's partial.
+  kv_drain();
   for (int i = tid; i < S * kSelWords; i += kThreads) ll_st(p.lp + (size_t)g * S * kSelWords + i, rec[i], c.tag);
   for (int i = tid; i < 2 * S; i += kThreads) ll_st(p.lpa + (size_t)g * S * 2 + i, rec[(i >> 1) * kSelWords + (i & 1)], c.tag);
   return true;
 }
 
-// Selection reduction.  Every workgroup reduces the (max, argmax) pairs to get the next token;
-// the last workgroup also merges the full partials (blocks of kRedBlock workgroups) into the
-// step outputs.
+// Selection reduction.  Every workgroup that runs a phase reading the next token reduces the
+// (max, argmax) pairs; one workgroup also merges the full partials (blocks of kRedBlock
+// workgroups) into the step outputs.
 DEV bool phase_reduce(const StepParams& p, const Lds& m, const StepCtx& c) {
-  const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x, S = p.S;
+  const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x, S = p.S, ng = p.ngroups;
   const bool last_step = c.st + 1 == p.nsteps;
   // Only the workgroups of the first two phases of the next step (layer 0 self-attention and
   // out-projection, which embed the next token) need the token; the output writer needs the
   // records.  Everyone else goes straight to its next phase, whose inputs depend on these.
-  const Grp g0 = phase_group(0, G), g1 = phase_group(1, G);
-  const int writer = phase_group(2, G).base;
+  const Grp g0 = phase_group(0, G, ng), g1 = phase_group(1, G, ng);
+  const int writer = phase_group(2, G, ng).base;
   const bool need_tok = !last_step && ((g >= g0.base && g < g0.base + g0.size) || (g >= g1.base && g < g1.base + g1.size));
   const bool is_writer = g == writer && p.out != nullptr;
   if (!need_tok && !is_writer) return true;
   float* pairs = m.big;  // [G][S][2]
   STAMP(0);
   if (need_tok) {
-    if (!ll_poll1(p.lpa, G * S * 2, pairs, c.tag, p.err)) return false;
+    if (!ll_poll1<8>(p.lpa, G * S * 2, pairs, c.tag, p.err)) return false;
   }
   STAMP(1);
   if (need_tok) {
@@ -1209,25 +1415,25 @@ DEV bool phase_reduce(const StepParams& p, const Lds& m, const StepCtx& c) {
       const int am = sel_argmax(pairs + 2 * s, G, 2 * S);
       if ((tid & 63) == 0) m.toks[s] = p.forced ? p.forced[(size_t)c.st * S + s] : (am == 0x7fffffff ? 0 : am);
     }
-    __syncthreads();
+    lds_barrier();
   }
   if (is_writer) {
     const int nblk = (G + kRedBlock - 1) / kRedBlock;
     float* blk = m.big;                                     // [kRedBlock][S][kSelWords]
     float* brec = blk + (size_t)kRedBlock * S * kSelWords;  // [nblk][S][kSelWords]
     for (int b = 0; b < nblk; ++b) {
-      const int gb = b * kRedBlock, ng = min(kRedBlock, G - gb);
-      if (!ll_wait_sparse(p.lp + (size_t)gb * S * kSelWords, ng, S * kSelWords, S * kSelWords - 1, -1, c.tag, p.err)) return false;
-      if (!ll_poll1(p.lp + (size_t)gb * S * kSelWords, ng * S * kSelWords, blk, c.tag, p.err)) return false;
+      const int gb = b * kRedBlock, ngb = min(kRedBlock, G - gb);
+      if (!ll_wait_sparse(p.lp + (size_t)gb * S * kSelWords, ngb, S * kSelWords, S * kSelWords - 1, -1, c.tag, p.err)) return false;
+      if (!ll_poll1<8>(p.lp + (size_t)gb * S * kSelWords, ngb * S * kSelWords, blk, c.tag, p.err)) return false;
       for (int s = tid >> 6; s < S; s += 4)
-        sel_merge(blk + s * kSelWords, ng, S * kSelWords, p.topk, brec + ((size_t)b * S + s) * kSelWords);
-      __syncthreads();
+        sel_merge(blk + s * kSelWords, ngb, S * kSelWords, p.topk, brec + ((size_t)b * S + s) * kSelWords);
+      lds_barrier();
     }
     float* fin = brec + (size_t)nblk * S * kSelWords;  // [S][kSelWords]
     for (int s = tid >> 6; s < S; s += 4) sel_merge(brec + s * kSelWords, nblk, S * kSelWords, p.topk, fin + s * kSelWords);
-    __syncthreads();
+    lds_barrier();
     if (tid < S) rec_to_out(fin + tid * kSelWords, p.topk, p.out + (size_t)c.st * S + tid);
-    __syncthreads();
+    lds_barrier();
   }
   return true;
 }
@@ -1243,10 +1449,12 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
   m.gout = m.red + kNB * 32 * SM;
   m.scr = m.gout + kNB * SM * 8;
   m.toks = reinterpret_cast<int*>(m.scr + 8);
-  m.big = m.scr + 8 + kMaxRows;
+  m.res = m.scr + 8 + kMaxRows;
+  m.big = m.res + kResItems * kMaxRows * 8;
   if (tid < S) m.toks[tid] = p.tokens0[tid];
-  __syncthreads();
+  lds_barrier();
   const int nph = 6 * p.L + 2;
+  const int G = gridDim.x, ng = p.ngroups;
   for (int st = 0; st < p.nsteps; ++st) {
     StepCtx c;
     c.tag = p.tag0 + (uint32_t)st;
@@ -1255,25 +1463,24 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
     c.pe = c.kv < p.C - 1 ? c.kv : p.C - 1;  // positional row (clamped as the reference)
     c.nph = nph;
     c.ph = 0;
-    const int G = gridDim.x;
     for (int l = 0; l < p.L; ++l) {
       const int q = 6 * l;
-      if (!phase_self<SM, WQ8>(p, m, c, l, phase_group(q, G))) return;
+      if (!phase_self<SM, WQ8>(p, m, c, l, phase_group(q, G, ng))) return;
       STAMP(3);
       ++c.ph;
-      if (!phase_out<SM, WQ8>(p, m, c, l, phase_group(q + 1, G), false)) return;
+      if (!phase_out<SM, WQ8>(p, m, c, l, phase_group(q + 1, G, ng), false)) return;
       STAMP(3);
       ++c.ph;
-      if (!phase_cross<SM, WQ8>(p, m, c, l, phase_group(q + 2, G))) return;
+      if (!phase_cross<SM, WQ8>(p, m, c, l, phase_group(q + 2, G, ng))) return;
       STAMP(3);
       ++c.ph;
-      if (!phase_out<SM, WQ8>(p, m, c, l, phase_group(q + 3, G), true)) return;
+      if (!phase_out<SM, WQ8>(p, m, c, l, phase_group(q + 3, G, ng), true)) return;
       STAMP(3);
       ++c.ph;
-      if (!phase_mlp1<SM, WQ8>(p, m, c, l, phase_group(q + 4, G))) return;
+      if (!phase_mlp1<SM, WQ8>(p, m, c, l, phase_group(q + 4, G, ng))) return;
       STAMP(3);
       ++c.ph;
-      if (!phase_mlp2<SM, WQ8>(p, m, c, l, phase_group(q + 5, G))) return;
+      if (!phase_mlp2<SM, WQ8>(p, m, c, l, phase_group(q + 5, G, ng))) return;
       STAMP(3);
       ++c.ph;
     }
@@ -1284,6 +1491,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
     STAMP(3);
     ++c.ph;
   }
+  kv_drain();
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1316,7 +1524,7 @@ __global__ void __launch_bounds__(kThreads) k_cross_kv(const LayerDev* layers, i
       }
       Bs[kk][r] = wv;
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll 8
     for (int kk = 0; kk < 32; ++kk) {
       float a[4], b[4];
@@ -1330,7 +1538,7 @@ __global__ void __launch_bounds__(kThreads) k_cross_kv(const LayerDev* layers, i
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
     }
-    __syncthreads();
+    lds_barrier();
   }
   uint16_t* out = (isv ? xv : xk) + (size_t)l * H * A * kHeadDim;
 #pragma unroll
@@ -1363,7 +1571,7 @@ __global__ void __launch_bounds__(kThreads) k_op_linear(const void* W, const uin
   float* red = xs + M * K;      // [32][8]
   float* out = red + 32 * 8;    // [8][8]
   for (int i = threadIdx.x; i < M * K; i += kThreads) xs[i] = x[i];
-  __syncthreads();
+  lds_barrier();
   const int it = blockIdx.x;
   WRegs<PFR> wr;
   gemv_prefetch<PFR, WQ8>(W, Ws, N, K, it * 8, wr);
@@ -1382,14 +1590,14 @@ __global__ void __launch_bounds__(kThreads) k_op_layernorm(const float* x, int r
   float* scr = ys + n;
   const int r = blockIdx.x;
   for (int i = threadIdx.x; i < n; i += kThreads) xs[i] = x[(size_t)r * n + i];
-  __syncthreads();
+  lds_barrier();
   wg_layernorm(xs, ys, 1, n, g, b, scr);
   for (int i = threadIdx.x; i < n; i += kThreads) y[(size_t)r * n + i] = ys[i];
 }
 
-__global__ void k_op_gelu(const float* x, int n, const float* table, float* y) {
+__global__ void k_op_gelu(const float* x, int n, float* y) {
   int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = table[f2h(x[i])];
+  if (i < n) y[i] = gelu_f16(x[i]);
 }
 
 // One workgroup per head; the keys are processed in chunks of kSelfChunk and merged exactly as the
@@ -1407,7 +1615,7 @@ __global__ void __launch_bounds__(kThreads) k_op_attention(const float* q, const
   float* red = sc + kSelfChunk + 4;         // [16][1][64]
   float* part = red + 16 * kHeadDim;        // [nc][kPartWords]
   for (int i = threadIdx.x; i < kHeadDim; i += kThreads) qs[i] = q[h * kHeadDim + i];
-  __syncthreads();
+  lds_barrier();
   const uint16_t* kb = k + (size_t)h * kv_len * kHeadDim;
   const uint16_t* vb = v + (size_t)h * kv_len * kHeadDim;
   for (int c = 0; c < nc; ++c) {
@@ -1418,7 +1626,7 @@ __global__ void __launch_bounds__(kThreads) k_op_attention(const float* q, const
     attn_compute<KPT_SELF, 1>(kr, n, 1, qs, nullptr, nullptr, scale, sc, kSelfChunk + 4, red, pmv, plv, acc);
     for (int i = threadIdx.x; i < kPartWords; i += kThreads)
       part[c * kPartWords + i] = i == 0 ? pmv[0] : (i == 1 ? plv[0] : acc[i - 2]);
-    __syncthreads();
+    lds_barrier();
   }
   attn_merge(part, nc, 1, acc);
   for (int i = threadIdx.x; i < kHeadDim; i += kThreads) out[h * kHeadDim + i] = acc[i];
@@ -1447,9 +1655,9 @@ __global__ void __launch_bounds__(kThreads) k_op_select_part(const float* logits
     }
     nl += min(8, n - it * 8);
   }
-  __syncthreads();
+  lds_barrier();
   if (threadIdx.x < 64) sel_partial(lg, rw, idx, nl, -1, k, rec);
-  __syncthreads();
+  lds_barrier();
   for (int i = threadIdx.x; i < kSelWords; i += kThreads) parts[((size_t)r * G + g) * kSelWords + i] = rec[i];
 }
 
@@ -1457,7 +1665,7 @@ __global__ void __launch_bounds__(64) k_op_select_final(const float* parts, int 
   __shared__ float rec[kSelWords];
   const int r = blockIdx.x;
   sel_merge(parts + (size_t)r * G * kSelWords, G, kSelWords, k, rec);
-  __syncthreads();
+  lds_barrier();
   if (threadIdx.x == 0) rec_to_out(rec, k, out + r);
 }
 
@@ -1466,7 +1674,8 @@ __global__ void __launch_bounds__(64) k_op_select_final(const float* parts, int 
 
 size_t step_lds_bytes(const StepParams& p, int grid) {
   const int S = p.S, d = p.d, SM = S > 1 ? kMaxRows : 1;
-  const size_t fixed = (size_t)S * 4 * d + (size_t)S * d + kNB * 32 * SM + kNB * SM * 8 + 8 + kMaxRows;
+  const size_t fixed =
+      (size_t)S * 4 * d + (size_t)S * d + kNB * 32 * SM + kNB * SM * 8 + 8 + kMaxRows + kResItems * kMaxRows * 8;
   const size_t self_attn = 2 * kHeadDim + 16 + kHeadDim + kSelfChunk + 4 + 16 * kHeadDim;
   const size_t cross_attn = SM * kHeadDim + 16 + SM * kHeadDim + 16 * SM * kHeadDim + (size_t)SM * (kMaxChunk + 4);
   const size_t merge_self = (size_t)p.ncs_max * S * p.H * kPartWords;
@@ -1562,8 +1771,8 @@ hipError_t launch_op_layernorm(const float* x, int rows, int n, const float* g, 
   return hipGetLastError();
 }
 
-hipError_t launch_op_gelu(const float* x, int n, const float* table, float* y, hipStream_t st) {
-  hipLaunchKernelGGL(k_op_gelu, dim3((n + 255) / 256), dim3(256), 0, st, x, n, table, y);
+hipError_t launch_op_gelu(const float* x, int n, float* y, hipStream_t st) {
+  hipLaunchKernelGGL(k_op_gelu, dim3((n + 255) / 256), dim3(256), 0, st, x, n, y);
   return hipGetLastError();
 }
 

@@ -9,7 +9,6 @@ namespace w4h {
 int fail(int code, const char* fmt, ...);
 float half_to_float(uint16_t h);
 uint16_t float_to_half(float f);
-void build_gelu_table(float* table65536);
 int session_rows(const w4h_session* s);
 w4h_dims session_dims(const w4h_session* s);
 }  // namespace w4h

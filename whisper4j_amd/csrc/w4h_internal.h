@@ -12,8 +12,9 @@ namespace w4h {
 constexpr int kHeadDim = 64;
 constexpr int kThreads = 256;  // threads per workgroup of every kernel
 constexpr int kMaxRows = 8;    // decoder rows per step handled by the persistent kernel
-constexpr int kSelfChunk = 128;  // self-attention keys per work item
+constexpr int kSelfChunk = 256;  // self-attention keys per work item
 constexpr int kMaxChunk = 256;   // longest key chunk an attention work item may take
+constexpr int kResItems = 4;     // d-row items (8 rows each) one workgroup may own in a phase
 constexpr int kPartWords = 2 + kHeadDim;            // (m, l, acc[64]) per attention partial
 constexpr int kSelWords = 6 + 2 * W4H_TOPK_MAX;     // per-workgroup selection partial
 
@@ -37,7 +38,6 @@ struct StepParams {
   const uint16_t* emb_s;
   const float* pos;
   const float *lnf_g, *lnf_b;
-  const float* gelu;
   // session
   int S, X, max_ctx;
   uint16_t *kv_k, *kv_v;        // [L][S][H][max_ctx][64]
@@ -57,6 +57,7 @@ struct StepParams {
   float* logits_out;            // [nsteps][S][V] or null
   unsigned* err;
   int rows_per_wg;              // vocab rows one workgroup keeps in LDS in the logits phase
+  int ngroups;                  // phase q runs on workgroup group q % ngroups (1 or 2)
   unsigned long long* trace;    // [nsteps][6L+2][grid] phase-end timestamps (wall clock) or null
 };
 
@@ -73,7 +74,7 @@ hipError_t launch_op_linear(const void* w, const uint16_t* ws, int wq8, int n, i
                             const float* x, int m, float* y, hipStream_t st);
 hipError_t launch_op_layernorm(const float* x, int rows, int n, const float* g, const float* b, float* y,
                                hipStream_t st);
-hipError_t launch_op_gelu(const float* x, int n, const float* table, float* y, hipStream_t st);
+hipError_t launch_op_gelu(const float* x, int n, float* y, hipStream_t st);
 hipError_t launch_op_attention(const float* q, const uint16_t* k, const uint16_t* v, int nh, int kv_len, float scale,
                                float* out, hipStream_t st);
 hipError_t launch_op_select(const float* logits, int rows, int n, const uint32_t* mask, int k, w4h_step_out* out,
