@@ -679,6 +679,239 @@ DEV void attn_merge(const float* part, int nc, int nrow, float* o) {
   lds_barrier();
 }
 
+constexpr int kVecRegs = 10;  // elements of a d-vector per thread (d <= 2560)
+
+
+// A d-vector parameter (LayerNorm gamma/beta, positional row) held in registers: thread t keeps
+// elements t + kThreads * i.  Loaded before a phase polls its inputs, so no parameter load sits
+// between the inputs' arrival and the phase's results.
+struct VecRegs {
+  float v[kVecRegs];
+};
+DEV void vec_prefetch(const float* src, int d, VecRegs& r) {
+  const auto rs = brsrc(src, (size_t)d * 4);
+#pragma unroll
+  for (int i = 0; i < kVecRegs; ++i) {
+    const int j = threadIdx.x + kThreads * i;
+    r.v[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, j < d ? j * 4 : (int)kOOB, 0, 0));
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Single-row (S = 1) paths, written as straight-line code: a lane's activation chunks are loaded
+// from LDS into registers once and reused by every 8-row group of the batch, out-of-range chunks
+// are zeroed by selects instead of branches (their weights are zero as well: buffer loads past the
+// end of a matrix return 0), and the only barrier is the one before the cross-wave reduction.
+
+// Activation chunks of a lane in the GEMV lane layout: round r holds x[(slot + 32 r) * CE + e],
+// e < CE, with CE = 8 (f16 weights: 8 halves per 16-byte chunk) or 16 (q8_0: 16 int8).
+template <int R, int WQ8>
+struct XR {
+  float v[R][WQ8 ? 16 : 8];
+};
+
+template <int R, int WQ8>
+DEV void xr_load(const float* x, int K, XR<R, WQ8>& X) {
+  constexpr int CE = WQ8 ? 16 : 8;
+  const int slot = ((threadIdx.x >> 6) << 3) | (threadIdx.x & 7);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int c = slot + 32 * r;
+    const bool ok = (c + 1) * CE <= K;
+    const float4* src = reinterpret_cast<const float4*>(x + (ok ? c * CE : 0));
+#pragma unroll
+    for (int q = 0; q < CE / 4; ++q) {
+      const float4 t = src[q];
+      X.v[r][4 * q + 0] = ok ? t.x : 0.f;
+      X.v[r][4 * q + 1] = ok ? t.y : 0.f;
+      X.v[r][4 * q + 2] = ok ? t.z : 0.f;
+      X.v[r][4 * q + 3] = ok ? t.w : 0.f;
+    }
+  }
+}
+
+DEV float dot8_fx(const uint4& w, const float* x) {
+  const float2 w0 = h2x2(w.x), w1 = h2x2(w.y), w2 = h2x2(w.z), w3 = h2x2(w.w);
+  float s = w0.x * x[0];
+  s = fmaf(w0.y, x[1], s);
+  s = fmaf(w1.x, x[2], s);
+  s = fmaf(w1.y, x[3], s);
+  s = fmaf(w2.x, x[4], s);
+  s = fmaf(w2.y, x[5], s);
+  s = fmaf(w3.x, x[6], s);
+  s = fmaf(w3.y, x[7], s);
+  return s;
+}
+
+DEV float dot16_qx(const uint4& w, const float* x) {
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    s = fmaf((float)(int8_t)(u[k] & 0xff), x[4 * k + 0], s);
+    s = fmaf((float)(int8_t)((u[k] >> 8) & 0xff), x[4 * k + 1], s);
+    s = fmaf((float)(int8_t)((u[k] >> 16) & 0xff), x[4 * k + 2], s);
+    s = fmaf((float)(int8_t)(u[k] >> 24), x[4 * k + 3], s);
+  }
+  return s;
+}
+
+// Partial dots of the NB items of a prefetched batch against the lane's activation chunks, reduced
+// over the 8 lanes of a row and written as red[i * 32 + wave * 8 + row] (LDS).  Chunks beyond the R
+// prefetched rounds (K > 32 R CE) are streamed here against x (LDS).  The caller puts an
+// lds_barrier() between this and gemv_out().
+template <int R, int NB, int WQ8>
+DEV void gemv_rx(const WBatch<R, NB>& wb, const XR<R, WQ8>& X, const void* W, const uint16_t* Ws, int N, int K, int it0,
+                 int istr, const float* x, float* red) {
+  constexpr int CE = WQ8 ? 16 : 8;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, row = lane >> 3;
+  const int slot = (w << 3) | (lane & 7);
+  float acc[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    float a = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (!WQ8)
+        a += dot8_fx(wb.w[i][r], X.v[r]);
+      else
+        a = fmaf(h2f(wb.s[i][r]), dot16_qx(wb.w[i][r], X.v[r]), a);
+    }
+    acc[i] = a;
+  }
+  if (K > 32 * R * CE) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      float t[1] = {0.f};
+      stream_rest<R, WQ8, 1>(W, Ws, N, K, (it0 + i * istr) * 8 + row, slot, 1, x, t);
+      acc[i] += t[0];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i) acc[i] = sum8(acc[i]);
+  if ((lane & 7) == 0) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) red[i * 32 + (w << 3) + row] = acc[i];
+  }
+}
+
+// Output rr of item i of the last gemv_rx (after the barrier).
+DEV float gemv_out(const float* red, int i, int rr) {
+  const float* p = red + i * 32 + rr;
+  return (p[0] + p[8]) + (p[16] + p[24]);
+}
+
+// Per-wave LayerNorm statistics of x[0, d) (LDS), two passes, eps 1e-5; no barrier.
+DEV void ln_stats(const float* x, int d, float& mean, float& inv) {
+  const int lane = threadIdx.x & 63;
+  float4 t[kVecRegs / 4 + 1];
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k <= kVecRegs / 4; ++k) {
+    const int i = lane * 4 + 256 * k;
+    const float4 v = *reinterpret_cast<const float4*>(x + (i < d ? i : 0));
+    t[k] = i < d ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+    s += (t[k].x + t[k].y) + (t[k].z + t[k].w);
+  }
+  mean = wave_sum(s) / (float)d;
+  float v = 0.f;
+#pragma unroll
+  for (int k = 0; k <= kVecRegs / 4; ++k) {
+    const int i = lane * 4 + 256 * k;
+    if (i < d) {
+      const float a = t[k].x - mean, b = t[k].y - mean, c = t[k].z - mean, e = t[k].w - mean;
+      v = fmaf(a, a, v);
+      v = fmaf(b, b, v);
+      v = fmaf(c, c, v);
+      v = fmaf(e, e, v);
+    }
+  }
+  inv = 1.0f / sqrtf(wave_sum(v) / (float)d + 1e-5f);
+}
+
+// LayerNorm of one row x[0, d) into y (LDS) with gamma/beta in registers (VecRegs layout); every
+// wave computes the statistics itself, so the only barrier is the one that publishes y.
+DEV void ln_row(const float* x, float* y, int d, const VecRegs& g, const VecRegs& b) {
+  float mean, inv;
+  ln_stats(x, d, mean, inv);
+#pragma unroll
+  for (int i = 0; i < kVecRegs; ++i) {
+    const int j = threadIdx.x + kThreads * i;
+    if (j < d) y[j] = (x[j] - mean) * inv * g.v[i] + b.v[i];
+  }
+  lds_barrier();
+}
+
+// Attention of one query row over n keys held in registers (8 lanes per key; key j = kg + 32 i,
+// kg = thread / 8), with the lane's query chunk Q = q[sub * 8, +8) in registers.  Each wave forms
+// its own softmax partial over its keys; the four partials are merged through LDS (wpart, 4 x 66
+// floats) after one barrier.  Threads 0..63 return acc[thread] of the merged partial (m, l, acc)
+// and m, l.
+template <int KPT>
+DEV void attn_rx(const KVRegs<KPT>& r, int n, const float (&Q)[8], float scale, float* wpart, float& m_out,
+                 float& l_out, float& acc_out) {
+  const int tid = threadIdx.x, kg = tid >> 3, sub = tid & 7, w = tid >> 6, lane = tid & 63;
+  float sc[KPT];
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const float t = sum8(dot8_fx(r.k[i], Q)) * scale;
+    sc[i] = (kg + 32 * i) < n ? t : -INFINITY;
+    mloc = fmaxf(mloc, sc[i]);
+  }
+  const float mw = wave_max(mloc);
+  float ls = 0.f, a[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a[e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const float pr = sc[i] > -INFINITY ? __expf(sc[i] - mw) : 0.f;
+    ls += pr;
+    const float2 v0 = h2x2(r.v[i].x), v1 = h2x2(r.v[i].y), v2 = h2x2(r.v[i].z), v3 = h2x2(r.v[i].w);
+    a[0] = fmaf(pr, v0.x, a[0]);
+    a[1] = fmaf(pr, v0.y, a[1]);
+    a[2] = fmaf(pr, v1.x, a[2]);
+    a[3] = fmaf(pr, v1.y, a[3]);
+    a[4] = fmaf(pr, v2.x, a[4]);
+    a[5] = fmaf(pr, v2.y, a[5]);
+    a[6] = fmaf(pr, v3.x, a[6]);
+    a[7] = fmaf(pr, v3.y, a[7]);
+  }
+  const float lw = wave_sum(sub == 0 ? ls : 0.f);
+  // sum over the 8 key groups of the wave (lanes sub + 8 g)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    a[e] += dpp<0x128>(a[e]);  // lane ^ 8 (row_ror:8 within 16 lanes)
+    a[e] += __shfl_xor(a[e], 16);
+    a[e] += __shfl_xor(a[e], 32);
+  }
+  if (lane < 8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wpart[w * kPartWords + 2 + sub * 8 + e] = a[e];
+    if (lane == 0) {
+      wpart[w * kPartWords] = mw;
+      wpart[w * kPartWords + 1] = lw;
+    }
+  }
+  lds_barrier();
+  if (tid < 64) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) M = fmaxf(M, wpart[q * kPartWords]);
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float mq = wpart[q * kPartWords];
+      const float f = mq > -INFINITY ? __expf(mq - M) : 0.f;
+      L = fmaf(wpart[q * kPartWords + 1], f, L);
+      A = fmaf(wpart[q * kPartWords + 2 + tid], f, A);
+    }
+    m_out = M;
+    l_out = L;
+    acc_out = A;
+  }
+}
+
 // ------------------------------------------------------------------------------------------------
 // Selection.  A workgroup partial over its rows (lg masked, rw raw logits, idx global ids) is
 // kSelWords floats: [max, argmax, sumexp(masked - max), raw max, raw sumexp, probe, topk values[8],
@@ -859,23 +1092,6 @@ struct Lds {
 };
 
 constexpr int kNB = 8;        // items per GEMV batch (64 rows)
-constexpr int kVecRegs = 10;  // elements of a d-vector per thread (d <= 2560)
-
-// A d-vector parameter (LayerNorm gamma/beta, positional row) held in registers: thread t keeps
-// elements t + kThreads * i.  Loaded before a phase polls its inputs, so no parameter load sits
-// between the inputs' arrival and the phase's results.
-struct VecRegs {
-  float v[kVecRegs];
-};
-DEV void vec_prefetch(const float* src, int d, VecRegs& r) {
-  const auto rs = brsrc(src, (size_t)d * 4);
-#pragma unroll
-  for (int i = 0; i < kVecRegs; ++i) {
-    const int j = threadIdx.x + kThreads * i;
-    r.v[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, j < d ? j * 4 : (int)kOOB, 0, 0));
-  }
-}
-
 // LayerNorm of S rows of d (LDS in, LDS out) with gamma/beta in registers; two passes, eps 1e-5.
 DEV void wg_layernorm_r(const float* x, float* y, int S, int d, const VecRegs& g, const VecRegs& b, float* scratch) {
   for (int s = 0; s < S; ++s) {
@@ -1438,6 +1654,398 @@ DEV bool phase_reduce(const StepParams& p, const Lds& m, const StepCtx& c) {
   return true;
 }
 
+// ------------------------------------------------------------------------------------------------
+// S = 1 phases (one row: greedy decode of one stream), built on the straight-line blocks above.
+// Same items, exchange buffers and publication order as the general phases.
+
+// Bias chunk of a lane for a 64-row head block: o[e] = b[base + (thread % 8) * 8 + e].
+DEV void bias8(const float* b, int base, float (&o)[8]) {
+  const float4* q = reinterpret_cast<const float4*>(b + base + (threadIdx.x & 7) * 8);
+  const float4 a = q[0], c = q[1];
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+  o[4] = c.x; o[5] = c.y; o[6] = c.z; o[7] = c.w;
+}
+
+template <int WQ8>
+DEV bool phase_self1(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
+  constexpr int R = 2;
+  const int tid = threadIdx.x, d = p.d, H = p.H, d3 = 3 * d, sub = tid & 7;
+  const LayerDev& lw = p.layers[l];
+  const int nold = (c.kv + kSelfChunk - 1) / kSelfChunk;
+  const int per = nold + 2;
+  const int nitems = H * per;
+  int it = grp_first(gr);
+  if (it >= nitems) return true;
+  STAMP(0);
+  VecRegs g1, b1, pe;
+  vec_prefetch(lw.ln1_g, d, g1);
+  vec_prefetch(lw.ln1_b, d, b1);
+  if (l == 0) vec_prefetch(p.pos + (size_t)c.pe * d, d, pe);
+  const size_t kv_bytes = (size_t)p.L * H * p.max_ctx * kHeadDim * 2;
+  const int mc = p.max_ctx;
+  bool have_x = false;
+  auto ensure_x = [&]() -> bool {
+    if (have_x) return true;
+    if (l == 0) {
+      embed_r<WQ8>(p, m, pe, m.xin);
+    } else if (!ll_poll1<8>(p.x3 + (size_t)(l - 1) * d, d, m.xin, c.tag, p.err)) {
+      return false;
+    }
+    STAMP(1);
+    ln_row(m.xin, m.xn, d, g1, b1);
+    have_x = true;
+    return true;
+  };
+  float* red = m.big;         // [8][32]
+  float* red2 = red + 256;    // [8][32]
+  float* wpart = red2 + 256;  // [4][kPartWords]
+  for (; it < nitems; it += gr.size) {
+    const int j = it % per, h = it / per;
+    const int kind = j < nold ? 0 : (j == nold ? 1 : 2);
+    const int rowA = (kind == 2 ? 2 * d : 0) + h * kHeadDim;  // q rows, or v rows for the value item
+    const int rowB = d + h * kHeadDim;                         // k rows
+    u64* dst = p.sp + (((size_t)l * p.ncs_max + (kind == 0 ? j : nold)) * H + h) * kPartWords;
+    if (kind == 0) {
+      // cached keys: q projection + attention over this chunk
+      WBatch<R, kNB> wa;
+      gemvb_prefetch<R, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, wa);
+      float bq[8];
+      bias8(lw.b_qkv, rowA, bq);
+      const int k0 = j * kSelfChunk;
+      const int n = min(kSelfChunk, c.kv - k0);
+      const int32_t* slots = p.slots;
+      const size_t lb = (size_t)l;
+      auto off = [=](int jj) -> size_t {
+        const int pos = k0 + jj;
+        const int slot = slots ? slots[pos] : 0;
+        return (((lb + slot) * H + h) * mc + pos) * kHeadDim;
+      };
+      KVRegs<KPT_SELF> kr;
+      attn_prefetch<KPT_SELF, 16>(p.kv_k, p.kv_v, kv_bytes, off, n, kr);
+      if (!ensure_x()) return false;
+      XR<R, WQ8> X;
+      xr_load<R, WQ8>(m.xn, d, X);
+      gemv_rx<R, kNB, WQ8>(wa, X, lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, m.xn, red);
+      lds_barrier();
+      float Q[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Q[e] = gemv_out(red, sub, e) + bq[e];
+      float M, Ls, A;
+      attn_rx<KPT_SELF>(kr, n, Q, 0.125f, wpart, M, Ls, A);
+      STAMP(2);
+      if (tid < 64) {
+        ll_st(dst + 2 + tid, A, c.tag);
+        if (tid == 0) {
+          ll_st(dst + 0, M, c.tag);
+          ll_st(dst + 1, Ls, c.tag);
+        }
+      }
+    } else {
+      // the current token: (q, k) score and k append, or v append
+      WBatch<R, kNB> wa, wb;
+      gemvb_prefetch<R, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, wa);
+      if (kind == 1) gemvb_prefetch<R, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, rowB >> 3, 1, kNB, wb);
+      const float ba = tid < kHeadDim ? lw.b_qkv[rowA + tid] : 0.f;
+      const float bb = (kind == 1 && tid < kHeadDim) ? lw.b_qkv[rowB + tid] : 0.f;
+      if (!ensure_x()) return false;
+      XR<R, WQ8> X;
+      xr_load<R, WQ8>(m.xn, d, X);
+      gemv_rx<R, kNB, WQ8>(wa, X, lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, m.xn, red);
+      if (kind == 1) gemv_rx<R, kNB, WQ8>(wb, X, lw.w_qkv, lw.s_qkv, d3, d, rowB >> 3, 1, m.xn, red2);
+      lds_barrier();
+      STAMP(2);
+      const size_t kvrow = (((size_t)l * H + h) * mc + c.kv) * kHeadDim;
+      if (tid < 64) {
+        const float va = gemv_out(red, tid >> 3, tid & 7) + ba;
+        if (kind == 1) {
+          const float vb = gemv_out(red2, tid >> 3, tid & 7) + bb;
+          const float t = wave_sum(va * vb);
+          if (tid == 0) {
+            ll_st(dst + 0, t * 0.125f, c.tag);
+            ll_st(dst + 1, 1.0f, c.tag);
+          }
+          kv_store(p.kv_k, kv_bytes, kvrow + tid, f2h(vb));
+        } else {
+          ll_st(dst + 2 + tid, va, c.tag);
+          kv_store(p.kv_v, kv_bytes, kvrow + tid, f2h(va));
+        }
+      }
+    }
+    lds_barrier();
+  }
+  return true;
+}
+
+template <int WQ8>
+DEV bool phase_cross1(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
+  constexpr int R = 2;
+  const int tid = threadIdx.x, d = p.d, H = p.H, L = p.L, sub = tid & 7;
+  const LayerDev& lw = p.layers[l];
+  const int nitems = H * p.ncc;
+  int it = grp_first(gr);
+  if (it >= nitems) return true;
+  STAMP(0);
+  VecRegs g2, b2;
+  vec_prefetch(lw.ln2_g, d, g2);
+  vec_prefetch(lw.ln2_b, d, b2);
+  bool have_x = false;
+  float* red = m.big;        // [8][32]
+  float* wpart = red + 256;  // [4][kPartWords]
+  for (; it < nitems; it += gr.size) {
+    const int ch = it % p.ncc, h = it / p.ncc;
+    const int k0 = ch * p.chc;
+    const int n = min(p.chc, p.A - k0);
+    const size_t base = ((((size_t)l) * H + h) * p.A + k0) * kHeadDim;
+    auto off = [=](int j) -> size_t { return base + (size_t)j * kHeadDim; };
+    WBatch<R, kNB> wq;
+    gemvb_prefetch<R, kNB, WQ8>(lw.w_cq, lw.s_cq, d, d, (h * kHeadDim) >> 3, 1, kNB, wq);
+    float bq[8];
+    bias8(lw.b_cq, h * kHeadDim, bq);
+    KVRegs<KPT_CROSS> kr;
+    attn_prefetch<KPT_CROSS, 0>(p.xk, p.xv, (size_t)L * H * p.A * kHeadDim * 2, off, n, kr);
+    if (!have_x) {
+      if (!ll_poll1<8>(p.x1 + (size_t)l * d, d, m.xin, c.tag, p.err)) return false;
+      STAMP(1);
+      ln_row(m.xin, m.xn, d, g2, b2);
+      have_x = true;
+    }
+    XR<R, WQ8> X;
+    xr_load<R, WQ8>(m.xn, d, X);
+    gemv_rx<R, kNB, WQ8>(wq, X, lw.w_cq, lw.s_cq, d, d, (h * kHeadDim) >> 3, 1, m.xn, red);
+    lds_barrier();
+    float Q[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) Q[e] = gemv_out(red, sub, e) + bq[e];
+    float M, Ls, A;
+    attn_rx<KPT_CROSS>(kr, n, Q, 0.125f, wpart, M, Ls, A);
+    STAMP(2);
+    u64* dst = p.cp + (((size_t)l * p.ncc + ch) * H + h) * kPartWords;
+    if (tid < 64) {
+      ll_st(dst + 2 + tid, A, c.tag);
+      if (tid == 0) {
+        ll_st(dst + 0, M, c.tag);
+        ll_st(dst + 1, Ls, c.tag);
+      }
+    }
+    lds_barrier();
+  }
+  return true;
+}
+
+// Merge attention partials, out-projection, bias and residual (the workgroup's own rows).
+template <int WQ8>
+DEV bool phase_out1(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr, bool cross) {
+  constexpr int R = 2;
+  const int tid = threadIdx.x, d = p.d, H = p.H;
+  const LayerDev& lw = p.layers[l];
+  const void* W = cross ? lw.w_co : lw.w_o;
+  const uint16_t* Ws = cross ? lw.s_co : lw.s_o;
+  const float* bias = cross ? lw.b_co : lw.b_o;
+  const int nitems = (d + 7) / 8;
+  const int it0 = grp_first(gr);
+  if (it0 >= nitems) return true;
+  STAMP(0);
+  const int nmine = (nitems - it0 + gr.size - 1) / gr.size;
+  WBatch<R, 1> wr;
+  gemvb_prefetch<R, 1, WQ8>(W, Ws, d, d, it0, gr.size, 1, wr);
+  const bool emb_res = !cross && l == 0;
+  auto row_of = [&](int b) -> int { return (it0 + b * gr.size) * 8 + (tid & 7); };
+  float bv = 0.f, pv = 0.f;
+  if (tid < 8 && row_of(0) < d) {
+    bv = bias[row_of(0)];
+    if (emb_res) pv = p.pos[(size_t)c.pe * d + row_of(0)];
+  }
+  float* part = m.big;
+  float* red = part + (size_t)(p.ncs_max > p.ncc ? p.ncs_max : p.ncc) * H * kPartWords;  // [2][256]
+  const int nc = cross ? p.ncc : (c.kv + kSelfChunk - 1) / kSelfChunk + 1;
+  const u64* psrc = cross ? p.cp + (size_t)l * p.ncc * H * kPartWords : p.sp + (size_t)l * p.ncs_max * H * kPartWords;
+  if (!ll_poll1<16>(psrc, nc * H * kPartWords, part, c.tag, p.err)) return false;
+  STAMP(1);
+  attn_merge(part, nc, H, m.xn);
+  XR<R, WQ8> X;
+  xr_load<R, WQ8>(m.xn, d, X);
+  u64* xout = (cross ? p.x2 : p.x1) + (size_t)l * d;
+  for (int b = 0; b < nmine; ++b) {
+    if (b > 0) {
+      gemvb_prefetch<R, 1, WQ8>(W, Ws, d, d, it0 + b * gr.size, gr.size, 1, wr);
+      if (tid < 8 && row_of(b) < d) {
+        bv = bias[row_of(b)];
+        if (emb_res) pv = p.pos[(size_t)c.pe * d + row_of(b)];
+      }
+    }
+    float* rb = red + (b & 1) * 256;
+    gemv_rx<R, 1, WQ8>(wr, X, W, Ws, d, d, it0 + b * gr.size, gr.size, m.xn, rb);
+    lds_barrier();
+    if (tid < 8) {
+      const int row = row_of(b);
+      if (row < d) {
+        float* rs = m.res + b * 8 + tid;
+        const float xr = emb_res ? resid_embed<WQ8>(p, m, 0, row, pv) : *rs;
+        const float y = xr + (gemv_out(rb, 0, tid) + bv);
+        *rs = y;
+        ll_st(xout + row, y, c.tag);
+      }
+    }
+    STAMP(2);
+  }
+  return true;
+}
+
+// LN3 + MLP1 + GELU.
+template <int WQ8>
+DEV bool phase_mlp1_1(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
+  constexpr int R = 2, NBM = 4;
+  const int tid = threadIdx.x, d = p.d, d4 = 4 * d;
+  const LayerDev& lw = p.layers[l];
+  const int nitems = (d4 + 7) / 8;
+  const int it0 = grp_first(gr);
+  if (it0 >= nitems) return true;
+  STAMP(0);
+  const int nmine = (nitems - it0 + gr.size - 1) / gr.size;
+  WBatch<R, NBM> wr;
+  gemvb_prefetch<R, NBM, WQ8>(lw.w_1, lw.s_1, d4, d, it0, gr.size, min(NBM, nmine), wr);
+  auto row_of = [&](int b) -> int { return (it0 + (b + (tid >> 3)) * gr.size) * 8 + (tid & 7); };
+  auto bias_of = [&](int b) -> float {
+    const int nit = min(NBM, nmine - b), row = row_of(b);
+    return (tid < nit * 8 && row < d4) ? lw.b_1[row] : 0.f;
+  };
+  float bv = bias_of(0);
+  VecRegs g3, b3;
+  vec_prefetch(lw.ln3_g, d, g3);
+  vec_prefetch(lw.ln3_b, d, b3);
+  float* red = m.big;  // [2][NBM * 32]
+  if (!ll_poll1<8>(p.x2 + (size_t)l * d, d, m.xin, c.tag, p.err)) return false;
+  STAMP(1);
+  ln_row(m.xin, m.xn, d, g3, b3);
+  XR<R, WQ8> X;
+  xr_load<R, WQ8>(m.xn, d, X);
+  for (int b = 0, k = 0; b < nmine; b += NBM, ++k) {
+    const int nit = min(NBM, nmine - b);
+    if (b > 0) {
+      gemvb_prefetch<R, NBM, WQ8>(lw.w_1, lw.s_1, d4, d, it0 + b * gr.size, gr.size, nit, wr);
+      bv = bias_of(b);
+    }
+    float* rb = red + (k & 1) * NBM * 32;
+    gemv_rx<R, NBM, WQ8>(wr, X, lw.w_1, lw.s_1, d4, d, it0 + b * gr.size, gr.size, m.xn, rb);
+    lds_barrier();
+    if (tid < nit * 8) {
+      const int row = row_of(b);
+      if (row < d4) ll_st(p.hm + (size_t)l * d4 + row, gelu_f16(gemv_out(rb, tid >> 3, tid & 7) + bv), c.tag);
+    }
+    STAMP(2);
+  }
+  return true;
+}
+
+// MLP2 + bias + residual (the workgroup's own x2 rows, kept in LDS by the cross-out phase).
+template <int WQ8>
+DEV bool phase_mlp2_1(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
+  constexpr int R = 8;
+  const int tid = threadIdx.x, d = p.d, d4 = 4 * d;
+  const LayerDev& lw = p.layers[l];
+  const int nitems = (d + 7) / 8;
+  const int it0 = grp_first(gr);
+  if (it0 >= nitems) return true;
+  STAMP(0);
+  const int nmine = (nitems - it0 + gr.size - 1) / gr.size;
+  WBatch<R, 1> wr;
+  gemvb_prefetch<R, 1, WQ8>(lw.w_2, lw.s_2, d, d4, it0, gr.size, 1, wr);
+  auto row_of = [&](int b) -> int { return (it0 + b * gr.size) * 8 + (tid & 7); };
+  float bv = (tid < 8 && row_of(0) < d) ? lw.b_2[row_of(0)] : 0.f;
+  float* red = m.big;  // [2][256]
+  if (!ll_poll1<16>(p.hm + (size_t)l * d4, d4, m.xin, c.tag, p.err)) return false;
+  STAMP(1);
+  XR<R, WQ8> X;
+  xr_load<R, WQ8>(m.xin, d4, X);
+  for (int b = 0; b < nmine; ++b) {
+    if (b > 0) {
+      gemvb_prefetch<R, 1, WQ8>(lw.w_2, lw.s_2, d, d4, it0 + b * gr.size, gr.size, 1, wr);
+      bv = (tid < 8 && row_of(b) < d) ? lw.b_2[row_of(b)] : 0.f;
+    }
+    float* rb = red + (b & 1) * 256;
+    gemv_rx<R, 1, WQ8>(wr, X, lw.w_2, lw.s_2, d, d4, it0 + b * gr.size, gr.size, m.xin, rb);
+    lds_barrier();
+    if (tid < 8) {
+      const int row = row_of(b);
+      if (row < d) {
+        float* rs = m.res + b * 8 + tid;
+        const float y = *rs + (gemv_out(rb, 0, tid) + bv);
+        *rs = y;
+        ll_st(p.x3 + (size_t)l * d + row, y, c.tag);
+      }
+    }
+    STAMP(2);
+  }
+  return true;
+}
+
+// Final LN + tied-embedding logits + masks + the workgroup's selection partial (one row).
+template <int WQ8>
+DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
+  constexpr int R = 2;
+  const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x, d = p.d, V = p.V;
+  const int nitems = (V + 7) / 8;
+  const int nmine = g < nitems ? (nitems - g + G - 1) / G : 0;
+  const int nb = (nmine + kNB - 1) / kNB;
+  const int rpw = p.rows_per_wg;
+  float* lg = m.big;                                  // [rpw] masked
+  float* rw = lg + rpw;                               // [rpw] raw
+  int* lidx = reinterpret_cast<int*>(rw + rpw);       // [rpw]
+  float* rec = reinterpret_cast<float*>(lidx + rpw);  // [kSelWords]
+  float* red = rec + kSelWords;                       // [2][256]
+  WBatch<R, kNB> wa, wb;
+  STAMP(0);
+  if (nb > 0) gemvb_prefetch<R, kNB, WQ8>(p.emb, p.emb_s, V, d, g, G, min(kNB, nmine), wa);
+  VecRegs gf, bf;
+  vec_prefetch(p.lnf_g, d, gf);
+  vec_prefetch(p.lnf_b, d, bf);
+  if (!ll_poll1<8>(p.x3 + (size_t)(p.L - 1) * d, d, m.xin, c.tag, p.err)) return false;
+  STAMP(1);
+  ln_row(m.xin, m.xn, d, gf, bf);
+  XR<R, WQ8> X;
+  xr_load<R, WQ8>(m.xn, d, X);
+  auto batch = [&](const WBatch<R, kNB>& w, int b) {
+    const int nit = min(kNB, nmine - b * kNB);
+    float* rb = red + (b & 1) * 256;
+    gemv_rx<R, kNB, WQ8>(w, X, p.emb, p.emb_s, V, d, g + b * kNB * G, G, m.xn, rb);
+    lds_barrier();
+    if (tid < nit * 8) {
+      const int i = tid >> 3, rr = tid & 7;
+      const int row = (g + (b * kNB + i) * G) * 8 + rr, li = (b * kNB + i) * 8 + rr;
+      if (row < V) {
+        const float v = gemv_out(rb, i, rr);
+        rw[li] = v;
+        lg[li] = (masked(p.mask, p.mw, 0, row) || masked(p.mask2, p.mw, 0, row)) ? -INFINITY : v;
+        lidx[li] = row;
+        if (p.logits_out) p.logits_out[(size_t)c.st * V + row] = v;
+      } else {
+        lidx[li] = -1;
+      }
+    }
+  };
+  for (int b = 0; b < nb; b += 2) {
+    if (b + 1 < nb) gemvb_prefetch<R, kNB, WQ8>(p.emb, p.emb_s, V, d, g + (b + 1) * kNB * G, G, min(kNB, nmine - (b + 1) * kNB), wb);
+    batch(wa, b);
+    if (b + 1 < nb) {
+      if (b + 2 < nb) gemvb_prefetch<R, kNB, WQ8>(p.emb, p.emb_s, V, d, g + (b + 2) * kNB * G, G, min(kNB, nmine - (b + 2) * kNB), wa);
+      batch(wb, b + 1);
+    }
+  }
+  lds_barrier();
+  STAMP(2);
+  int nl = nmine * 8;
+  if (nmine > 0) {
+    const int last_row0 = (g + (nmine - 1) * G) * 8;
+    nl = (nmine - 1) * 8 + min(8, V - last_row0);
+  }
+  if (tid < 64) sel_partial(lg, rw, lidx, nl, p.probe, p.topk, rec);
+  lds_barrier();
+  kv_drain();
+  for (int i = tid; i < kSelWords; i += kThreads) ll_st(p.lp + (size_t)g * kSelWords + i, rec[i], c.tag);
+  if (tid < 2) ll_st(p.lpa + (size_t)g * 2 + tid, rec[tid], c.tag);
+  return true;
+}
+
 template <int SM, int WQ8>
 __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
   extern __shared__ float lds_raw[];
@@ -1465,6 +2073,27 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
     c.ph = 0;
     for (int l = 0; l < p.L; ++l) {
       const int q = 6 * l;
+      if constexpr (SM == 1) {
+        if (!phase_self1<WQ8>(p, m, c, l, phase_group(q, G, ng))) return;
+        STAMP(3);
+        ++c.ph;
+        if (!phase_out1<WQ8>(p, m, c, l, phase_group(q + 1, G, ng), false)) return;
+        STAMP(3);
+        ++c.ph;
+        if (!phase_cross1<WQ8>(p, m, c, l, phase_group(q + 2, G, ng))) return;
+        STAMP(3);
+        ++c.ph;
+        if (!phase_out1<WQ8>(p, m, c, l, phase_group(q + 3, G, ng), true)) return;
+        STAMP(3);
+        ++c.ph;
+        if (!phase_mlp1_1<WQ8>(p, m, c, l, phase_group(q + 4, G, ng))) return;
+        STAMP(3);
+        ++c.ph;
+        if (!phase_mlp2_1<WQ8>(p, m, c, l, phase_group(q + 5, G, ng))) return;
+        STAMP(3);
+        ++c.ph;
+        continue;
+      }
       if (!phase_self<SM, WQ8>(p, m, c, l, phase_group(q, G, ng))) return;
       STAMP(3);
       ++c.ph;
@@ -1484,7 +2113,11 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
       STAMP(3);
       ++c.ph;
     }
-    if (!phase_logits<SM, WQ8>(p, m, c)) return;
+    if constexpr (SM == 1) {
+      if (!phase_logits1<WQ8>(p, m, c)) return;
+    } else {
+      if (!phase_logits<SM, WQ8>(p, m, c)) return;
+    }
     STAMP(3);
     ++c.ph;
     if (!phase_reduce(p, m, c)) return;
@@ -1678,13 +2311,16 @@ size_t step_lds_bytes(const StepParams& p, int grid) {
       (size_t)S * 4 * d + (size_t)S * d + kNB * 32 * SM + kNB * SM * 8 + 8 + kMaxRows + kResItems * kMaxRows * 8;
   const size_t self_attn = 2 * kHeadDim + 16 + kHeadDim + kSelfChunk + 4 + 16 * kHeadDim;
   const size_t cross_attn = SM * kHeadDim + 16 + SM * kHeadDim + 16 * SM * kHeadDim + (size_t)SM * (kMaxChunk + 4);
-  const size_t merge_self = (size_t)p.ncs_max * S * p.H * kPartWords;
-  const size_t merge_cross = (size_t)p.ncc * S * p.H * kPartWords;
-  const size_t logits = (size_t)2 * S * p.rows_per_wg + p.rows_per_wg + (size_t)S * kSelWords;
+  const size_t mp = (size_t)(p.ncs_max > p.ncc ? p.ncs_max : p.ncc) * S * p.H * kPartWords;
+  const size_t merge_self = mp + 512;   // partials + two GEMV reduction buffers
+  const size_t merge_cross = mp + 512;
+  const size_t logits = (size_t)2 * S * p.rows_per_wg + p.rows_per_wg + (size_t)S * kSelWords + 512;
+  const size_t fast_attn = 512 + 4 * kPartWords;
   const int nblk = (grid + kRedBlock - 1) / kRedBlock;
   size_t reduce = (size_t)(kRedBlock + nblk + 1) * S * kSelWords;
   if ((size_t)grid * S * 2 > reduce) reduce = (size_t)grid * S * 2;
   size_t big = self_attn;
+  big = big > fast_attn ? big : fast_attn;
   big = big > cross_attn ? big : cross_attn;
   big = big > merge_self ? big : merge_self;
   big = big > merge_cross ? big : merge_cross;
