@@ -397,6 +397,7 @@ int w4h_model_destroy(w4h_model* m) {
 struct w4h_session {
   w4h_model* m = nullptr;
   int S = 1, X = 1, max_ctx = 0, grid = 0, ngroups = 2, ncs_max = 0, ncc = 0, chc = 0, rpw = 0, mw = 0;
+  size_t rep_stride = 0;
   size_t lds = 0;
   hipStream_t stream = nullptr;
   DevBuf kvk, kvv, xk, xv, slots, ll, err, out, toks, forced, mask, mask2, logits, xa_tmp, trace;
@@ -456,6 +457,7 @@ static StepParams base_params(w4h_session* s) {
   p.err = s->err.as<unsigned>();
   p.rows_per_wg = s->rpw;
   p.ngroups = s->ngroups;
+  p.rep_stride = s->rep_stride;
   return p;
 }
 
@@ -605,7 +607,8 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
                n_vec = (size_t)L * s->S * d, n_cp = (size_t)L * s->ncc * s->S * H * kPartWords, n_hm = (size_t)L * s->S * 4 * d,
                n_lp = (size_t)s->grid * s->S * kSelWords, n_lpa = (size_t)s->grid * s->S * 2;
   const size_t total = n_qkv + n_sp + 4 * n_vec + n_cp + n_hm + n_lp + n_lpa;
-  if ((rc = s->ll.alloc(total * sizeof(u64)))) return rc;
+  s->rep_stride = total;  // kRep replicas of the whole set, consecutive
+  if ((rc = s->ll.alloc(total * kRep * sizeof(u64)))) return rc;
   u64* b = s->ll.as<u64>();
   s->qkv = b; b += n_qkv;
   s->sp = b; b += n_sp;
@@ -618,7 +621,7 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   s->lp = b; b += n_lp;
   s->lpa = b;
   HIPCHK(hipStreamCreate(&s->stream));
-  HIPCHK(launch_fill_u64(s->ll.as<u64>(), total, s->stream));
+  HIPCHK(launch_fill_u64(s->ll.as<u64>(), total * kRep, s->stream));
   if ((rc = s->err.alloc(256))) return rc;
   if ((rc = s->mask.alloc(sizeof(uint32_t) * (size_t)s->S * s->mw))) return rc;
   HIPCHK(hipStreamSynchronize(s->stream));

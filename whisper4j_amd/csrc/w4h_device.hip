@@ -67,8 +67,13 @@ DEV void kv_store(uint16_t* base, size_t bytes, size_t elem, uint16_t v) {
 DEV void kv_drain() { __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0), expcnt and lgkmcnt untouched */ }
 
 DEV u64 ll_ld(const u64* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-DEV void ll_st(u64* p, float v, uint32_t tag) {
-  __hip_atomic_store(p, ((u64)tag << 32) | (u64)__float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Publish one tagged word to every replica of an exchange buffer (replica r sits rs words after
+// replica r - 1).  Consumers poll the replica of their own workgroup (blockIdx % kRep), which
+// spreads the polling load of ~100 consumer workgroups over kRep copies of each word.
+DEV void ll_st(u64* p, float v, uint32_t tag, size_t rs) {
+  const u64 w = ((u64)tag << 32) | (u64)__float_as_uint(v);
+#pragma unroll
+  for (int r = 0; r < kRep; ++r) __hip_atomic_store(p + r * rs, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 DEV bool aborted(const unsigned* err) {
   return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
@@ -1142,6 +1147,9 @@ DEV int grp_first(Grp gr) {
   return (g >= gr.base && g < gr.base + gr.size) ? g - gr.base : 0x7fffffff;
 }
 
+// This workgroup's replica of an exchange buffer.
+DEV const u64* rep(const StepParams& p, const u64* b) { return b + (size_t)(blockIdx.x % kRep) * p.rep_stride; }
+
 struct StepCtx {
   uint32_t tag;
   int st, kv, pe, ph, nph;
@@ -1233,7 +1241,7 @@ DEV bool phase_self(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
     if (have_x) return true;
     if (l == 0) {
       embed_r<WQ8>(p, m, pe, m.xin);
-    } else if (!ll_poll1<8>(p.x3 + (size_t)(l - 1) * S * d, S * d, m.xin, c.tag, p.err)) {
+    } else if (!ll_poll1<8>(rep(p, p.x3 + (size_t)(l - 1) * S * d), S * d, m.xin, c.tag, p.err)) {
       return false;
     }
     STAMP(1);
@@ -1276,7 +1284,7 @@ DEV bool phase_self(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
       lds_barrier();
       attn_compute<KPT_SELF, 1>(kr, n, 1, va, nullptr, nullptr, 0.125f, sc, kSelfChunk + 4, red, pmv, plv, acc);
       STAMP(2);
-      for (int i = tid; i < kPartWords; i += kThreads) ll_st(dst + i, i == 0 ? pmv[0] : (i == 1 ? plv[0] : acc[i - 2]), c.tag);
+      for (int i = tid; i < kPartWords; i += kThreads) ll_st(dst + i, i == 0 ? pmv[0] : (i == 1 ? plv[0] : acc[i - 2]), c.tag, p.rep_stride);
     } else {
       // the current token: (q, k) score and k append, or v append
       WBatch<2, kNB> wa, wb;
@@ -1297,12 +1305,12 @@ DEV bool phase_self(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
         if (kind == 1) {
           const float t = wave_sum(va[tid] * vb[tid]);
           if (tid == 0) {
-            ll_st(dst + 0, t * 0.125f, c.tag);
-            ll_st(dst + 1, 1.0f, c.tag);
+            ll_st(dst + 0, t * 0.125f, c.tag, p.rep_stride);
+            ll_st(dst + 1, 1.0f, c.tag, p.rep_stride);
           }
           kv_store(p.kv_k, kv_bytes, kvrow + tid, f2h(vb[tid]));
         } else {
-          ll_st(dst + 2 + tid, va[tid], c.tag);
+          ll_st(dst + 2 + tid, va[tid], c.tag, p.rep_stride);
           kv_store(p.kv_v, kv_bytes, kvrow + tid, f2h(va[tid]));
         }
       }
@@ -1361,7 +1369,7 @@ DEV bool phase_out(const StepParams& p, const Lds& m, const StepCtx& c, int l, G
   float* part = m.big;
   const int nc = cross ? p.ncc : (c.kv + kSelfChunk - 1) / kSelfChunk + 1;
   const u64* psrc = cross ? p.cp + (size_t)l * p.ncc * S * H * kPartWords : p.sp + (size_t)l * p.ncs_max * S * H * kPartWords;
-  if (!ll_poll1<16>(psrc, nc * S * H * kPartWords, part, c.tag, p.err)) return false;
+  if (!ll_poll1<16>(rep(p, psrc), nc * S * H * kPartWords, part, c.tag, p.err)) return false;
   STAMP(1);
   attn_merge(part, nc, S * H, m.xn);
   u64* xout = (cross ? p.x2 : p.x1) + (size_t)l * S * d;
@@ -1381,7 +1389,7 @@ DEV bool phase_out(const StepParams& p, const Lds& m, const StepCtx& c, int l, G
         const float xr = emb_res ? resid_embed<WQ8>(p, m, s, row, pv) : *rs;
         const float y = xr + (m.gout[(i * SM + s) * 8 + rr] + bv);
         *rs = y;
-        ll_st(xout + (size_t)s * d + row, y, c.tag);
+        ll_st(xout + (size_t)s * d + row, y, c.tag, p.rep_stride);
       }
     }
     STAMP(2);
@@ -1418,7 +1426,7 @@ DEV bool phase_cross(const StepParams& p, const Lds& m, const StepCtx& c, int l,
     KVRegs<KPT_CROSS> kr;
     attn_prefetch<KPT_CROSS, 0>(p.xk, p.xv, (size_t)p.X * L * H * p.A * kHeadDim * 2, off, n, kr);
     if (!have_x) {
-      if (!ll_poll1<8>(p.x1 + (size_t)l * S * d, S * d, m.xin, c.tag, p.err)) return false;
+      if (!ll_poll1<8>(rep(p, p.x1 + (size_t)l * S * d), S * d, m.xin, c.tag, p.err)) return false;
       STAMP(1);
       wg_layernorm_r(m.xin, m.xn, S, d, g2, b2, m.scr);
       have_x = true;
@@ -1441,7 +1449,7 @@ DEV bool phase_cross(const StepParams& p, const Lds& m, const StepCtx& c, int l,
       const int s = i / kPartWords, w = i - s * kPartWords;
       const int row = p.X == 1 ? s : grp;
       u64* dst = p.cp + ((((size_t)l * p.ncc + ch) * S + row) * H + h) * kPartWords;
-      ll_st(dst + w, w == 0 ? pmv[s] : (w == 1 ? plv[s] : acc[s * kHeadDim + w - 2]), c.tag);
+      ll_st(dst + w, w == 0 ? pmv[s] : (w == 1 ? plv[s] : acc[s * kHeadDim + w - 2]), c.tag, p.rep_stride);
     }
   }
   return true;
@@ -1471,7 +1479,7 @@ DEV bool phase_mlp1(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
   VecRegs g3, b3;
   vec_prefetch(lw.ln3_g, d, g3);
   vec_prefetch(lw.ln3_b, d, b3);
-  if (!ll_poll1<8>(p.x2 + (size_t)l * S * d, S * d, m.xin, c.tag, p.err)) return false;
+  if (!ll_poll1<8>(rep(p, p.x2 + (size_t)l * S * d), S * d, m.xin, c.tag, p.err)) return false;
   STAMP(1);
   wg_layernorm_r(m.xin, m.xn, S, d, g3, b3, m.scr);
   for (int b = 0; b < nmine; b += NBM) {
@@ -1484,7 +1492,7 @@ DEV bool phase_mlp1(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
     if (tid < nit * S * 8) {
       const int i = tid / (S * 8), rem = tid - i * S * 8, s = rem >> 3, rr = rem & 7;
       const int row = (it0 + (b + i) * gr.size) * 8 + rr;
-      if (row < d4) ll_st(p.hm + ((size_t)l * S + s) * d4 + row, gelu_f16(m.gout[(i * SM + s) * 8 + rr] + bv), c.tag);
+      if (row < d4) ll_st(p.hm + ((size_t)l * S + s) * d4 + row, gelu_f16(m.gout[(i * SM + s) * 8 + rr] + bv), c.tag, p.rep_stride);
     }
     STAMP(2);
   }
@@ -1510,7 +1518,7 @@ DEV bool phase_mlp2(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
     return (tid < nit * S * 8 && row < d) ? lw.b_2[row] : 0.f;
   };
   float bv = bias_of(0);
-  if (!ll_poll1<16>(p.hm + (size_t)l * S * d4, S * d4, m.xin, c.tag, p.err)) return false;
+  if (!ll_poll1<16>(rep(p, p.hm + (size_t)l * S * d4), S * d4, m.xin, c.tag, p.err)) return false;
   STAMP(1);
   for (int b = 0; b < nmine; b += NBM) {
     const int nit = min(NBM, nmine - b);
@@ -1526,7 +1534,7 @@ DEV bool phase_mlp2(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
         float* rs = m.res + ((b + i) * S + s) * 8 + rr;
         const float y = *rs + (m.gout[(i * SM + s) * 8 + rr] + bv);
         *rs = y;
-        ll_st(p.x3 + ((size_t)l * S + s) * d + row, y, c.tag);
+        ll_st(p.x3 + ((size_t)l * S + s) * d + row, y, c.tag, p.rep_stride);
       }
     }
     STAMP(2);
@@ -1575,7 +1583,7 @@ DEV bool phase_logits(const StepParams& p, const Lds& m, const StepCtx& c) {
   VecRegs gf, bf;
   vec_prefetch(p.lnf_g, d, gf);
   vec_prefetch(p.lnf_b, d, bf);
-  if (!ll_poll1<8>(p.x3 + (size_t)(p.L - 1) * S * d, S * d, m.xin, c.tag, p.err)) return false;
+  if (!ll_poll1<8>(rep(p, p.x3 + (size_t)(p.L - 1) * S * d), S * d, m.xin, c.tag, p.err)) return false;
   STAMP(1);
   wg_layernorm_r(m.xin, m.xn, S, d, gf, bf, m.scr);
   for (int b = 0; b < nb; b += 2) {
@@ -1601,8 +1609,8 @@ DEV bool phase_logits(const StepParams& p, const Lds& m, const StepCtx& c) {
   // every workgroup of the next step's phases waits (directly or through other phases) on the
   // selection, which waits on every workgroup's partial.
   kv_drain();
-  for (int i = tid; i < S * kSelWords; i += kThreads) ll_st(p.lp + (size_t)g * S * kSelWords + i, rec[i], c.tag);
-  for (int i = tid; i < 2 * S; i += kThreads) ll_st(p.lpa + (size_t)g * S * 2 + i, rec[(i >> 1) * kSelWords + (i & 1)], c.tag);
+  for (int i = tid; i < S * kSelWords; i += kThreads) ll_st(p.lp + (size_t)g * S * kSelWords + i, rec[i], c.tag, p.rep_stride);
+  for (int i = tid; i < 2 * S; i += kThreads) ll_st(p.lpa + (size_t)g * S * 2 + i, rec[(i >> 1) * kSelWords + (i & 1)], c.tag, p.rep_stride);
   return true;
 }
 
@@ -1623,7 +1631,7 @@ DEV bool phase_reduce(const StepParams& p, const Lds& m, const StepCtx& c) {
   float* pairs = m.big;  // [G][S][2]
   STAMP(0);
   if (need_tok) {
-    if (!ll_poll1<8>(p.lpa, G * S * 2, pairs, c.tag, p.err)) return false;
+    if (!ll_poll1<8>(rep(p, p.lpa), G * S * 2, pairs, c.tag, p.err)) return false;
   }
   STAMP(1);
   if (need_tok) {
@@ -1639,8 +1647,8 @@ DEV bool phase_reduce(const StepParams& p, const Lds& m, const StepCtx& c) {
     float* brec = blk + (size_t)kRedBlock * S * kSelWords;  // [nblk][S][kSelWords]
     for (int b = 0; b < nblk; ++b) {
       const int gb = b * kRedBlock, ngb = min(kRedBlock, G - gb);
-      if (!ll_wait_sparse(p.lp + (size_t)gb * S * kSelWords, ngb, S * kSelWords, S * kSelWords - 1, -1, c.tag, p.err)) return false;
-      if (!ll_poll1<8>(p.lp + (size_t)gb * S * kSelWords, ngb * S * kSelWords, blk, c.tag, p.err)) return false;
+      if (!ll_wait_sparse(rep(p, p.lp + (size_t)gb * S * kSelWords), ngb, S * kSelWords, S * kSelWords - 1, -1, c.tag, p.err)) return false;
+      if (!ll_poll1<8>(rep(p, p.lp + (size_t)gb * S * kSelWords), ngb * S * kSelWords, blk, c.tag, p.err)) return false;
       for (int s = tid >> 6; s < S; s += 4)
         sel_merge(blk + s * kSelWords, ngb, S * kSelWords, p.topk, brec + ((size_t)b * S + s) * kSelWords);
       lds_barrier();
@@ -1688,7 +1696,7 @@ DEV bool phase_self1(const StepParams& p, const Lds& m, const StepCtx& c, int l,
     if (have_x) return true;
     if (l == 0) {
       embed_r<WQ8>(p, m, pe, m.xin);
-    } else if (!ll_poll1<8>(p.x3 + (size_t)(l - 1) * d, d, m.xin, c.tag, p.err)) {
+    } else if (!ll_poll1<8>(rep(p, p.x3 + (size_t)(l - 1) * d), d, m.xin, c.tag, p.err)) {
       return false;
     }
     STAMP(1);
@@ -1734,10 +1742,10 @@ DEV bool phase_self1(const StepParams& p, const Lds& m, const StepCtx& c, int l,
       attn_rx<KPT_SELF>(kr, n, Q, 0.125f, wpart, M, Ls, A);
       STAMP(2);
       if (tid < 64) {
-        ll_st(dst + 2 + tid, A, c.tag);
+        ll_st(dst + 2 + tid, A, c.tag, p.rep_stride);
         if (tid == 0) {
-          ll_st(dst + 0, M, c.tag);
-          ll_st(dst + 1, Ls, c.tag);
+          ll_st(dst + 0, M, c.tag, p.rep_stride);
+          ll_st(dst + 1, Ls, c.tag, p.rep_stride);
         }
       }
     } else {
@@ -1761,12 +1769,12 @@ DEV bool phase_self1(const StepParams& p, const Lds& m, const StepCtx& c, int l,
           const float vb = gemv_out(red2, tid >> 3, tid & 7) + bb;
           const float t = wave_sum(va * vb);
           if (tid == 0) {
-            ll_st(dst + 0, t * 0.125f, c.tag);
-            ll_st(dst + 1, 1.0f, c.tag);
+            ll_st(dst + 0, t * 0.125f, c.tag, p.rep_stride);
+            ll_st(dst + 1, 1.0f, c.tag, p.rep_stride);
           }
           kv_store(p.kv_k, kv_bytes, kvrow + tid, f2h(vb));
         } else {
-          ll_st(dst + 2 + tid, va, c.tag);
+          ll_st(dst + 2 + tid, va, c.tag, p.rep_stride);
           kv_store(p.kv_v, kv_bytes, kvrow + tid, f2h(va));
         }
       }
@@ -1804,7 +1812,7 @@ DEV bool phase_cross1(const StepParams& p, const Lds& m, const StepCtx& c, int l
     KVRegs<KPT_CROSS> kr;
     attn_prefetch<KPT_CROSS, 0>(p.xk, p.xv, (size_t)L * H * p.A * kHeadDim * 2, off, n, kr);
     if (!have_x) {
-      if (!ll_poll1<8>(p.x1 + (size_t)l * d, d, m.xin, c.tag, p.err)) return false;
+      if (!ll_poll1<8>(rep(p, p.x1 + (size_t)l * d), d, m.xin, c.tag, p.err)) return false;
       STAMP(1);
       ln_row(m.xin, m.xn, d, g2, b2);
       have_x = true;
@@ -1821,10 +1829,10 @@ DEV bool phase_cross1(const StepParams& p, const Lds& m, const StepCtx& c, int l
     STAMP(2);
     u64* dst = p.cp + (((size_t)l * p.ncc + ch) * H + h) * kPartWords;
     if (tid < 64) {
-      ll_st(dst + 2 + tid, A, c.tag);
+      ll_st(dst + 2 + tid, A, c.tag, p.rep_stride);
       if (tid == 0) {
-        ll_st(dst + 0, M, c.tag);
-        ll_st(dst + 1, Ls, c.tag);
+        ll_st(dst + 0, M, c.tag, p.rep_stride);
+        ll_st(dst + 1, Ls, c.tag, p.rep_stride);
       }
     }
     lds_barrier();
@@ -1859,7 +1867,7 @@ DEV bool phase_out1(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
   float* red = part + (size_t)(p.ncs_max > p.ncc ? p.ncs_max : p.ncc) * H * kPartWords;  // [2][256]
   const int nc = cross ? p.ncc : (c.kv + kSelfChunk - 1) / kSelfChunk + 1;
   const u64* psrc = cross ? p.cp + (size_t)l * p.ncc * H * kPartWords : p.sp + (size_t)l * p.ncs_max * H * kPartWords;
-  if (!ll_poll1<16>(psrc, nc * H * kPartWords, part, c.tag, p.err)) return false;
+  if (!ll_poll1<16>(rep(p, psrc), nc * H * kPartWords, part, c.tag, p.err)) return false;
   STAMP(1);
   attn_merge(part, nc, H, m.xn);
   XR<R, WQ8> X;
@@ -1883,7 +1891,7 @@ DEV bool phase_out1(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
         const float xr = emb_res ? resid_embed<WQ8>(p, m, 0, row, pv) : *rs;
         const float y = xr + (gemv_out(rb, 0, tid) + bv);
         *rs = y;
-        ll_st(xout + row, y, c.tag);
+        ll_st(xout + row, y, c.tag, p.rep_stride);
       }
     }
     STAMP(2);
@@ -1914,7 +1922,7 @@ DEV bool phase_mlp1_1(const StepParams& p, const Lds& m, const StepCtx& c, int l
   vec_prefetch(lw.ln3_g, d, g3);
   vec_prefetch(lw.ln3_b, d, b3);
   float* red = m.big;  // [2][NBM * 32]
-  if (!ll_poll1<8>(p.x2 + (size_t)l * d, d, m.xin, c.tag, p.err)) return false;
+  if (!ll_poll1<8>(rep(p, p.x2 + (size_t)l * d), d, m.xin, c.tag, p.err)) return false;
   STAMP(1);
   ln_row(m.xin, m.xn, d, g3, b3);
   XR<R, WQ8> X;
@@ -1930,7 +1938,7 @@ DEV bool phase_mlp1_1(const StepParams& p, const Lds& m, const StepCtx& c, int l
     lds_barrier();
     if (tid < nit * 8) {
       const int row = row_of(b);
-      if (row < d4) ll_st(p.hm + (size_t)l * d4 + row, gelu_f16(gemv_out(rb, tid >> 3, tid & 7) + bv), c.tag);
+      if (row < d4) ll_st(p.hm + (size_t)l * d4 + row, gelu_f16(gemv_out(rb, tid >> 3, tid & 7) + bv), c.tag, p.rep_stride);
     }
     STAMP(2);
   }
@@ -1953,7 +1961,7 @@ DEV bool phase_mlp2_1(const StepParams& p, const Lds& m, const StepCtx& c, int l
   auto row_of = [&](int b) -> int { return (it0 + b * gr.size) * 8 + (tid & 7); };
   float bv = (tid < 8 && row_of(0) < d) ? lw.b_2[row_of(0)] : 0.f;
   float* red = m.big;  // [2][256]
-  if (!ll_poll1<16>(p.hm + (size_t)l * d4, d4, m.xin, c.tag, p.err)) return false;
+  if (!ll_poll1<16>(rep(p, p.hm + (size_t)l * d4), d4, m.xin, c.tag, p.err)) return false;
   STAMP(1);
   XR<R, WQ8> X;
   xr_load<R, WQ8>(m.xin, d4, X);
@@ -1971,7 +1979,7 @@ DEV bool phase_mlp2_1(const StepParams& p, const Lds& m, const StepCtx& c, int l
         float* rs = m.res + b * 8 + tid;
         const float y = *rs + (gemv_out(rb, 0, tid) + bv);
         *rs = y;
-        ll_st(p.x3 + (size_t)l * d + row, y, c.tag);
+        ll_st(p.x3 + (size_t)l * d + row, y, c.tag, p.rep_stride);
       }
     }
     STAMP(2);
@@ -1999,7 +2007,7 @@ DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
   VecRegs gf, bf;
   vec_prefetch(p.lnf_g, d, gf);
   vec_prefetch(p.lnf_b, d, bf);
-  if (!ll_poll1<8>(p.x3 + (size_t)(p.L - 1) * d, d, m.xin, c.tag, p.err)) return false;
+  if (!ll_poll1<8>(rep(p, p.x3 + (size_t)(p.L - 1) * d), d, m.xin, c.tag, p.err)) return false;
   STAMP(1);
   ln_row(m.xin, m.xn, d, gf, bf);
   XR<R, WQ8> X;
@@ -2041,8 +2049,8 @@ DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
   if (tid < 64) sel_partial(lg, rw, lidx, nl, p.probe, p.topk, rec);
   lds_barrier();
   kv_drain();
-  for (int i = tid; i < kSelWords; i += kThreads) ll_st(p.lp + (size_t)g * kSelWords + i, rec[i], c.tag);
-  if (tid < 2) ll_st(p.lpa + (size_t)g * 2 + tid, rec[tid], c.tag);
+  for (int i = tid; i < kSelWords; i += kThreads) ll_st(p.lp + (size_t)g * kSelWords + i, rec[i], c.tag, p.rep_stride);
+  if (tid < 2) ll_st(p.lpa + (size_t)g * 2 + tid, rec[tid], c.tag, p.rep_stride);
   return true;
 }
 

@@ -15,6 +15,7 @@ constexpr int kMaxRows = 8;    // decoder rows per step handled by the persisten
 constexpr int kSelfChunk = 256;  // self-attention keys per work item
 constexpr int kMaxChunk = 256;   // longest key chunk an attention work item may take
 constexpr int kResItems = 4;     // d-row items (8 rows each) one workgroup may own in a phase
+constexpr int kRep = 1;          // replicas of every exchange buffer (consumers poll blockIdx % kRep)
 constexpr int kPartWords = 2 + kHeadDim;            // (m, l, acc[64]) per attention partial
 constexpr int kSelWords = 6 + 2 * W4H_TOPK_MAX;     // per-workgroup selection partial
 
@@ -58,6 +59,7 @@ struct StepParams {
   unsigned* err;
   int rows_per_wg;              // vocab rows one workgroup keeps in LDS in the logits phase
   int ngroups;                  // phase q runs on workgroup group q % ngroups (1 or 2)
+  size_t rep_stride;            // words between replicas of the exchange buffers
   unsigned long long* trace;    // [nsteps][6L+2][grid] phase-end timestamps (wall clock) or null
 };
 
