@@ -128,6 +128,87 @@ def traffic_from(fetch_csv, write_csv, copy_mib, out_path):
     print(open(out_path).read())
 
 
+def measure_forced(w4h, synth, name, wtype, n_steps, repeats, n_rows=1, n_encoders=1, n_sessions=1):
+    """Teacher-forced decode of one config: 4-token prefix prefilled untimed, then `n_steps` steps in
+    one launch per session and repeat; returns (tokens/s over all rows and sessions, us per step,
+    roofline fraction of the mean step)."""
+    dims = synth.SHAPES[name]
+    T = synth.make_decoder(dims, seed=0, wtype=wtype)
+    model = w4h.Model.from_tensors(dims, T)
+    prompt = list(synth.BENCH_PREFIX)
+    forced = synth.forced_tokens(n_steps, 0)
+    sessions = []
+    for q in range(n_sessions):
+        sess = model.session(n_rows=n_rows, n_encoders=n_encoders, max_ctx=dims.n_text_ctx)
+        for e in range(n_encoders):
+            sess.set_encoder(synth.encoder_output(dims, 0, stream=q * n_encoders + e), enc=e)
+        first = [prompt[0]] * n_rows
+        rest = [[t] * n_rows for t in prompt[1:]]
+        sess.run(first, forced=rest, n_steps=len(prompt))
+        sessions.append(sess)
+    kv0 = sessions[0].kv_len
+    tok0 = [int(forced[0])] * n_rows
+    fwd = [[int(t)] * n_rows for t in forced[1:n_steps]]
+    for sess in sessions:
+        sess.time_run(tok0, fwd, n_steps, 1)  # warm-up
+    total_ms = 0.0
+    for sess in sessions:
+        ms, _ = sess.time_run(tok0, fwd, n_steps, repeats)
+        total_ms += float(np.mean(ms))
+    for sess in sessions:
+        sess.close()
+    model.close()
+    step_us = total_ms * 1e3 / n_steps
+    w_b = 34.0 / 32.0 if wtype == "q8_0" else 2.0
+    rows = n_rows * n_sessions
+    encs = n_encoders * n_sessions
+    byts = sum(algorithmic_bytes_per_step(dims, kv0 + i, rows=rows, encoders=encs, w_b=w_b) for i in range(n_steps))
+    frac = byts / (total_ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+    return rows * n_steps / (total_ms * 1e-3), step_us, frac
+
+
+def measure_beam(w4h, synth, name, n_steps, beam):
+    """Beam search through the library's beam driver (device step + host candidate bookkeeping and KV
+    reorder per step); EOT is suppressed so every hypothesis runs all steps."""
+    from whisper4j_amd.decoder import WhisperDecoder
+
+    dims = synth.SHAPES[name]
+    T = synth.make_decoder(dims, seed=0, wtype="f16")
+    model = w4h.Model.from_tensors(dims, T)
+    dec = WhisperDecoder(model, beam_size=beam)
+    xa = synth.encoder_output(dims, 0)
+    eot = 50256
+    prompt = list(synth.BENCH_PREFIX)
+    dec.decode_beam(xa, prompt, eot, 16, suppress_tokens=[eot])  # warm-up
+    t0 = time.perf_counter()
+    r = dec.decode_beam(xa, prompt, eot, n_steps, suppress_tokens=[eot])
+    dt = time.perf_counter() - t0
+    dec.close()
+    model.close()
+    steps = len(r.tokens)
+    return steps / dt, beam * steps / dt, dt * 1e6 / steps, steps
+
+
+def other_configs(w4h, synth):
+    """Absolute decode rates of the four other workload shapes (one bounded run each)."""
+    out = {}
+    tps, us, frac = measure_forced(w4h, synth, "tiny.en", "f16", 224, 5)
+    out["tiny.en greedy b=1, 224 forced steps"] = {"tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
+                                                   "roofline_frac": round(frac, 4)}
+    sps, hps, us, steps = measure_beam(w4h, synth, "small", 224, 5)
+    out["small beam 5, 224 steps (library beam driver, EOT suppressed)"] = {
+        "steps_per_s": round(sps, 1), "hypothesis_tokens_per_s": round(hps, 1), "us_per_step": round(us, 2),
+        "steps": steps}
+    tps, us, frac = measure_forced(w4h, synth, "large-v3-turbo", "f16", 224, 2, n_rows=4, n_encoders=4,
+                                   n_sessions=8)
+    out["large-v3-turbo 32 streams, 224 forced steps (8 sessions x 4 streams, run one after another)"] = {
+        "tokens_per_s": round(tps, 1), "us_per_step": round(us, 2), "roofline_frac": round(frac, 4)}
+    tps, us, frac = measure_forced(w4h, synth, "medium", "q8_0", 444, 2)
+    out["medium q8_0 greedy b=1, 444 forced steps"] = {"tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
+                                                      "roofline_frac": round(frac, 4)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -136,6 +217,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum timed oracle work for the CPU baseline")
     ap.add_argument("--cpu-max-sweeps", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the tiny/small/turbo/medium lines")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run a plain copy of this many MiB (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -182,6 +264,8 @@ def main():
     achieved = bytes_launch / (ms_mean * 1e-3) / 1e9
     traffic = read_traffic()
 
+    configs = None if args.no_configs else other_configs(w4h, synth)
+
     cpu = None
     if not args.no_cpu:
         cps, dt, sweeps = cpu_baseline(dims, T, xa, prompt, forced, args.cpu_seconds, args.cpu_max_sweeps)
@@ -213,6 +297,7 @@ def main():
                      "kernel": "w4h::k_step<1,0> (persistent decoder step, whole sweep per launch)",
                      "algorithmic_bytes_per_launch": int(bytes_launch)},
         "cpu_baseline": cpu,
+        "other_configs": configs,
     }
     print(json.dumps(line))
 

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdarg>
@@ -397,7 +398,8 @@ int w4h_model_destroy(w4h_model* m) {
 struct w4h_session {
   w4h_model* m = nullptr;
   int S = 1, X = 1, max_ctx = 0, grid = 0, ngroups = 2, ncs_max = 0, ncc = 0, chc = 0, rpw = 0, mw = 0;
-  size_t rep_stride = 0;
+  size_t rep_stride = 0, res_off = 0;
+  int nres = 0;
   size_t lds = 0;
   hipStream_t stream = nullptr;
   DevBuf kvk, kvv, xk, xv, slots, ll, err, out, toks, forced, mask, mask2, logits, xa_tmp, trace;
@@ -458,6 +460,8 @@ static StepParams base_params(w4h_session* s) {
   p.rows_per_wg = s->rpw;
   p.ngroups = s->ngroups;
   p.rep_stride = s->rep_stride;
+  p.nres = s->nres;
+  p.res_off = s->res_off;
   return p;
 }
 
@@ -589,6 +593,18 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   probe_p.ncc = s->ncc;
   probe_p.rows_per_wg = s->rpw;
   s->lds = step_lds_bytes(probe_p, s->grid);
+  // One-row sessions keep the first vocabulary items of each workgroup's logits share resident in
+  // the LDS left over by the step (two 16-byte chunks per thread and item, plus q8_0 scales).
+  s->res_off = (s->lds + 15) & ~(size_t)15;
+  if (s->S == 1) {
+    const size_t item_bytes = (size_t)2 * kThreads * 16 + (m->wq8 ? (size_t)2 * kThreads * 2 : 0);
+    const size_t limit = (size_t)prop.sharedMemPerBlock;
+    const size_t avail = limit > s->res_off + 1024 ? limit - s->res_off - 1024 : 0;
+    const int nmine = ((V + 7) / 8 + s->grid - 1) / s->grid;
+    s->nres = (int)std::min<size_t>((size_t)nmine, avail / item_bytes);
+    if (const char* e = getenv("W4H_NRES")) s->nres = std::max(0, std::min(s->nres, atoi(e)));
+    s->lds = s->res_off + (size_t)s->nres * item_bytes;
+  }
   if (s->lds > (size_t)prop.sharedMemPerBlock)
     return fail(W4H_ERR_INVALID, "n_rows %d x n_text_state %d needs %zu bytes of LDS per workgroup (max %zu)", s->S, d, s->lds,
                 (size_t)prop.sharedMemPerBlock);

@@ -118,17 +118,22 @@ DEV float wave_max(float v) {
   v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), 0x143, 0xC, 0xF, false)));
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
-// (value, index) maximum; equal values keep the lower index.  NaN never wins.
+DEV int wave_min_i(int v) {
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true));
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, true));
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, true));
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, true));
+  v = min(v, __builtin_amdgcn_update_dpp(0x7fffffff, v, 0x142, 0xA, 0xF, false));
+  v = min(v, __builtin_amdgcn_update_dpp(0x7fffffff, v, 0x143, 0xC, 0xF, false));
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+// (value, index) maximum over the wave; equal values keep the lower index, NaN never wins.  Two
+// DPP reductions: the maximum value, then the lowest index that holds it.  Every lane gets both.
 DEV void wave_argmax(float& v, int& i) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float ov = __shfl_xor(v, o);
-    int oi = __shfl_xor(i, o);
-    if (ov > v || (ov == v && oi < i)) {
-      v = ov;
-      i = oi;
-    }
-  }
+  const float m = wave_max(v);
+  i = wave_min_i(v == m ? i : 0x7fffffff);
+  v = m;
 }
 
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS operations (lgkmcnt), not for
@@ -685,6 +690,7 @@ DEV void attn_merge(const float* part, int nc, int nrow, float* o) {
 }
 
 constexpr int kVecRegs = 10;  // elements of a d-vector per thread (d <= 2560)
+constexpr int kNB = 8;        // items per GEMV batch (64 rows)
 
 
 // A d-vector parameter (LayerNorm gamma/beta, positional row) held in registers: thread t keeps
@@ -804,6 +810,54 @@ DEV void gemv_rx(const WBatch<R, NB>& wb, const XR<R, WQ8>& X, const void* W, co
 DEV float gemv_out(const float* red, int i, int rr) {
   const float* p = red + i * 32 + rr;
   return (p[0] + p[8]) + (p[16] + p[24]);
+}
+
+// gemv_rx for items whose weight chunks sit in LDS in register-image order
+// (wl[(i * R + r) * kThreads + thread], scales alike); items i >= nit are skipped.
+template <int R, int NB, int WQ8>
+DEV void gemv_lds(const uint4* wl, const uint16_t* sl, int nit, const XR<R, WQ8>& X, float* red) {
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, row = lane >> 3;
+  float acc[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    float a = 0.f;
+    if (i < nit) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint4 wv = wl[(i * R + r) * kThreads + tid];
+        if (!WQ8)
+          a += dot8_fx(wv, X.v[r]);
+        else
+          a = fmaf(h2f(sl[(i * R + r) * kThreads + tid]), dot16_qx(wv, X.v[r]), a);
+      }
+    }
+    acc[i] = sum8(a);
+  }
+  if ((lane & 7) == 0) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) red[i * 32 + (w << 3) + row] = acc[i];
+  }
+}
+
+// Load this workgroup's first nres vocabulary items (items g, g + G, ...) into LDS in the register
+// image of the logits GEMV (two 16-byte chunks per lane and row), eight items per batch of loads.
+template <int WQ8>
+DEV void load_resident_vocab(const StepParams& p, uint4* ew, uint16_t* es, int nres) {
+  const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x;
+  for (int b = 0; b < nres; b += kNB) {
+    WBatch<2, kNB> wb;
+    gemvb_prefetch<2, kNB, WQ8>(p.emb, p.emb_s, p.V, p.d, g + b * G, G, min(kNB, nres - b), wb);
+#pragma unroll
+    for (int i = 0; i < kNB; ++i)
+      if (b + i < nres) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          ew[((b + i) * 2 + r) * kThreads + tid] = wb.w[i][r];
+          if (WQ8) es[((b + i) * 2 + r) * kThreads + tid] = wb.s[i][r];
+        }
+      }
+  }
+  lds_barrier();
 }
 
 // Per-wave LayerNorm statistics of x[0, d) (LDS), two passes, eps 1e-5; no barrier.
@@ -1094,9 +1148,10 @@ struct Lds {
   int* toks;    // [kMaxRows]     tokens of the current step
   float* res;   // [kResItems][S][8] residual rows of this workgroup's d-row items
   float* big;   // phase scratch
+  uint4* ew;    // [nres][2][kThreads] resident vocabulary rows (S = 1), GEMV register image
+  uint16_t* es; // [nres][2][kThreads] their q8_0 scales
 };
 
-constexpr int kNB = 8;        // items per GEMV batch (64 rows)
 // LayerNorm of S rows of d (LDS in, LDS out) with gamma/beta in registers; two passes, eps 1e-5.
 DEV void wg_layernorm_r(const float* x, float* y, int S, int d, const VecRegs& g, const VecRegs& b, float* scratch) {
   for (int s = 0; s < S; ++s) {
@@ -1366,12 +1421,17 @@ DEV bool phase_out(const StepParams& p, const Lds& m, const StepCtx& c, int l, G
     return (emb_res && tid < nit * S * 8 && row < d) ? p.pos[(size_t)c.pe * d + row] : 0.f;
   };
   float bv = bias_of(0), pv = pos_of(0);
-  float* part = m.big;
+  // The phase needs no activation buffer, so the partials start at the union region (over xin)
+  // and the merged attention output and GEMV scratch follow them.
+  float* part = m.xin;
+  float* o = part + (size_t)(p.ncs_max > p.ncc ? p.ncs_max : p.ncc) * S * H * kPartWords;
+  float* ored = o + S * d;
+  float* ogout = ored + kNB * 32 * SM;
   const int nc = cross ? p.ncc : (c.kv + kSelfChunk - 1) / kSelfChunk + 1;
   const u64* psrc = cross ? p.cp + (size_t)l * p.ncc * S * H * kPartWords : p.sp + (size_t)l * p.ncs_max * S * H * kPartWords;
   if (!ll_poll1<16>(rep(p, psrc), nc * S * H * kPartWords, part, c.tag, p.err)) return false;
   STAMP(1);
-  attn_merge(part, nc, S * H, m.xn);
+  attn_merge(part, nc, S * H, o);
   u64* xout = (cross ? p.x2 : p.x1) + (size_t)l * S * d;
   for (int b = 0; b < nmine; b += NBO) {
     const int nit = min(NBO, nmine - b);
@@ -1380,14 +1440,14 @@ DEV bool phase_out(const StepParams& p, const Lds& m, const StepCtx& c, int l, G
       bv = bias_of(b);
       pv = pos_of(b);
     }
-    gemvb_compute<RO, NBO, WQ8, SM>(wr, W, Ws, d, d, it0 + b * gr.size, gr.size, nit, S, m.xn, m.red, m.gout);
+    gemvb_compute<RO, NBO, WQ8, SM>(wr, W, Ws, d, d, it0 + b * gr.size, gr.size, nit, S, o, ored, ogout);
     if (tid < nit * S * 8) {
       const int i = tid / (S * 8), rem = tid - i * S * 8, s = rem >> 3, rr = rem & 7;
       const int row = row_of(b);
       if (row < d) {
         float* rs = m.res + ((b + i) * S + s) * 8 + rr;
         const float xr = emb_res ? resid_embed<WQ8>(p, m, s, row, pv) : *rs;
-        const float y = xr + (m.gout[(i * SM + s) * 8 + rr] + bv);
+        const float y = xr + (ogout[(i * SM + s) * 8 + rr] + bv);
         *rs = y;
         ll_st(xout + (size_t)s * d + row, y, c.tag, p.rep_stride);
       }
@@ -1994,7 +2054,9 @@ DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
   const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x, d = p.d, V = p.V;
   const int nitems = (V + 7) / 8;
   const int nmine = g < nitems ? (nitems - g + G - 1) / G : 0;
-  const int nb = (nmine + kNB - 1) / kNB;
+  const int nr = min(p.nres, nmine);                // items resident in LDS
+  const int nst = nmine - nr;                       // items streamed from memory
+  const int nb = (nst + kNB - 1) / kNB;
   const int rpw = p.rows_per_wg;
   float* lg = m.big;                                  // [rpw] masked
   float* rw = lg + rpw;                               // [rpw] raw
@@ -2003,7 +2065,10 @@ DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
   float* red = rec + kSelWords;                       // [2][256]
   WBatch<R, kNB> wa, wb;
   STAMP(0);
-  if (nb > 0) gemvb_prefetch<R, kNB, WQ8>(p.emb, p.emb_s, V, d, g, G, min(kNB, nmine), wa);
+  // streamed item k (0-based among the streamed ones) is item nr + k of this workgroup; the first
+  // two batches are in flight before the poll
+  if (nb > 0) gemvb_prefetch<R, kNB, WQ8>(p.emb, p.emb_s, V, d, g + nr * G, G, min(kNB, nst), wa);
+  if (nb > 1) gemvb_prefetch<R, kNB, WQ8>(p.emb, p.emb_s, V, d, g + (nr + kNB) * G, G, min(kNB, nst - kNB), wb);
   VecRegs gf, bf;
   vec_prefetch(p.lnf_g, d, gf);
   vec_prefetch(p.lnf_b, d, bf);
@@ -2012,14 +2077,12 @@ DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
   ln_row(m.xin, m.xn, d, gf, bf);
   XR<R, WQ8> X;
   xr_load<R, WQ8>(m.xn, d, X);
-  auto batch = [&](const WBatch<R, kNB>& w, int b) {
-    const int nit = min(kNB, nmine - b * kNB);
-    float* rb = red + (b & 1) * 256;
-    gemv_rx<R, kNB, WQ8>(w, X, p.emb, p.emb_s, V, d, g + b * kNB * G, G, m.xn, rb);
-    lds_barrier();
+  int nbat = 0;  // batches done (alternates the reduction buffers)
+  // outputs of a batch of nit items starting at local item i0
+  auto emit = [&](const float* rb, int i0, int nit) {
     if (tid < nit * 8) {
       const int i = tid >> 3, rr = tid & 7;
-      const int row = (g + (b * kNB + i) * G) * 8 + rr, li = (b * kNB + i) * 8 + rr;
+      const int row = (g + (i0 + i) * G) * 8 + rr, li = (i0 + i) * 8 + rr;
       if (row < V) {
         const float v = gemv_out(rb, i, rr);
         rw[li] = v;
@@ -2031,11 +2094,26 @@ DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
       }
     }
   };
+  for (int b = 0; b < nr; b += kNB, ++nbat) {
+    const int nit = min(kNB, nr - b);
+    float* rb = red + (nbat & 1) * 256;
+    gemv_lds<R, kNB, WQ8>(m.ew + (size_t)b * R * kThreads, m.es + (size_t)b * R * kThreads, nit, X, rb);
+    lds_barrier();
+    emit(rb, b, nit);
+  }
+  auto batch = [&](const WBatch<R, kNB>& w, int b) {
+    const int nit = min(kNB, nst - b * kNB);
+    float* rb = red + (nbat & 1) * 256;
+    ++nbat;
+    gemv_rx<R, kNB, WQ8>(w, X, p.emb, p.emb_s, V, d, g + (nr + b * kNB) * G, G, m.xn, rb);
+    lds_barrier();
+    emit(rb, nr + b * kNB, nit);
+  };
   for (int b = 0; b < nb; b += 2) {
-    if (b + 1 < nb) gemvb_prefetch<R, kNB, WQ8>(p.emb, p.emb_s, V, d, g + (b + 1) * kNB * G, G, min(kNB, nmine - (b + 1) * kNB), wb);
+    if (b > 0 && b + 1 < nb) gemvb_prefetch<R, kNB, WQ8>(p.emb, p.emb_s, V, d, g + (nr + (b + 1) * kNB) * G, G, min(kNB, nst - (b + 1) * kNB), wb);
     batch(wa, b);
     if (b + 1 < nb) {
-      if (b + 2 < nb) gemvb_prefetch<R, kNB, WQ8>(p.emb, p.emb_s, V, d, g + (b + 2) * kNB * G, G, min(kNB, nmine - (b + 2) * kNB), wa);
+      if (b + 2 < nb) gemvb_prefetch<R, kNB, WQ8>(p.emb, p.emb_s, V, d, g + (nr + (b + 2) * kNB) * G, G, min(kNB, nst - (b + 2) * kNB), wa);
       batch(wb, b + 1);
     }
   }
@@ -2059,15 +2137,25 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
   extern __shared__ float lds_raw[];
   const int tid = threadIdx.x, S = p.S, d = p.d;
   Lds m;
-  m.xin = lds_raw;
+  // persistent: scratch words, tokens, residual rows; then the per-phase region
+  m.scr = lds_raw;
+  m.toks = reinterpret_cast<int*>(m.scr + 8);
+  m.res = m.scr + 8 + kMaxRows;
+  m.xin = m.res + kResItems * kMaxRows * 8;
   m.xn = m.xin + S * 4 * d;
   m.red = m.xn + S * d;
   m.gout = m.red + kNB * 32 * SM;
-  m.scr = m.gout + kNB * SM * 8;
-  m.toks = reinterpret_cast<int*>(m.scr + 8);
-  m.res = m.scr + 8 + kMaxRows;
-  m.big = m.res + kResItems * kMaxRows * 8;
+  m.big = m.gout + kNB * SM * 8;
+  m.ew = reinterpret_cast<uint4*>(reinterpret_cast<char*>(lds_raw) + p.res_off);
+  m.es = reinterpret_cast<uint16_t*>(m.ew + (size_t)p.nres * 2 * kThreads);
   if (tid < S) m.toks[tid] = p.tokens0[tid];
+  if constexpr (SM == 1) {
+    if (p.nres > 0) {
+      const int nitems = (p.V + 7) / 8, G = gridDim.x;
+      const int nmine = blockIdx.x < nitems ? (nitems - blockIdx.x + G - 1) / G : 0;
+      load_resident_vocab<WQ8>(p, m.ew, m.es, min(p.nres, nmine));
+    }
+  }
   lds_barrier();
   const int nph = 6 * p.L + 2;
   const int G = gridDim.x, ng = p.ngroups;
@@ -2315,13 +2403,16 @@ __global__ void __launch_bounds__(64) k_op_select_final(const float* parts, int 
 
 size_t step_lds_bytes(const StepParams& p, int grid) {
   const int S = p.S, d = p.d, SM = S > 1 ? kMaxRows : 1;
-  const size_t fixed =
-      (size_t)S * 4 * d + (size_t)S * d + kNB * 32 * SM + kNB * SM * 8 + 8 + kMaxRows + kResItems * kMaxRows * 8;
+  const size_t persistent = 8 + kMaxRows + kResItems * kMaxRows * 8;
+  const size_t fixed = (size_t)S * 4 * d + (size_t)S * d + kNB * 32 * SM + kNB * SM * 8;
   const size_t self_attn = 2 * kHeadDim + 16 + kHeadDim + kSelfChunk + 4 + 16 * kHeadDim;
   const size_t cross_attn = SM * kHeadDim + 16 + SM * kHeadDim + 16 * SM * kHeadDim + (size_t)SM * (kMaxChunk + 4);
   const size_t mp = (size_t)(p.ncs_max > p.ncc ? p.ncs_max : p.ncc) * S * p.H * kPartWords;
-  const size_t merge_self = mp + 512;   // partials + two GEMV reduction buffers
-  const size_t merge_cross = mp + 512;
+  // one-row out phases: partials + two reduction buffers in big; general out phases: partials,
+  // merged output and GEMV scratch from the start of the per-phase region
+  const size_t merge_self = S == 1 ? mp + 512 : 0;
+  const size_t merge_cross = merge_self;
+  const size_t out_general = S == 1 ? 0 : mp + (size_t)S * d + kNB * 32 * SM + kNB * SM * 8;
   const size_t logits = (size_t)2 * S * p.rows_per_wg + p.rows_per_wg + (size_t)S * kSelWords + 512;
   const size_t fast_attn = 512 + 4 * kPartWords;
   const int nblk = (grid + kRedBlock - 1) / kRedBlock;
@@ -2334,7 +2425,8 @@ size_t step_lds_bytes(const StepParams& p, int grid) {
   big = big > merge_cross ? big : merge_cross;
   big = big > logits ? big : logits;
   big = big > reduce ? big : reduce;
-  return (fixed + big) * sizeof(float);
+  const size_t region = fixed + big > out_general ? fixed + big : out_general;
+  return (persistent + region) * sizeof(float);
 }
 
 int step_max_grid(size_t lds_bytes) {

@@ -60,6 +60,8 @@ struct StepParams {
   int rows_per_wg;              // vocab rows one workgroup keeps in LDS in the logits phase
   int ngroups;                  // phase q runs on workgroup group q % ngroups (1 or 2)
   size_t rep_stride;            // words between replicas of the exchange buffers
+  int nres;                     // vocabulary items (8 rows) a workgroup keeps resident in LDS (S = 1)
+  size_t res_off;               // byte offset of the resident vocabulary rows in dynamic LDS
   unsigned long long* trace;    // [nsteps][6L+2][grid] phase-end timestamps (wall clock) or null
 };
 
