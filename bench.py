@@ -77,16 +77,24 @@ def cpu_baseline(dims, T, xa, prompt, forced, min_seconds, max_sweeps):
 
 def copy_calibration(mib):
     """A plain device-to-device copy of `mib` MiB (reads mib, writes mib), run three times so that a
-    counter pass over this process sees a kernel of known traffic beside the decoder kernel."""
-    import torch
+    counter pass over this process sees a kernel of known traffic beside the decoder kernel.  Uses the
+    HIP runtime directly (hipMemcpy device-to-device runs the runtime's copy kernel); rocprofv3's
+    TCC counter passes abort in processes that have loaded torch, so torch is not used here."""
+    import ctypes
 
-    n = mib << 20
-    src = torch.empty(n, dtype=torch.uint8, device="cuda")
-    src.fill_(1)
-    dst = torch.empty_like(src)
+    hip = ctypes.CDLL("libamdhip64.so")
+    n = ctypes.c_size_t(mib << 20)
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    for ptr in (a, b):
+        if hip.hipMalloc(ctypes.byref(ptr), n) != 0:
+            raise RuntimeError("hipMalloc failed")
+    hip.hipMemset(a, 1, n)
     for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
+        if hip.hipMemcpy(b, a, n, 3) != 0:  # hipMemcpyDeviceToDevice
+            raise RuntimeError("hipMemcpy failed")
+    hip.hipDeviceSynchronize()
+    hip.hipFree(a)
+    hip.hipFree(b)
 
 
 def traffic_from(fetch_csv, write_csv, copy_mib, out_path):
