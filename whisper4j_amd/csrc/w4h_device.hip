@@ -860,6 +860,72 @@ DEV void load_resident_vocab(const StepParams& p, uint4* ew, uint16_t* es, int n
   lds_barrier();
 }
 
+// Multi-row GEMV: rows s < S of x (LDS, row stride K) against the NB items of a prefetched batch.
+// Weight chunks are read from registers once per round and applied to every row; a row's
+// activation chunk is loaded from LDS once per round and applied to every item.  Result layout
+// red[((i * 32) + wave * 8 + row) * SM + s], read back with gemv_outm() after a barrier.
+template <int SM, int R, int NB, int WQ8>
+DEV void gemv_rxm(const WBatch<R, NB>& wb, const float* x, int S, int K, const void* W, const uint16_t* Ws, int N,
+                  int it0, int istr, float* red) {
+  constexpr int CE = WQ8 ? 16 : 8;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, row = lane >> 3;
+  const int slot = (w << 3) | (lane & 7);
+  float acc[NB][SM];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int s = 0; s < SM; ++s) acc[i][s] = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int c = slot + 32 * r;
+    const bool ok = (c + 1) * CE <= K;
+#pragma unroll
+    for (int s = 0; s < SM; ++s) {
+      if (s < S) {
+        float xv[CE];
+        const float4* src = reinterpret_cast<const float4*>(x + (size_t)s * K + (ok ? c * CE : 0));
+#pragma unroll
+        for (int q = 0; q < CE / 4; ++q) {
+          const float4 t = src[q];
+          xv[4 * q + 0] = ok ? t.x : 0.f;
+          xv[4 * q + 1] = ok ? t.y : 0.f;
+          xv[4 * q + 2] = ok ? t.z : 0.f;
+          xv[4 * q + 3] = ok ? t.w : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+          if (!WQ8)
+            acc[i][s] += dot8_fx(wb.w[i][r], xv);
+          else
+            acc[i][s] = fmaf(h2f(wb.s[i][r]), dot16_qx(wb.w[i][r], xv), acc[i][s]);
+        }
+      }
+    }
+  }
+  if (K > 32 * R * CE) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) stream_rest<R, WQ8, SM>(W, Ws, N, K, (it0 + i * istr) * 8 + row, slot, S, x, acc[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int s = 0; s < SM; ++s) acc[i][s] = sum8(acc[i][s]);
+  if ((lane & 7) == 0) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int s = 0; s < SM; ++s)
+        if (s < S) red[((i * 32) + (w << 3) + row) * SM + s] = acc[i][s];
+  }
+}
+
+// Output rr of item i, row s of the last gemv_rxm (after the barrier).
+template <int SM>
+DEV float gemv_outm(const float* red, int i, int rr, int s) {
+  const float* q = red + (i * 32 + rr) * SM + s;
+  return (q[0] + q[8 * SM]) + (q[16 * SM] + q[24 * SM]);
+}
+
 // Per-wave LayerNorm statistics of x[0, d) (LDS), two passes, eps 1e-5; no barrier.
 DEV void ln_stats(const float* x, int d, float& mean, float& inv) {
   const int lane = threadIdx.x & 63;
@@ -1142,8 +1208,6 @@ DEV bool masked(const uint32_t* m, int mw, int s, int v) {
 struct Lds {
   float* xin;   // [S][4d]        polled activations
   float* xn;    // [S][d]         LayerNorm output / merged attention output
-  float* red;   // [kNB][32][SM]  GEMV cross-wave partials
-  float* gout;  // [kNB][SM][8]   GEMV results
   float* scr;   // [8]
   int* toks;    // [kMaxRows]     tokens of the current step
   float* res;   // [kResItems][S][8] residual rows of this workgroup's d-row items
@@ -1265,6 +1329,21 @@ DEV float gelu_f16(float v) {
   return (0.5f * x) * (1.0f + (float)t);
 }
 
+// ------------------------------------------------------------------------------------------------
+// Phases.  SM is the row capacity of the kernel instance (1: greedy decode of one stream; 8: beams or
+// streams, S <= 8 rows at run time).  Every phase is built on the straight-line blocks above:
+// weights (and key/value chunks) are prefetched into registers before the poll, a lane's
+// activation chunks are read from LDS once per round and applied to every weight row it holds, and
+// the only barriers are the cross-wave reductions.
+
+// Bias chunk of a lane for a 64-row head block: o[e] = b[base + (thread % 8) * 8 + e].
+DEV void bias8(const float* b, int base, float (&o)[8]) {
+  const float4* q = reinterpret_cast<const float4*>(b + base + (threadIdx.x & 7) * 8);
+  const float4 a = q[0], c = q[1];
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+  o[4] = c.x; o[5] = c.y; o[6] = c.z; o[7] = c.w;
+}
+
 // Self-attention with the q/k/v projection folded in.  Per (row s, head h) the items are:
 //   j <  nold : cached-key chunk j (keys [j*C, min((j+1)*C, kv)));  projects q_h, attends, writes a
 //               partial (m, l, acc[64]) to chunk slot j;
@@ -1276,7 +1355,8 @@ DEV float gelu_f16(float v) {
 // before it publishes, which orders them before any later step reads the cache.
 template <int SM, int WQ8>
 DEV bool phase_self(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
-  const int tid = threadIdx.x, S = p.S, d = p.d, H = p.H, d3 = 3 * d;
+  constexpr int R = 2;
+  const int tid = threadIdx.x, S = p.S, d = p.d, H = p.H, d3 = 3 * d, sub = tid & 7;
   const LayerDev& lw = p.layers[l];
   const int nold = (c.kv + kSelfChunk - 1) / kSelfChunk;
   const int per = nold + 2;
@@ -1291,7 +1371,6 @@ DEV bool phase_self(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
   const size_t kv_bytes = (size_t)p.L * S * H * p.max_ctx * kHeadDim * 2;
   const int mc = p.max_ctx;
   bool have_x = false;
-  // Layer input and LN1 (once per phase, before the first item's compute).
   auto ensure_x = [&]() -> bool {
     if (have_x) return true;
     if (l == 0) {
@@ -1300,28 +1379,26 @@ DEV bool phase_self(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
       return false;
     }
     STAMP(1);
-    wg_layernorm_r(m.xin, m.xn, S, d, g1, b1, m.scr);
+    for (int s = 0; s < S; ++s) ln_row(m.xin + s * d, m.xn + s * d, d, g1, b1);
     have_x = true;
     return true;
   };
-  float* va = m.big;                 // [64] q (or v)
-  float* vb = va + kHeadDim;         // [64] k
-  float* pmv = vb + kHeadDim;        // [8]
-  float* plv = pmv + 8;              // [8]
-  float* acc = plv + 8;              // [64]
-  float* sc = acc + kHeadDim;        // [kSelfChunk + 4]
-  float* red = sc + kSelfChunk + 4;  // [16][64]
+  float* red = m.big;         // [8][32]
+  float* red2 = red + 256;    // [8][32]
+  float* wpart = red2 + 256;  // [4][kPartWords]
   for (; it < nitems; it += gr.size) {
     const int j = it % per, sh = it / per, h = sh % H, s = sh / H;
     const int kind = j < nold ? 0 : (j == nold ? 1 : 2);
     const int rowA = (kind == 2 ? 2 * d : 0) + h * kHeadDim;  // q rows, or v rows for the value item
     const int rowB = d + h * kHeadDim;                         // k rows
-    const float biasA = tid < kHeadDim ? lw.b_qkv[rowA + tid] : 0.f;
     u64* dst = p.sp + ((((size_t)l * p.ncs_max + (kind == 0 ? j : nold)) * S + s) * H + h) * kPartWords;
+    const float* xs = m.xn + s * d;
     if (kind == 0) {
       // cached keys: q projection + attention over this chunk
-      WBatch<2, kNB> wa;
-      gemvb_prefetch<2, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, wa);
+      WBatch<R, kNB> wa;
+      gemvb_prefetch<R, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, wa);
+      float bq[8];
+      bias8(lw.b_qkv, rowA, bq);
       const int k0 = j * kSelfChunk;
       const int n = min(kSelfChunk, c.kv - k0);
       const int32_t* slots = p.slots ? p.slots + (size_t)s * mc : nullptr;
@@ -1334,39 +1411,47 @@ DEV bool phase_self(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
       KVRegs<KPT_SELF> kr;
       attn_prefetch<KPT_SELF, 16>(p.kv_k, p.kv_v, kv_bytes, off, n, kr);
       if (!ensure_x()) return false;
-      gemvb_compute<2, kNB, WQ8, SM>(wa, lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, 1, m.xn + s * d, m.red, m.gout);
-      if (tid < kHeadDim) va[tid] = m.gout[((tid >> 3) * SM) * 8 + (tid & 7)] + biasA;
+      gemv_rxm<1, R, kNB, WQ8>(wa, xs, 1, d, lw.w_qkv, lw.s_qkv, d3, rowA >> 3, 1, red);
       lds_barrier();
-      attn_compute<KPT_SELF, 1>(kr, n, 1, va, nullptr, nullptr, 0.125f, sc, kSelfChunk + 4, red, pmv, plv, acc);
+      float Q[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Q[e] = gemv_outm<1>(red, sub, e, 0) + bq[e];
+      float M, Ls, A;
+      attn_rx<KPT_SELF>(kr, n, Q, 0.125f, wpart, M, Ls, A);
       STAMP(2);
-      for (int i = tid; i < kPartWords; i += kThreads) ll_st(dst + i, i == 0 ? pmv[0] : (i == 1 ? plv[0] : acc[i - 2]), c.tag, p.rep_stride);
+      if (tid < 64) {
+        ll_st(dst + 2 + tid, A, c.tag, p.rep_stride);
+        if (tid == 0) {
+          ll_st(dst + 0, M, c.tag, p.rep_stride);
+          ll_st(dst + 1, Ls, c.tag, p.rep_stride);
+        }
+      }
     } else {
       // the current token: (q, k) score and k append, or v append
-      WBatch<2, kNB> wa, wb;
-      gemvb_prefetch<2, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, wa);
-      if (kind == 1) gemvb_prefetch<2, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, rowB >> 3, 1, kNB, wb);
-      const float biasB = (kind == 1 && tid < kHeadDim) ? lw.b_qkv[rowB + tid] : 0.f;
+      WBatch<R, kNB> wa, wb;
+      gemvb_prefetch<R, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, wa);
+      if (kind == 1) gemvb_prefetch<R, kNB, WQ8>(lw.w_qkv, lw.s_qkv, d3, d, rowB >> 3, 1, kNB, wb);
+      const float ba = tid < kHeadDim ? lw.b_qkv[rowA + tid] : 0.f;
+      const float bb = (kind == 1 && tid < kHeadDim) ? lw.b_qkv[rowB + tid] : 0.f;
       if (!ensure_x()) return false;
-      gemvb_compute<2, kNB, WQ8, SM>(wa, lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, kNB, 1, m.xn + s * d, m.red, m.gout);
-      if (tid < kHeadDim) va[tid] = m.gout[((tid >> 3) * SM) * 8 + (tid & 7)] + biasA;
-      if (kind == 1) {
-        gemvb_compute<2, kNB, WQ8, SM>(wb, lw.w_qkv, lw.s_qkv, d3, d, rowB >> 3, 1, kNB, 1, m.xn + s * d, m.red, m.gout);
-        if (tid < kHeadDim) vb[tid] = m.gout[((tid >> 3) * SM) * 8 + (tid & 7)] + biasB;
-      }
+      gemv_rxm<1, R, kNB, WQ8>(wa, xs, 1, d, lw.w_qkv, lw.s_qkv, d3, rowA >> 3, 1, red);
+      if (kind == 1) gemv_rxm<1, R, kNB, WQ8>(wb, xs, 1, d, lw.w_qkv, lw.s_qkv, d3, rowB >> 3, 1, red2);
       lds_barrier();
       STAMP(2);
       const size_t kvrow = ((((size_t)l * S + s) * H + h) * mc + c.kv) * kHeadDim;
       if (tid < 64) {
+        const float va = gemv_outm<1>(red, tid >> 3, tid & 7, 0) + ba;
         if (kind == 1) {
-          const float t = wave_sum(va[tid] * vb[tid]);
+          const float vb = gemv_outm<1>(red2, tid >> 3, tid & 7, 0) + bb;
+          const float t = wave_sum(va * vb);
           if (tid == 0) {
             ll_st(dst + 0, t * 0.125f, c.tag, p.rep_stride);
             ll_st(dst + 1, 1.0f, c.tag, p.rep_stride);
           }
-          kv_store(p.kv_k, kv_bytes, kvrow + tid, f2h(vb[tid]));
+          kv_store(p.kv_k, kv_bytes, kvrow + tid, f2h(vb));
         } else {
-          ll_st(dst + 2 + tid, va[tid], c.tag, p.rep_stride);
-          kv_store(p.kv_v, kv_bytes, kvrow + tid, f2h(va[tid]));
+          ll_st(dst + 2 + tid, va, c.tag, p.rep_stride);
+          kv_store(p.kv_v, kv_bytes, kvrow + tid, f2h(va));
         }
       }
     }
@@ -1392,11 +1477,11 @@ DEV float resid_embed(const StepParams& p, const Lds& m, int s, int row, float p
   return e + pos;
 }
 
-// Merge attention partials, out-projection, bias and residual:  xout = xres + (Wo . o + b).
+// Merge attention partials, out-projection, bias and residual (the workgroup's own rows):
+// xout = xres + (Wo . o + b).
 template <int SM, int WQ8>
 DEV bool phase_out(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr, bool cross) {
-  constexpr int NBO = 1;            // items whose weights are prefetched before the poll
-  constexpr int RO = WQ8 ? 2 : 4;   // 16-byte chunks per lane and row kept in registers
+  constexpr int R = 2;
   const int tid = threadIdx.x, S = p.S, d = p.d, H = p.H;
   const LayerDev& lw = p.layers[l];
   const void* W = cross ? lw.w_co : lw.w_o;
@@ -1407,47 +1492,45 @@ DEV bool phase_out(const StepParams& p, const Lds& m, const StepCtx& c, int l, G
   if (it0 >= nitems) return true;
   STAMP(0);
   const int nmine = (nitems - it0 + gr.size - 1) / gr.size;
-  WBatch<RO, NBO> wr;
-  gemvb_prefetch<RO, NBO, WQ8>(W, Ws, d, d, it0, gr.size, min(NBO, nmine), wr);
-  // the output this thread publishes in batch b: item b + tid / (S * 8), row s, row-in-item rr
-  auto row_of = [&](int b) -> int { return (it0 + (b + tid / (S * 8)) * gr.size) * 8 + (tid & 7); };
-  auto bias_of = [&](int b) -> float {
-    const int nit = min(NBO, nmine - b), row = row_of(b);
-    return (tid < nit * S * 8 && row < d) ? bias[row] : 0.f;
-  };
+  WBatch<R, 1> wr;
+  gemvb_prefetch<R, 1, WQ8>(W, Ws, d, d, it0, gr.size, 1, wr);
   const bool emb_res = !cross && l == 0;
-  auto pos_of = [&](int b) -> float {
-    const int nit = min(NBO, nmine - b), row = row_of(b);
-    return (emb_res && tid < nit * S * 8 && row < d) ? p.pos[(size_t)c.pe * d + row] : 0.f;
-  };
-  float bv = bias_of(0), pv = pos_of(0);
-  // The phase needs no activation buffer, so the partials start at the union region (over xin)
-  // and the merged attention output and GEMV scratch follow them.
-  float* part = m.xin;
-  float* o = part + (size_t)(p.ncs_max > p.ncc ? p.ncs_max : p.ncc) * S * H * kPartWords;
-  float* ored = o + S * d;
-  float* ogout = ored + kNB * 32 * SM;
+  const bool mine = tid < S * 8;  // thread -> (row s = tid / 8, row-in-item tid % 8)
+  auto row_of = [&](int b) -> int { return (it0 + b * gr.size) * 8 + (tid & 7); };
+  float bv = 0.f, pv = 0.f;
+  if (mine && row_of(0) < d) {
+    bv = bias[row_of(0)];
+    if (emb_res) pv = p.pos[(size_t)c.pe * d + row_of(0)];
+  }
+  // partials, merged attention output and reduction buffers: one row in the phase scratch; several
+  // rows from the start of the per-phase region (the phase needs no activation buffer)
+  const size_t mp = (size_t)(p.ncs_max > p.ncc ? p.ncs_max : p.ncc) * S * H * kPartWords;
+  float* part = SM == 1 ? m.big : m.xin;
+  float* o = SM == 1 ? m.xn : part + mp;
+  float* red = SM == 1 ? part + mp : o + S * d;  // [2][32 * SM]
   const int nc = cross ? p.ncc : (c.kv + kSelfChunk - 1) / kSelfChunk + 1;
   const u64* psrc = cross ? p.cp + (size_t)l * p.ncc * S * H * kPartWords : p.sp + (size_t)l * p.ncs_max * S * H * kPartWords;
   if (!ll_poll1<16>(rep(p, psrc), nc * S * H * kPartWords, part, c.tag, p.err)) return false;
   STAMP(1);
   attn_merge(part, nc, S * H, o);
   u64* xout = (cross ? p.x2 : p.x1) + (size_t)l * S * d;
-  for (int b = 0; b < nmine; b += NBO) {
-    const int nit = min(NBO, nmine - b);
+  for (int b = 0; b < nmine; ++b) {
     if (b > 0) {
-      gemvb_prefetch<RO, NBO, WQ8>(W, Ws, d, d, it0 + b * gr.size, gr.size, nit, wr);
-      bv = bias_of(b);
-      pv = pos_of(b);
+      gemvb_prefetch<R, 1, WQ8>(W, Ws, d, d, it0 + b * gr.size, gr.size, 1, wr);
+      if (mine && row_of(b) < d) {
+        bv = bias[row_of(b)];
+        if (emb_res) pv = p.pos[(size_t)c.pe * d + row_of(b)];
+      }
     }
-    gemvb_compute<RO, NBO, WQ8, SM>(wr, W, Ws, d, d, it0 + b * gr.size, gr.size, nit, S, o, ored, ogout);
-    if (tid < nit * S * 8) {
-      const int i = tid / (S * 8), rem = tid - i * S * 8, s = rem >> 3, rr = rem & 7;
-      const int row = row_of(b);
+    float* rb = red + (b & 1) * 32 * SM;
+    gemv_rxm<SM, R, 1, WQ8>(wr, o, S, d, W, Ws, d, it0 + b * gr.size, gr.size, rb);
+    lds_barrier();
+    if (mine) {
+      const int s = tid >> 3, rr = tid & 7, row = row_of(b);
       if (row < d) {
-        float* rs = m.res + ((b + i) * S + s) * 8 + rr;
+        float* rs = m.res + (b * S + s) * 8 + rr;
         const float xr = emb_res ? resid_embed<WQ8>(p, m, s, row, pv) : *rs;
-        const float y = xr + (ogout[(i * SM + s) * 8 + rr] + bv);
+        const float y = xr + (gemv_outm<SM>(rb, 0, rr, s) + bv);
         *rs = y;
         ll_st(xout + (size_t)s * d + row, y, c.tag, p.rep_stride);
       }
@@ -1459,10 +1542,11 @@ DEV bool phase_out(const StepParams& p, const Lds& m, const StepCtx& c, int l, G
 
 // Cross-attention with the q projection folded in: one item per (encoder group, head, key chunk);
 // the item projects q_h for its rows from LN2(x1), then attends over its chunk of encoder keys.
-// Rows sharing an encoder output are processed together so the chunk's K/V is read once.
+// Rows sharing an encoder output (beams) are processed together so the chunk's K/V is read once.
 template <int SM, int WQ8>
 DEV bool phase_cross(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
-  const int tid = threadIdx.x, S = p.S, d = p.d, H = p.H, L = p.L;
+  constexpr int R = 2;
+  const int tid = threadIdx.x, S = p.S, d = p.d, H = p.H, L = p.L, sub = tid & 7;
   const LayerDev& lw = p.layers[l];
   const int ngrp = p.X == 1 ? 1 : S;
   const int ns = p.X == 1 ? S : 1;
@@ -1474,42 +1558,49 @@ DEV bool phase_cross(const StepParams& p, const Lds& m, const StepCtx& c, int l,
   vec_prefetch(lw.ln2_g, d, g2);
   vec_prefetch(lw.ln2_b, d, b2);
   bool have_x = false;
+  float* red = m.big;             // [8][32][SM]
+  float* wpart = red + 256 * SM;  // [4][kPartWords]
   for (; it < nitems; it += gr.size) {
     const int ch = it % p.ncc, gh = it / p.ncc, h = gh % H, grp = gh / H;
     const int k0 = ch * p.chc;
     const int n = min(p.chc, p.A - k0);
     const size_t base = ((((size_t)grp * L + l) * H + h) * p.A + k0) * kHeadDim;
     auto off = [=](int j) -> size_t { return base + (size_t)j * kHeadDim; };
-    WBatch<2, kNB> wq;
-    gemvb_prefetch<2, kNB, WQ8>(lw.w_cq, lw.s_cq, d, d, (h * kHeadDim) >> 3, 1, kNB, wq);
-    const float bq = tid < kHeadDim ? lw.b_cq[h * kHeadDim + tid] : 0.f;
+    WBatch<R, kNB> wq;
+    gemvb_prefetch<R, kNB, WQ8>(lw.w_cq, lw.s_cq, d, d, (h * kHeadDim) >> 3, 1, kNB, wq);
+    float bq[8];
+    bias8(lw.b_cq, h * kHeadDim, bq);
     KVRegs<KPT_CROSS> kr;
     attn_prefetch<KPT_CROSS, 0>(p.xk, p.xv, (size_t)p.X * L * H * p.A * kHeadDim * 2, off, n, kr);
     if (!have_x) {
       if (!ll_poll1<8>(rep(p, p.x1 + (size_t)l * S * d), S * d, m.xin, c.tag, p.err)) return false;
       STAMP(1);
-      wg_layernorm_r(m.xin, m.xn, S, d, g2, b2, m.scr);
+      for (int s = 0; s < S; ++s) ln_row(m.xin + s * d, m.xn + s * d, d, g2, b2);
       have_x = true;
     }
-    float* q = m.big;                      // [ns][64]
-    float* pmv = q + SM * kHeadDim;        // [8]
-    float* plv = pmv + 8;                  // [8]
-    float* acc = plv + 8;                  // [ns][64]
-    float* red = acc + SM * kHeadDim;      // [4][SM][64]
-    float* sc = red + 4 * SM * kHeadDim;   // [ns][kMaxChunk + 4]
     const float* xs = m.xn + (p.X == 1 ? 0 : grp) * d;
-    gemvb_compute<2, kNB, WQ8, SM>(wq, lw.w_cq, lw.s_cq, d, d, (h * kHeadDim) >> 3, 1, kNB, ns, xs, m.red, m.gout);
-    if (tid < kHeadDim) {
-      for (int s = 0; s < ns; ++s) q[s * kHeadDim + tid] = m.gout[((tid >> 3) * SM + s) * 8 + (tid & 7)] + bq;
-    }
+    if (ns == 1)
+      gemv_rxm<1, R, kNB, WQ8>(wq, xs, 1, d, lw.w_cq, lw.s_cq, d, (h * kHeadDim) >> 3, 1, red);
+    else
+      gemv_rxm<SM, R, kNB, WQ8>(wq, xs, ns, d, lw.w_cq, lw.s_cq, d, (h * kHeadDim) >> 3, 1, red);
     lds_barrier();
-    attn_compute<KPT_CROSS, SM>(kr, n, ns, q, nullptr, nullptr, 0.125f, sc, kMaxChunk + 4, red, pmv, plv, acc);
-    STAMP(2);
-    for (int i = tid; i < ns * kPartWords; i += kThreads) {
-      const int s = i / kPartWords, w = i - s * kPartWords;
-      const int row = p.X == 1 ? s : grp;
+    for (int q = 0; q < ns; ++q) {
+      float Q[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Q[e] = (ns == 1 ? gemv_outm<1>(red, sub, e, 0) : gemv_outm<SM>(red, sub, e, q)) + bq[e];
+      float M, Ls, A;
+      attn_rx<KPT_CROSS>(kr, n, Q, 0.125f, wpart, M, Ls, A);
+      STAMP(2);
+      const int row = p.X == 1 ? q : grp;
       u64* dst = p.cp + ((((size_t)l * p.ncc + ch) * S + row) * H + h) * kPartWords;
-      ll_st(dst + w, w == 0 ? pmv[s] : (w == 1 ? plv[s] : acc[s * kHeadDim + w - 2]), c.tag, p.rep_stride);
+      if (tid < 64) {
+        ll_st(dst + 2 + tid, A, c.tag, p.rep_stride);
+        if (tid == 0) {
+          ll_st(dst + 0, M, c.tag, p.rep_stride);
+          ll_st(dst + 1, Ls, c.tag, p.rep_stride);
+        }
+      }
+      lds_barrier();
     }
   }
   return true;
@@ -1518,8 +1609,7 @@ DEV bool phase_cross(const StepParams& p, const Lds& m, const StepCtx& c, int l,
 // LN3 + MLP1 + GELU.
 template <int SM, int WQ8>
 DEV bool phase_mlp1(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
-  constexpr int NBM = 4;            // items whose weights are prefetched before the poll
-  constexpr int RM = WQ8 ? 2 : 4;   // 16-byte chunks per lane and row kept in registers
+  constexpr int R = 2, NBM = 4;
   const int tid = threadIdx.x, S = p.S, d = p.d, d4 = 4 * d;
   const LayerDev& lw = p.layers[l];
   const int nitems = (d4 + 7) / 8;
@@ -1527,32 +1617,36 @@ DEV bool phase_mlp1(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
   if (it0 >= nitems) return true;
   STAMP(0);
   const int nmine = (nitems - it0 + gr.size - 1) / gr.size;
-  WBatch<RM, NBM> wr;
-  gemvb_prefetch<RM, NBM, WQ8>(lw.w_1, lw.s_1, d4, d, it0, gr.size, min(NBM, nmine), wr);
+  WBatch<R, NBM> wr;
+  gemvb_prefetch<R, NBM, WQ8>(lw.w_1, lw.s_1, d4, d, it0, gr.size, min(NBM, nmine), wr);
+  // thread -> (item tid / (S * 8), row s, row-in-item tid % 8)
+  auto row_of = [&](int b) -> int { return (it0 + (b + tid / (S * 8)) * gr.size) * 8 + (tid & 7); };
   auto bias_of = [&](int b) -> float {
-    const int nit = min(NBM, nmine - b);
-    if (tid >= nit * S * 8) return 0.f;
-    const int i = tid / (S * 8), row = (it0 + (b + i) * gr.size) * 8 + (tid & 7);
-    return row < d4 ? lw.b_1[row] : 0.f;
+    const int nit = min(NBM, nmine - b), row = row_of(b);
+    return (tid < nit * S * 8 && row < d4) ? lw.b_1[row] : 0.f;
   };
   float bv = bias_of(0);
   VecRegs g3, b3;
   vec_prefetch(lw.ln3_g, d, g3);
   vec_prefetch(lw.ln3_b, d, b3);
+  float* red = m.big;  // [2][NBM * 32 * SM]
   if (!ll_poll1<8>(rep(p, p.x2 + (size_t)l * S * d), S * d, m.xin, c.tag, p.err)) return false;
   STAMP(1);
-  wg_layernorm_r(m.xin, m.xn, S, d, g3, b3, m.scr);
-  for (int b = 0; b < nmine; b += NBM) {
+  for (int s = 0; s < S; ++s) ln_row(m.xin + s * d, m.xn + s * d, d, g3, b3);
+  for (int b = 0, k = 0; b < nmine; b += NBM, ++k) {
     const int nit = min(NBM, nmine - b);
     if (b > 0) {
-      gemvb_prefetch<RM, NBM, WQ8>(lw.w_1, lw.s_1, d4, d, it0 + b * gr.size, gr.size, nit, wr);
+      gemvb_prefetch<R, NBM, WQ8>(lw.w_1, lw.s_1, d4, d, it0 + b * gr.size, gr.size, nit, wr);
       bv = bias_of(b);
     }
-    gemvb_compute<RM, NBM, WQ8, SM>(wr, lw.w_1, lw.s_1, d4, d, it0 + b * gr.size, gr.size, nit, S, m.xn, m.red, m.gout);
+    float* rb = red + (k & 1) * NBM * 32 * SM;
+    gemv_rxm<SM, R, NBM, WQ8>(wr, m.xn, S, d, lw.w_1, lw.s_1, d4, it0 + b * gr.size, gr.size, rb);
+    lds_barrier();
     if (tid < nit * S * 8) {
-      const int i = tid / (S * 8), rem = tid - i * S * 8, s = rem >> 3, rr = rem & 7;
-      const int row = (it0 + (b + i) * gr.size) * 8 + rr;
-      if (row < d4) ll_st(p.hm + ((size_t)l * S + s) * d4 + row, gelu_f16(m.gout[(i * SM + s) * 8 + rr] + bv), c.tag, p.rep_stride);
+      const int i = tid / (S * 8), s = (tid - i * S * 8) >> 3, rr = tid & 7;
+      const int row = row_of(b);
+      if (row < d4)
+        ll_st(p.hm + ((size_t)l * S + s) * d4 + row, gelu_f16(gemv_outm<SM>(rb, i, rr, s) + bv), c.tag, p.rep_stride);
     }
     STAMP(2);
   }
@@ -1562,7 +1656,7 @@ DEV bool phase_mlp1(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
 // MLP2 + bias + residual (the workgroup's own x2 rows, kept in LDS by the cross-out phase).
 template <int SM, int WQ8>
 DEV bool phase_mlp2(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
-  constexpr int NBM = 1;  // items whose weights are prefetched before the poll (8 chunks per lane and row)
+  constexpr int R = 8;
   const int tid = threadIdx.x, S = p.S, d = p.d, d4 = 4 * d;
   const LayerDev& lw = p.layers[l];
   const int nitems = (d + 7) / 8;
@@ -1570,29 +1664,27 @@ DEV bool phase_mlp2(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
   if (it0 >= nitems) return true;
   STAMP(0);
   const int nmine = (nitems - it0 + gr.size - 1) / gr.size;
-  WBatch<8, NBM> wr;
-  gemvb_prefetch<8, NBM, WQ8>(lw.w_2, lw.s_2, d, d4, it0, gr.size, min(NBM, nmine), wr);
-  auto row_of = [&](int b) -> int { return (it0 + (b + tid / (S * 8)) * gr.size) * 8 + (tid & 7); };
-  auto bias_of = [&](int b) -> float {
-    const int nit = min(NBM, nmine - b), row = row_of(b);
-    return (tid < nit * S * 8 && row < d) ? lw.b_2[row] : 0.f;
-  };
-  float bv = bias_of(0);
+  WBatch<R, 1> wr;
+  gemvb_prefetch<R, 1, WQ8>(lw.w_2, lw.s_2, d, d4, it0, gr.size, 1, wr);
+  const bool mine = tid < S * 8;
+  auto row_of = [&](int b) -> int { return (it0 + b * gr.size) * 8 + (tid & 7); };
+  float bv = (mine && row_of(0) < d) ? lw.b_2[row_of(0)] : 0.f;
+  float* red = m.big;  // [2][32 * SM]
   if (!ll_poll1<16>(rep(p, p.hm + (size_t)l * S * d4), S * d4, m.xin, c.tag, p.err)) return false;
   STAMP(1);
-  for (int b = 0; b < nmine; b += NBM) {
-    const int nit = min(NBM, nmine - b);
+  for (int b = 0; b < nmine; ++b) {
     if (b > 0) {
-      gemvb_prefetch<8, NBM, WQ8>(lw.w_2, lw.s_2, d, d4, it0 + b * gr.size, gr.size, nit, wr);
-      bv = bias_of(b);
+      gemvb_prefetch<R, 1, WQ8>(lw.w_2, lw.s_2, d, d4, it0 + b * gr.size, gr.size, 1, wr);
+      bv = (mine && row_of(b) < d) ? lw.b_2[row_of(b)] : 0.f;
     }
-    gemvb_compute<8, NBM, WQ8, SM>(wr, lw.w_2, lw.s_2, d, d4, it0 + b * gr.size, gr.size, nit, S, m.xin, m.red, m.gout);
-    if (tid < nit * S * 8) {
-      const int i = tid / (S * 8), rem = tid - i * S * 8, s = rem >> 3, rr = rem & 7;
-      const int row = row_of(b);
+    float* rb = red + (b & 1) * 32 * SM;
+    gemv_rxm<SM, R, 1, WQ8>(wr, m.xin, S, d4, lw.w_2, lw.s_2, d, it0 + b * gr.size, gr.size, rb);
+    lds_barrier();
+    if (mine) {
+      const int s = tid >> 3, rr = tid & 7, row = row_of(b);
       if (row < d) {
-        float* rs = m.res + ((b + i) * S + s) * 8 + rr;
-        const float y = *rs + (m.gout[(i * SM + s) * 8 + rr] + bv);
+        float* rs = m.res + (b * S + s) * 8 + rr;
+        const float y = *rs + (gemv_outm<SM>(rb, 0, rr, s) + bv);
         *rs = y;
         ll_st(p.x3 + ((size_t)l * S + s) * d + row, y, c.tag, p.rep_stride);
       }
@@ -1602,61 +1694,81 @@ DEV bool phase_mlp2(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
   return true;
 }
 
-// Final LN + tied-embedding logits over this workgroup's 8-row vocabulary items (items g, g+G, ...,
-// taken kNB at a time with the next batch's weights in flight), masks, and the workgroup's
-// selection partial (a full record and a (max, argmax) pair).
-template <int SM, int WQ8>
-DEV void logits_batch(const StepParams& p, const Lds& m, const StepCtx& c, const WBatch<2, kNB>& wb, int b,
-                      int nmine, float* lg, float* rw, int* lidx, int rpw) {
-  const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x, S = p.S, V = p.V, d = p.d;
-  const int nit = min(kNB, nmine - b * kNB);
-  gemvb_compute<2, kNB, WQ8, SM>(wb, p.emb, p.emb_s, V, d, g + b * kNB * G, G, nit, S, m.xn, m.red, m.gout);
-  for (int idx = tid; idx < nit * S * 8; idx += kThreads) {
-    const int i = idx / (S * 8), rem = idx - i * S * 8, s = rem >> 3, rr = rem & 7;
-    const int row = (g + (b * kNB + i) * G) * 8 + rr, li = (b * kNB + i) * 8 + rr;
-    if (row < V) {
-      const float v = m.gout[(i * SM + s) * 8 + rr];
-      rw[s * rpw + li] = v;
-      lg[s * rpw + li] = (masked(p.mask, p.mw, s, row) || masked(p.mask2, p.mw, s, row)) ? -INFINITY : v;
-      if (s == 0) lidx[li] = row;
-      if (p.logits_out) p.logits_out[((size_t)c.st * S + s) * V + row] = v;
-    } else if (s == 0) {
-      lidx[li] = -1;
-    }
-  }
-}
-
+// Final LN + tied-embedding logits over this workgroup's 8-row vocabulary items (items g, g+G, ...)
+// + masks + the workgroup's selection partial per row (a full record and a (max, argmax) pair).
+// One-row sessions keep the first nres items resident in LDS; the rest are streamed, two batches
+// in flight before the poll.
 template <int SM, int WQ8>
 DEV bool phase_logits(const StepParams& p, const Lds& m, const StepCtx& c) {
+  constexpr int R = 2, NBL = SM == 1 ? kNB : 4;
   const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x, S = p.S, d = p.d, V = p.V;
   const int nitems = (V + 7) / 8;
   const int nmine = g < nitems ? (nitems - g + G - 1) / G : 0;
-  const int nb = (nmine + kNB - 1) / kNB;
+  const int nr = SM == 1 ? min(p.nres, nmine) : 0;  // items resident in LDS
+  const int nst = nmine - nr;                       // items streamed from memory
+  const int nb = (nst + NBL - 1) / NBL;
   const int rpw = p.rows_per_wg;
   float* lg = m.big;                                  // [S][rpw] masked
   float* rw = lg + S * rpw;                           // [S][rpw] raw
   int* lidx = reinterpret_cast<int*>(rw + S * rpw);   // [rpw]
   float* rec = reinterpret_cast<float*>(lidx + rpw);  // [S][kSelWords]
-  WBatch<2, kNB> wa, wb;
+  float* red = rec + S * kSelWords;                   // [2][NBL * 32 * SM]
+  WBatch<R, NBL> wa, wb;
   STAMP(0);
-  if (nb > 0) gemvb_prefetch<2, kNB, WQ8>(p.emb, p.emb_s, V, d, g, G, min(kNB, nmine), wa);
+  if (nb > 0) gemvb_prefetch<R, NBL, WQ8>(p.emb, p.emb_s, V, d, g + nr * G, G, min(NBL, nst), wa);
+  if (nb > 1) gemvb_prefetch<R, NBL, WQ8>(p.emb, p.emb_s, V, d, g + (nr + NBL) * G, G, min(NBL, nst - NBL), wb);
   VecRegs gf, bf;
   vec_prefetch(p.lnf_g, d, gf);
   vec_prefetch(p.lnf_b, d, bf);
   if (!ll_poll1<8>(rep(p, p.x3 + (size_t)(p.L - 1) * S * d), S * d, m.xin, c.tag, p.err)) return false;
   STAMP(1);
-  wg_layernorm_r(m.xin, m.xn, S, d, gf, bf, m.scr);
+  for (int s = 0; s < S; ++s) ln_row(m.xin + s * d, m.xn + s * d, d, gf, bf);
+  int nbat = 0;  // batches done (alternates the reduction buffers)
+  // outputs of a batch of nit items starting at local item i0
+  auto emit = [&](const float* rb, int i0, int nit) {
+    if (tid < nit * S * 8) {
+      const int i = tid / (S * 8), s = (tid - i * S * 8) >> 3, rr = tid & 7;
+      const int row = (g + (i0 + i) * G) * 8 + rr, li = (i0 + i) * 8 + rr;
+      if (row < V) {
+        const float v = gemv_outm<SM>(rb, i, rr, s);
+        rw[s * rpw + li] = v;
+        lg[s * rpw + li] = (masked(p.mask, p.mw, s, row) || masked(p.mask2, p.mw, s, row)) ? -INFINITY : v;
+        if (s == 0) lidx[li] = row;
+        if (p.logits_out) p.logits_out[((size_t)c.st * S + s) * V + row] = v;
+      } else if (s == 0) {
+        lidx[li] = -1;
+      }
+    }
+  };
+  if constexpr (SM == 1) {
+    XR<R, WQ8> X;
+    xr_load<R, WQ8>(m.xn, d, X);
+    for (int b = 0; b < nr; b += kNB, ++nbat) {
+      const int nit = min(kNB, nr - b);
+      float* rb = red + (nbat & 1) * NBL * 32 * SM;
+      gemv_lds<R, kNB, WQ8>(m.ew + (size_t)b * R * kThreads, m.es + (size_t)b * R * kThreads, nit, X, rb);
+      lds_barrier();
+      emit(rb, b, nit);
+    }
+  }
+  auto batch = [&](const WBatch<R, NBL>& w, int b) {
+    const int nit = min(NBL, nst - b * NBL);
+    float* rb = red + (nbat & 1) * NBL * 32 * SM;
+    ++nbat;
+    gemv_rxm<SM, R, NBL, WQ8>(w, m.xn, S, d, p.emb, p.emb_s, V, g + (nr + b * NBL) * G, G, rb);
+    lds_barrier();
+    emit(rb, nr + b * NBL, nit);
+  };
   for (int b = 0; b < nb; b += 2) {
-    if (b + 1 < nb) gemvb_prefetch<2, kNB, WQ8>(p.emb, p.emb_s, V, d, g + (b + 1) * kNB * G, G, min(kNB, nmine - (b + 1) * kNB), wb);
-    logits_batch<SM, WQ8>(p, m, c, wa, b, nmine, lg, rw, lidx, rpw);
+    if (b > 0 && b + 1 < nb) gemvb_prefetch<R, NBL, WQ8>(p.emb, p.emb_s, V, d, g + (nr + (b + 1) * NBL) * G, G, min(NBL, nst - (b + 1) * NBL), wb);
+    batch(wa, b);
     if (b + 1 < nb) {
-      if (b + 2 < nb) gemvb_prefetch<2, kNB, WQ8>(p.emb, p.emb_s, V, d, g + (b + 2) * kNB * G, G, min(kNB, nmine - (b + 2) * kNB), wa);
-      logits_batch<SM, WQ8>(p, m, c, wb, b + 1, nmine, lg, rw, lidx, rpw);
+      if (b + 2 < nb) gemvb_prefetch<R, NBL, WQ8>(p.emb, p.emb_s, V, d, g + (nr + (b + 2) * NBL) * G, G, min(NBL, nst - (b + 2) * NBL), wa);
+      batch(wb, b + 1);
     }
   }
   lds_barrier();
   STAMP(2);
-  // compact: rows beyond V (only in the last item) carry lidx -1 and sit at the end
   int nl = nmine * 8;
   if (nmine > 0) {
     const int last_row0 = (g + (nmine - 1) * G) * 8;
@@ -1670,7 +1782,8 @@ DEV bool phase_logits(const StepParams& p, const Lds& m, const StepCtx& c) {
   // selection, which waits on every workgroup's partial.
   kv_drain();
   for (int i = tid; i < S * kSelWords; i += kThreads) ll_st(p.lp + (size_t)g * S * kSelWords + i, rec[i], c.tag, p.rep_stride);
-  for (int i = tid; i < 2 * S; i += kThreads) ll_st(p.lpa + (size_t)g * S * 2 + i, rec[(i >> 1) * kSelWords + (i & 1)], c.tag, p.rep_stride);
+  for (int i = tid; i < 2 * S; i += kThreads)
+    ll_st(p.lpa + (size_t)g * S * 2 + i, rec[(i >> 1) * kSelWords + (i & 1)], c.tag, p.rep_stride);
   return true;
 }
 
@@ -1723,16 +1836,10 @@ DEV bool phase_reduce(const StepParams& p, const Lds& m, const StepCtx& c) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// S = 1 phases (one row: greedy decode of one stream), built on the straight-line blocks above.
-// Same items, exchange buffers and publication order as the general phases.
-
-// Bias chunk of a lane for a 64-row head block: o[e] = b[base + (thread % 8) * 8 + e].
-DEV void bias8(const float* b, int base, float (&o)[8]) {
-  const float4* q = reinterpret_cast<const float4*>(b + base + (threadIdx.x & 7) * 8);
-  const float4 a = q[0], c = q[1];
-  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
-  o[4] = c.x; o[5] = c.y; o[6] = c.z; o[7] = c.w;
-}
+// One-row phases (SM = 1: greedy decode of one stream).  Same items, exchange buffers and
+// publication order as the phases above, specialised for one row: a lane's activation chunks stay
+// in registers across both projections of an item, and the logits read part of the vocabulary
+// from LDS.
 
 template <int WQ8>
 DEV bool phase_self1(const StepParams& p, const Lds& m, const StepCtx& c, int l, Grp gr) {
@@ -2143,9 +2250,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
   m.res = m.scr + 8 + kMaxRows;
   m.xin = m.res + kResItems * kMaxRows * 8;
   m.xn = m.xin + S * 4 * d;
-  m.red = m.xn + S * d;
-  m.gout = m.red + kNB * 32 * SM;
-  m.big = m.gout + kNB * SM * 8;
+  m.big = m.xn + S * d;
   m.ew = reinterpret_cast<uint4*>(reinterpret_cast<char*>(lds_raw) + p.res_off);
   m.es = reinterpret_cast<uint16_t*>(m.ew + (size_t)p.nres * 2 * kThreads);
   if (tid < S) m.toks[tid] = p.tokens0[tid];
@@ -2402,30 +2507,32 @@ __global__ void __launch_bounds__(64) k_op_select_final(const float* parts, int 
 // launchers
 
 size_t step_lds_bytes(const StepParams& p, int grid) {
+  // in floats: persistent words, then the per-phase region [xin S*4d][xn S*d][big]
   const int S = p.S, d = p.d, SM = S > 1 ? kMaxRows : 1;
   const size_t persistent = 8 + kMaxRows + kResItems * kMaxRows * 8;
-  const size_t fixed = (size_t)S * 4 * d + (size_t)S * d + kNB * 32 * SM + kNB * SM * 8;
-  const size_t self_attn = 2 * kHeadDim + 16 + kHeadDim + kSelfChunk + 4 + 16 * kHeadDim;
-  const size_t cross_attn = SM * kHeadDim + 16 + SM * kHeadDim + 16 * SM * kHeadDim + (size_t)SM * (kMaxChunk + 4);
+  const size_t fixed = (size_t)S * 4 * d + (size_t)S * d;
   const size_t mp = (size_t)(p.ncs_max > p.ncc ? p.ncs_max : p.ncc) * S * p.H * kPartWords;
-  // one-row out phases: partials + two reduction buffers in big; general out phases: partials,
-  // merged output and GEMV scratch from the start of the per-phase region
-  const size_t merge_self = S == 1 ? mp + 512 : 0;
-  const size_t merge_cross = merge_self;
-  const size_t out_general = S == 1 ? 0 : mp + (size_t)S * d + kNB * 32 * SM + kNB * SM * 8;
-  const size_t logits = (size_t)2 * S * p.rows_per_wg + p.rows_per_wg + (size_t)S * kSelWords + 512;
-  const size_t fast_attn = 512 + 4 * kPartWords;
+  const size_t self_attn = 512 + 4 * kPartWords;                   // two reductions + wave partials
+  const size_t cross_attn = (size_t)kNB * 32 * SM + 4 * kPartWords;  // reduction + wave partials
+  const size_t mlp1 = (size_t)2 * 4 * 32 * SM;
+  const size_t mlp2 = SM == 1 ? 512 : (size_t)2 * 32 * SM;  // phase_mlp2_1 uses two 256-float buffers
+  const size_t nbl = SM == 1 ? kNB : 4;
+  const size_t logits = (size_t)2 * S * p.rows_per_wg + p.rows_per_wg + (size_t)S * kSelWords + 2 * nbl * 32 * SM;
   const int nblk = (grid + kRedBlock - 1) / kRedBlock;
   size_t reduce = (size_t)(kRedBlock + nblk + 1) * S * kSelWords;
   if ((size_t)grid * S * 2 > reduce) reduce = (size_t)grid * S * 2;
+  // out phases: one row keeps partials + reductions in big; several rows put partials, merged
+  // output and reductions at the start of the region
+  const size_t out_one = S == 1 ? mp + 512 : 0;  // phase_out1: partials + two 256-float reductions
+  const size_t out_rows = S == 1 ? 0 : mp + (size_t)S * d + 2 * 32 * SM;
   size_t big = self_attn;
-  big = big > fast_attn ? big : fast_attn;
   big = big > cross_attn ? big : cross_attn;
-  big = big > merge_self ? big : merge_self;
-  big = big > merge_cross ? big : merge_cross;
+  big = big > mlp1 ? big : mlp1;
+  big = big > mlp2 ? big : mlp2;
   big = big > logits ? big : logits;
   big = big > reduce ? big : reduce;
-  const size_t region = fixed + big > out_general ? fixed + big : out_general;
+  big = big > out_one ? big : out_one;
+  const size_t region = fixed + big > out_rows ? fixed + big : out_rows;
   return (persistent + region) * sizeof(float);
 }
 
