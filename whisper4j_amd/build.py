@@ -22,8 +22,11 @@ DEVICE_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-Wall",
 CLANG = os.environ.get("W4H_HOST_CXX", "/opt/rocm/lib/llvm/bin/clang++")
 # Host-only translation units: plain C++ against the HIP runtime API (no device code).
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include"]
-SOURCES = [("w4h_device.hip", HIPCC, DEVICE_FLAGS), ("w4h_api.cpp", CLANG, HOST_FLAGS),
-           ("w4h_ggml.cpp", CLANG, HOST_FLAGS), ("w4h_decode.cpp", CLANG, HOST_FLAGS)]
+# Step-kernel instances (rows x weight type x register rounds), one translation unit each so they
+# compile in parallel; the shared device code is w4h_kernels.h.
+STEP_VARIANTS = ["1_f16_r2", "1_f16_r3", "1_q8_r2", "8_f16_r2", "8_f16_r3", "8_q8_r2"]
+SOURCES = ([("w4h_device.hip", HIPCC, DEVICE_FLAGS)] + [(f"w4h_step_{v}.hip", HIPCC, DEVICE_FLAGS) for v in STEP_VARIANTS] +
+           [("w4h_api.cpp", CLANG, HOST_FLAGS), ("w4h_ggml.cpp", CLANG, HOST_FLAGS), ("w4h_decode.cpp", CLANG, HOST_FLAGS)])
 
 
 def _compile(src, cxx, flags):
@@ -39,7 +42,7 @@ def _compile(src, cxx, flags):
 
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
         results = list(ex.map(lambda s: _compile(*s), SOURCES))
     if verbose:
         for _, msg in results:

@@ -594,14 +594,17 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   probe_p.rows_per_wg = s->rpw;
   s->lds = step_lds_bytes(probe_p, s->grid);
   // One-row sessions keep the first vocabulary items of each workgroup's logits share resident in
-  // the LDS left over by the step (two 16-byte chunks per thread and item, plus q8_0 scales).
+  // the LDS left over by the step (step_rounds 16-byte chunks per thread and item, plus q8_0 scales).
   s->res_off = (s->lds + 15) & ~(size_t)15;
   if (s->S == 1) {
-    const size_t item_bytes = (size_t)2 * kThreads * 16 + (m->wq8 ? (size_t)2 * kThreads * 2 : 0);
+    const int dr = step_rounds(d, m->wq8);
+    const size_t item_bytes = (size_t)dr * kThreads * 16 + (m->wq8 ? (size_t)dr * kThreads * 2 : 0);
     const size_t limit = (size_t)prop.sharedMemPerBlock;
     const size_t avail = limit > s->res_off + 1024 ? limit - s->res_off - 1024 : 0;
     const int nmine = ((V + 7) / 8 + s->grid - 1) / s->grid;
-    s->nres = (int)std::min<size_t>((size_t)nmine, avail / item_bytes);
+    // resident rows hold only the register rounds, so rows longer than those rounds are streamed
+    const bool rows_fit = d <= (m->wq8 ? 512 : 256) * dr;
+    s->nres = rows_fit ? (int)std::min<size_t>((size_t)nmine, avail / item_bytes) : 0;
     if (const char* e = getenv("W4H_NRES")) s->nres = std::max(0, std::min(s->nres, atoi(e)));
     s->lds = s->res_off + (size_t)s->nres * item_bytes;
   }

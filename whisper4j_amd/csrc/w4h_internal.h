@@ -65,6 +65,12 @@ struct StepParams {
   unsigned long long* trace;    // [nsteps][6L+2][grid] phase-end timestamps (wall clock) or null
 };
 
+// 16-byte weight chunks per lane and weight row kept in registers by the step kernel's GEMVs over
+// d (32 lanes cover a row, so a row of d halves needs d / 256 rounds, of d int8 values d / 512):
+// 2 rounds for d <= 512 (f16) / d <= 1024 (q8_0), 3 for wider f16 rows; anything past the prefetched
+// rounds is streamed inside the GEMV.
+inline int step_rounds(int d, int wq8) { return wq8 ? 2 : (d <= 512 ? 2 : 3); }
+
 // Launchers (return the HIP error of the launch).
 hipError_t launch_step(const StepParams& p, int grid, size_t lds_bytes, hipStream_t st);
 size_t step_lds_bytes(const StepParams& p, int grid);
