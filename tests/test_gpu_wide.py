@@ -34,12 +34,14 @@ def forced_rows(gpu, dims, T, xas, prompt, forced, n_rows, n_enc):
     return out
 
 
-@pytest.mark.parametrize("d,heads,n_rows,n_enc", [(768, 12, 1, 1), (768, 12, 3, 1), (1024, 16, 1, 1),
-                                                  (1024, 16, 2, 2)])
-def test_wide_forced(gpu, orc, d, heads, n_rows, n_enc):
+@pytest.mark.parametrize("d,heads,n_rows,n_enc,wtype", [(768, 12, 1, 1, "f16"), (768, 12, 3, 1, "f16"),
+                                                        (1024, 16, 1, 1, "f16"), (1024, 16, 2, 2, "f16"),
+                                                        (1024, 16, 1, 1, "q8_0"), (1280, 20, 1, 1, "f16"),
+                                                        (1280, 20, 4, 4, "f16")])
+def test_wide_forced(gpu, orc, d, heads, n_rows, n_enc, wtype):
     dims = synth.Dims(n_vocab=1200, n_text_ctx=48, n_text_state=d, n_text_head=heads, n_text_layer=2, n_audio_ctx=80)
-    say(f"d={d} heads={heads} rows={n_rows} encoders={n_enc}")
-    T = synth.make_decoder(dims, seed=31, ln_random=True)
+    say(f"d={d} heads={heads} rows={n_rows} encoders={n_enc} {wtype}")
+    T = synth.make_decoder(dims, seed=31, wtype=wtype, ln_random=True)
     xas = [synth.encoder_output(dims, 31, stream=e) for e in range(n_enc)]
     prompt, forced = [1, 2, 3], synth.forced_tokens(12, 31, high=dims.n_vocab - 1)
     om = orc.Model(dims, T)
