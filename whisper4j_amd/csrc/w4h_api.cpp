@@ -412,6 +412,11 @@ struct w4h_session {
   std::vector<int32_t> slots_host;
   bool slots_identity = true, slots_dirty = false;
   bool closed = false;
+  // batched (wide) engine
+  bool wide = false;
+  int Rp = 0, nch = 0, chlen = 0, nsel = 0;
+  WideGemm g_qkv{}, g_o{}, g_cq{}, g_co{}, g_1{}, g_2{}, g_v{};
+  DevBuf wx, wact, wpa, wpb, wcpart, wselp, wnext;
 };
 
 namespace w4h {
@@ -465,6 +470,54 @@ static StepParams base_params(w4h_session* s) {
   return p;
 }
 
+static WideParams wide_params(w4h_session* s) {
+  w4h_model* m = s->m;
+  WideParams p{};
+  p.layers = m->layers.data();
+  p.L = m->dims.n_text_layer;
+  p.d = m->dims.n_text_state;
+  p.H = m->dims.n_text_head;
+  p.V = m->dims.n_vocab;
+  p.C = m->dims.n_text_ctx;
+  p.A = m->dims.n_audio_ctx;
+  p.wq8 = m->wq8;
+  p.emb = m->emb;
+  p.emb_s = m->emb_s;
+  p.pos = m->pos;
+  p.lnf_g = m->lnf_g;
+  p.lnf_b = m->lnf_b;
+  p.S = s->S;
+  p.X = s->X;
+  p.max_ctx = s->max_ctx;
+  p.Rp = s->Rp;
+  p.kv_k = s->kvk.as<uint16_t>();
+  p.kv_v = s->kvv.as<uint16_t>();
+  p.xk = s->xk.as<uint16_t>();
+  p.xv = s->xv.as<uint16_t>();
+  p.slots = s->slots_identity ? nullptr : s->slots.as<int32_t>();
+  p.x = s->wx.as<float>();
+  p.act = s->wact.as<float>();
+  p.pa = s->wpa.as<float>();
+  p.pb = s->wpb.as<float>();
+  p.cpart = s->wcpart.as<float>();
+  p.selp = s->wselp.as<float>();
+  p.next_tok = s->wnext.as<int32_t>();
+  p.nch = s->nch;
+  p.chlen = s->chlen;
+  p.nsel = s->nsel;
+  p.g_qkv = s->g_qkv;
+  p.g_o = s->g_o;
+  p.g_cq = s->g_cq;
+  p.g_co = s->g_co;
+  p.g_1 = s->g_1;
+  p.g_2 = s->g_2;
+  p.g_v = s->g_v;
+  p.mask = s->has_mask ? s->mask.as<uint32_t>() : nullptr;
+  p.mw = s->mw;
+  p.probe = s->probe;
+  return p;
+}
+
 static int ensure(DevBuf& b, size_t bytes) {
   if (b.n >= bytes) return W4H_OK;
   return b.alloc(bytes);
@@ -507,6 +560,38 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
   const size_t trace_n = (size_t)n_steps * (6 * s->m->dims.n_text_layer + 2) * 4 * s->grid;
   if (trace && (rc = ensure(s->trace, trace_n * sizeof(uint64_t)))) return rc;
   HIPCHK(hipMemsetAsync(s->err.p, 0, sizeof(unsigned), s->stream));
+  if (s->wide) {
+    if (trace) return fail(W4H_ERR_INVALID, "phase traces are recorded by the persistent step kernel only");
+    WideParams wp = wide_params(s);
+    wp.nsteps = n_steps;
+    wp.kv_len0 = s->kv_len;
+    wp.tokens0 = s->toks.as<int32_t>();
+    wp.forced = (forced && n_steps > 1) ? s->forced.as<int32_t>() : nullptr;
+    wp.mask2 = extra_mask ? s->mask2.as<uint32_t>() : nullptr;
+    wp.topk = topk;
+    wp.out = out ? s->out.as<w4h_step_out>() : nullptr;
+    wp.logits_out = logits ? s->logits.as<float>() : nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (ms) {
+      HIPCHK(hipEventCreate(&e0));
+      HIPCHK(hipEventCreate(&e1));
+      HIPCHK(hipEventRecord(e0, s->stream));
+    }
+    hipError_t le = launch_wide(wp, s->stream);
+    if (le != hipSuccess) return fail(W4H_ERR_DEVICE, "batched step launch failed: %s", hipGetErrorString(le));
+    if (ms) HIPCHK(hipEventRecord(e1, s->stream));
+    if (out) HIPCHK(hipMemcpyAsync(out, s->out.p, sizeof(w4h_step_out) * (size_t)n_steps * s->S, hipMemcpyDeviceToHost, s->stream));
+    if (logits)
+      HIPCHK(hipMemcpyAsync(logits, s->logits.p, sizeof(float) * (size_t)n_steps * s->S * V, hipMemcpyDeviceToHost, s->stream));
+    HIPCHK(hipStreamSynchronize(s->stream));
+    if (ms) {
+      HIPCHK(hipEventElapsedTime(ms, e0, e1));
+      (void)hipEventDestroy(e0);
+      (void)hipEventDestroy(e1);
+    }
+    s->kv_len += n_steps;
+    return W4H_OK;
+  }
   StepParams p = base_params(s);
   p.nsteps = n_steps;
   p.kv_len0 = s->kv_len;
@@ -545,6 +630,62 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
   return W4H_OK;
 }
 
+// Session set-up for the batched engine: KV cache, cross K/V, slot table, GEMM slicing and the
+// work buffers (residual rows, GEMM input rows, GEMM partials, attention and selection partials).
+int create_wide(std::unique_ptr<w4h_session>& s, const hipDeviceProp_t& prop, w4h_session** out) {
+  w4h_model* m = s->m;
+  const w4h_dims& D = m->dims;
+  const int L = D.n_text_layer, d = D.n_text_state, H = D.n_text_head, A = D.n_audio_ctx, V = D.n_vocab;
+  if (d % kWideKBlock != 0 || d > 2048 || H * kHeadDim != d)
+    return fail(W4H_ERR_INVALID, "batched engine needs n_text_state a multiple of %d (<= 2048) and head size %d", kWideKBlock, kHeadDim);
+  const int ncu = prop.multiProcessorCount;
+  s->Rp = s->S <= 16 ? 16 : 32;
+  s->g_qkv = wide_plan(nullptr, nullptr, 3 * d, d, ncu);
+  s->g_o = wide_plan(nullptr, nullptr, d, d, ncu);
+  s->g_cq = s->g_o;
+  s->g_co = s->g_o;
+  s->g_1 = wide_plan(nullptr, nullptr, 4 * d, d, ncu);
+  s->g_2 = wide_plan(nullptr, nullptr, d, 4 * d, ncu);
+  s->g_v = wide_plan(m->emb, m->emb_s, V, d, ncu);
+  size_t pmax = 0;
+  for (const WideGemm* g : {&s->g_qkv, &s->g_o, &s->g_1, &s->g_2, &s->g_v})
+    pmax = std::max(pmax, (size_t)g->ks * s->Rp * g->N);
+  // cross-attention chunks: enough (encoder, head, chunk) workgroups for two per compute unit,
+  // chunks of at least 64 keys
+  const int ngroups = s->X == s->S ? 1 : (s->S + 7) / 8;
+  int nch = (2 * ncu + s->X * H * ngroups - 1) / (s->X * H * ngroups);
+  nch = std::max(1, std::min(nch, A / 64));
+  s->chlen = (A + nch - 1) / nch;
+  s->nch = (A + s->chlen - 1) / s->chlen;
+  s->nsel = (V + kWideSelChunk - 1) / kWideSelChunk;
+  int rc;
+  const size_t kv_elems = (size_t)L * s->S * H * s->max_ctx * kHeadDim;
+  if ((rc = s->kvk.alloc(kv_elems * 2)) || (rc = s->kvv.alloc(kv_elems * 2))) return rc;
+  const size_t x_elems = (size_t)s->X * L * H * A * kHeadDim;
+  if ((rc = s->xk.alloc(x_elems * 2)) || (rc = s->xv.alloc(x_elems * 2))) return rc;
+  HIPCHK(hipMemset(s->xk.p, 0, x_elems * 2));
+  HIPCHK(hipMemset(s->xv.p, 0, x_elems * 2));
+  s->slots_host.resize((size_t)s->S * s->max_ctx);
+  for (int r = 0; r < s->S; r++)
+    for (int q = 0; q < s->max_ctx; q++) s->slots_host[(size_t)r * s->max_ctx + q] = r;
+  if ((rc = upload(s->slots, s->slots_host.data(), s->slots_host.size() * 4))) return rc;
+  if ((rc = s->wx.alloc(sizeof(float) * (size_t)s->S * d))) return rc;
+  if ((rc = s->wact.alloc(sizeof(float) * (size_t)s->Rp * 4 * d))) return rc;
+  HIPCHK(hipMemset(s->wact.p, 0, sizeof(float) * (size_t)s->Rp * 4 * d));
+  if ((rc = s->wpa.alloc(sizeof(float) * pmax)) || (rc = s->wpb.alloc(sizeof(float) * pmax))) return rc;
+  if ((rc = s->wcpart.alloc(sizeof(float) * (size_t)s->S * H * s->nch * kPartWords))) return rc;
+  if ((rc = s->wselp.alloc(sizeof(float) * (size_t)s->S * s->nsel * kSelWords))) return rc;
+  if ((rc = s->wnext.alloc(sizeof(int32_t) * s->S))) return rc;
+  HIPCHK(hipStreamCreate(&s->stream));
+  if ((rc = s->err.alloc(256))) return rc;
+  HIPCHK(hipMemset(s->err.p, 0, 256));
+  if ((rc = s->mask.alloc(sizeof(uint32_t) * (size_t)s->S * s->mw))) return rc;
+  HIPCHK(hipDeviceSynchronize());
+  m->refs.fetch_add(1);
+  *out = s.release();
+  return W4H_OK;
+}
+
 }  // namespace w4h
 
 extern "C" {
@@ -554,8 +695,8 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   *out = nullptr;
   if (m->closed) return fail(W4H_ERR_CLOSED, "model destroyed");
   const w4h_dims& D = m->dims;
-  if (desc->n_rows < 1 || desc->n_rows > kMaxRows)
-    return fail(W4H_ERR_INVALID, "n_rows %d outside [1, %d]", desc->n_rows, kMaxRows);
+  if (desc->n_rows < 1 || desc->n_rows > kWideMaxRows)
+    return fail(W4H_ERR_INVALID, "n_rows %d outside [1, %d]", desc->n_rows, kWideMaxRows);
   if (desc->n_encoders != 1 && desc->n_encoders != desc->n_rows)
     return fail(W4H_ERR_INVALID, "n_encoders must be 1 or n_rows");
   if (desc->max_ctx < 1 || desc->max_ctx > 8192) return fail(W4H_ERR_INVALID, "max_ctx %d outside [1, 8192]", desc->max_ctx);
@@ -574,6 +715,14 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   hipDeviceProp_t prop;
   HIPCHK(hipGetDeviceProperties(&prop, m->device));
   s->grid = prop.multiProcessorCount;
+  // Engine: the persistent step kernel for up to kMaxRows rows, the batched MFMA engine beyond
+  // (W4H_ENGINE=wide or persistent overrides where both apply).
+  s->wide = s->S > kMaxRows;
+  if (const char* e = getenv("W4H_ENGINE")) {
+    if (!strcmp(e, "wide")) s->wide = true;
+    else if (!strcmp(e, "persistent") && s->S <= kMaxRows) s->wide = false;
+  }
+  if (s->wide) return create_wide(s, prop, out);
   // Phase groups (phase q runs on workgroup group q % ngroups, 1 or 2); W4H_NGROUPS overrides the
   // default of 2 for tuning.  A workgroup owns at most kResItems of the d/8 residual-row items.
   if (const char* e = getenv("W4H_NGROUPS")) {

@@ -71,6 +71,60 @@ struct StepParams {
 // rounds is streamed inside the GEMV.
 inline int step_rounds(int d, int wq8) { return wq8 ? 2 : (d <= 512 ? 2 : 3); }
 
+// Batched ("wide") step engine: rows that decode in lockstep (beams or independent streams, up to
+// kWideMaxRows) run as a sequence of ordinary kernels per token step, with every projection an MFMA
+// GEMM over all rows.  Row counts are padded to Rp = 16 or 32 (one or two 16-row MFMA tiles).
+constexpr int kWideMaxRows = 32;
+constexpr int kWideCols = 64;        // output columns per GEMM workgroup (16 per wave)
+constexpr int kWideKBlock = 128;     // k per block: four 16x16x32 MFMA steps
+constexpr int kWideSelChunk = 512;   // vocabulary entries per selection partial (one wave)
+
+// One GEMM of the wide engine: out[ks][Rp][N] = act[:, ks-th k slice] . W[N][K]^T.
+struct WideGemm {
+  const void* w;         // [N][K] f16, or int8 with f16 scales [N][K/32] in ws
+  const uint16_t* ws;
+  int N, K;
+  int kb;                // 128-blocks per k slice (1..4); slices = ceil(K / (128 kb))
+  int ks;                // number of k slices
+};
+
+struct WideParams {
+  // model
+  const LayerDev* layers;  // host array
+  int L, d, H, V, C, A, wq8;
+  const void* emb;
+  const uint16_t* emb_s;
+  const float* pos;
+  const float *lnf_g, *lnf_b;
+  // session
+  int S, X, max_ctx, Rp;
+  uint16_t *kv_k, *kv_v;    // [L][S][H][max_ctx][64]
+  const uint16_t *xk, *xv;  // [X][L][H][A][64]
+  const int32_t* slots;     // [S][max_ctx] or null
+  float* x;                 // [S][d] residual stream
+  float* act;               // [Rp][4d] GEMM input rows (rows >= S stay zero)
+  float *pa, *pb;           // GEMM partials, each [slices][Rp][N] (sized for the largest GEMM)
+  float* cpart;             // [S][H][nch][kPartWords] cross-attention chunk partials
+  float* selp;              // [S][nsel][kSelWords] selection partials
+  int32_t* next_tok;        // [S] argmax of the last step (greedy feedback)
+  int nch, chlen, nsel;
+  WideGemm g_qkv, g_o, g_cq, g_co, g_1, g_2, g_v;  // per-layer shapes and slicing; g_v = logits
+  // control
+  int nsteps, kv_len0;
+  const int32_t* tokens0;   // [S]
+  const int32_t* forced;    // [nsteps-1][S] or null
+  const uint32_t* mask;
+  const uint32_t* mask2;
+  int mw, probe, topk;
+  w4h_step_out* out;        // [nsteps][S] or null
+  float* logits_out;        // [nsteps][S][V] or null
+};
+
+// Enqueue p.nsteps wide steps on st.
+hipError_t launch_wide(const WideParams& p, hipStream_t st);
+// Slicing of one wide GEMM for a device with n_cu compute units.
+WideGemm wide_plan(const void* w, const uint16_t* ws, int N, int K, int n_cu);
+
 // Launchers (return the HIP error of the launch).
 hipError_t launch_step(const StepParams& p, int grid, size_t lds_bytes, hipStream_t st);
 size_t step_lds_bytes(const StepParams& p, int grid);
