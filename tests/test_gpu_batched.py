@@ -122,3 +122,59 @@ def test_batched_beam_driver(gpu, orc, monkeypatch):
     assert b.avg_logprob == pytest.approx(ob["avg_logprob"], abs=1e-3)
     bdec.close()
     m.close()
+
+
+def _session_script(gpu, dims, T, xas, n):
+    """Runs of different lengths, greedy feedback, a logits request, a suppress mask and a reorder
+    on one batched session; returns every result."""
+    m = gpu.Model.from_tensors(dims, T)
+    s = m.session(n_rows=n, n_encoders=len(xas))
+    for e, xa in enumerate(xas):
+        s.set_encoder(xa, enc=e)
+    out = []
+    first = list(range(3, 3 + n))
+    forced = [[(7 * i + r) % dims.n_vocab for r in range(n)] for i in range(4)]
+    out.append(s.run(first, forced=forced, n_steps=5, topk=3))
+    res, lg = s.step(list(range(20, 20 + n)), want_logits=True, topk=2)
+    out.append(res)
+    out.append(lg)
+    out.append(s.run(first, forced=None, n_steps=6, topk=1))
+    s.set_suppress([1, 2, 3, 50])
+    s.reorder([(r + 1) % n for r in range(n)])
+    res, lg = s.step(list(range(40, 40 + n)), want_logits=True, topk=4)
+    out.append(res)
+    out.append(lg)
+    s.close()
+    m.close()
+    return out
+
+
+def _flatten(results):
+    flat = []
+    for item in results:
+        if isinstance(item, np.ndarray):
+            flat.append(item)
+        else:
+            for x in item:
+                for r in (x if isinstance(x, list) else [x]):
+                    flat.append((r.argmax, r.max_logit, r.logsumexp, r.raw_logsumexp, tuple(r.topk_ids), tuple(r.topk_logits)))
+    return flat
+
+
+def test_batched_graph_replay_matches_eager(gpu, monkeypatch):
+    """The captured step, replayed for every step of a run (with eager work and synchronisations
+    between runs), gives bit-identical results to launching every kernel of every step."""
+    dims = synth.Dims(n_vocab=1100, n_text_ctx=40, n_text_state=512, n_text_head=8, n_text_layer=2, n_audio_ctx=64)
+    T = synth.make_decoder(dims, seed=45, ln_random=True)
+    n = 10
+    xas = [synth.encoder_output(dims, 45, stream=e) for e in range(n)]
+    monkeypatch.setenv("W4H_GRAPH", "0")
+    eager = _flatten(_session_script(gpu, dims, T, xas, n))
+    monkeypatch.setenv("W4H_GRAPH", "1")
+    graph = _flatten(_session_script(gpu, dims, T, xas, n))
+    assert len(eager) == len(graph)
+    for a, b in zip(eager, graph):
+        if isinstance(a, np.ndarray):
+            np.testing.assert_array_equal(a, b)
+        else:
+            assert a == b

@@ -416,7 +416,9 @@ struct w4h_session {
   bool wide = false;
   int Rp = 0, nch = 0, chlen = 0, nsel = 0;
   WideGemm g_qkv{}, g_o{}, g_cq{}, g_co{}, g_1{}, g_2{}, g_v{};
-  DevBuf wx, wact, wpa, wpb, wcpart, wselp, wnext;
+  DevBuf wx, wact, whid, wqkv, wlgt, wpart, wcnt, wcpart, wselp, wnext, wctl;
+  WideGraph wgraph;
+  bool use_graph = true;
 };
 
 namespace w4h {
@@ -497,11 +499,16 @@ static WideParams wide_params(w4h_session* s) {
   p.slots = s->slots_identity ? nullptr : s->slots.as<int32_t>();
   p.x = s->wx.as<float>();
   p.act = s->wact.as<float>();
-  p.pa = s->wpa.as<float>();
-  p.pb = s->wpb.as<float>();
+  p.hid = s->whid.as<float>();
+  p.qkv = s->wqkv.as<float>();
+  p.lgt = s->wlgt.as<float>();
+  p.part = s->wpart.as<float>();
+  p.cnt = s->wcnt.as<unsigned>();
   p.cpart = s->wcpart.as<float>();
   p.selp = s->wselp.as<float>();
   p.next_tok = s->wnext.as<int32_t>();
+  p.ctl = s->wctl.as<WideCtl>();
+  p.graph = s->use_graph ? &s->wgraph : nullptr;
   p.nch = s->nch;
   p.chlen = s->chlen;
   p.nsel = s->nsel;
@@ -672,10 +679,22 @@ int create_wide(std::unique_ptr<w4h_session>& s, const hipDeviceProp_t& prop, w4
   if ((rc = s->wx.alloc(sizeof(float) * (size_t)s->S * d))) return rc;
   if ((rc = s->wact.alloc(sizeof(float) * (size_t)s->Rp * 4 * d))) return rc;
   HIPCHK(hipMemset(s->wact.p, 0, sizeof(float) * (size_t)s->Rp * 4 * d));
-  if ((rc = s->wpa.alloc(sizeof(float) * pmax)) || (rc = s->wpb.alloc(sizeof(float) * pmax))) return rc;
+  if ((rc = s->whid.alloc(sizeof(float) * (size_t)s->Rp * 4 * d))) return rc;
+  HIPCHK(hipMemset(s->whid.p, 0, sizeof(float) * (size_t)s->Rp * 4 * d));
+  if ((rc = s->wqkv.alloc(sizeof(float) * (size_t)s->S * 3 * d))) return rc;
+  if ((rc = s->wlgt.alloc(sizeof(float) * (size_t)s->S * V))) return rc;
+  if ((rc = s->wpart.alloc(sizeof(float) * pmax))) return rc;
+  const size_t ncnt = (size_t)(std::max(V, 4 * d) + 15) / 16 + 16;  // column blocks of the widest GEMM
+  if ((rc = s->wcnt.alloc(sizeof(unsigned) * ncnt))) return rc;
+  HIPCHK(hipMemset(s->wcnt.p, 0, sizeof(unsigned) * ncnt));
   if ((rc = s->wcpart.alloc(sizeof(float) * (size_t)s->S * H * s->nch * kPartWords))) return rc;
   if ((rc = s->wselp.alloc(sizeof(float) * (size_t)s->S * s->nsel * kSelWords))) return rc;
   if ((rc = s->wnext.alloc(sizeof(int32_t) * s->S))) return rc;
+  if ((rc = s->wctl.alloc(sizeof(WideCtl)))) return rc;
+  HIPCHK(hipMemset(s->wctl.p, 0, sizeof(WideCtl)));
+  HIPCHK(wide_prepare(s->Rp, m->wq8));
+  // One step is captured as a HIP graph and replayed per step; W4H_GRAPH=0 launches every kernel.
+  if (const char* e = getenv("W4H_GRAPH")) s->use_graph = atoi(e) != 0;
   HIPCHK(hipStreamCreate(&s->stream));
   if ((rc = s->err.alloc(256))) return rc;
   HIPCHK(hipMemset(s->err.p, 0, 256));
@@ -804,6 +823,7 @@ int w4h_session_destroy(w4h_session* s) {
   (void)hipSetDevice(m->device);
   if (s->stream) {
     (void)hipStreamSynchronize(s->stream);
+    wide_graph_release(&s->wgraph);
     (void)hipStreamDestroy(s->stream);
   }
   delete s;

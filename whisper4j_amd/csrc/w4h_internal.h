@@ -84,8 +84,25 @@ struct WideGemm {
   const void* w;         // [N][K] f16, or int8 with f16 scales [N][K/32] in ws
   const uint16_t* ws;
   int N, K;
-  int kb;                // 128-blocks per k slice (1..4); slices = ceil(K / (128 kb))
-  int ks;                // number of k slices
+  int nw;                // column groups of 16 per workgroup (4, 2, 1); the 4 / nw waves of a
+                         // column group split the workgroup's k range
+  int kb;                // 128-blocks per wave; a workgroup covers (4 / nw) * kb blocks
+  int ks;                // number of k slices (workgroups per column block)
+};
+
+// Per-run values of the batched engine that its kernels read from device memory, so one captured
+// step can be replayed for every step of a run.
+struct WideCtl {
+  int i;           // step index within the run (advanced by the last selection-merge workgroup)
+  int kv_len0;     // KV length before the run
+  int forced_on, out_on, logits_on, mask_on, mask2_on, slots_on, topk, probe;
+  unsigned done;   // selection-merge arrivals in the current step
+};
+
+// Captured step of a session (HIP graph exec) and the buffer addresses it was captured with.
+struct WideGraph {
+  void* exec = nullptr;
+  const void* key[8] = {};
 };
 
 struct WideParams {
@@ -102,12 +119,18 @@ struct WideParams {
   const uint16_t *xk, *xv;  // [X][L][H][A][64]
   const int32_t* slots;     // [S][max_ctx] or null
   float* x;                 // [S][d] residual stream
-  float* act;               // [Rp][4d] GEMM input rows (rows >= S stay zero)
-  float *pa, *pb;           // GEMM partials, each [slices][Rp][N] (sized for the largest GEMM)
+  float* act;               // [Rp][4d] GEMM input rows: LN outputs, attention outputs
+  float* hid;               // [Rp][4d] MLP hidden rows (GELU output, MLP2 input)
+  float* qkv;               // [S][3d] QKV projection rows, then cross-attention query rows
+  float* lgt;               // [S][V] logits
+  float* part;              // GEMM split-K partial sums [slices][Rp][N] (largest GEMM)
+  unsigned* cnt;            // split-K arrival counters, one per 64-column block (zero at rest)
   float* cpart;             // [S][H][nch][kPartWords] cross-attention chunk partials
   float* selp;              // [S][nsel][kSelWords] selection partials
   int32_t* next_tok;        // [S] argmax of the last step (greedy feedback)
   int nch, chlen, nsel;
+  WideCtl* ctl;             // device control block
+  WideGraph* graph;         // host cache of the captured step, or null to launch every kernel
   WideGemm g_qkv, g_o, g_cq, g_co, g_1, g_2, g_v;  // per-layer shapes and slicing; g_v = logits
   // control
   int nsteps, kv_len0;
@@ -122,6 +145,9 @@ struct WideParams {
 
 // Enqueue p.nsteps wide steps on st.
 hipError_t launch_wide(const WideParams& p, hipStream_t st);
+// Set the GEMM kernels' LDS limits (before any capture) and release a captured step.
+hipError_t wide_prepare(int Rp, int wq8);
+void wide_graph_release(WideGraph* g);
 // Slicing of one wide GEMM for a device with n_cu compute units.
 WideGemm wide_plan(const void* w, const uint16_t* ws, int N, int K, int n_cu);
 

@@ -2,10 +2,10 @@
 // streams, up to 32) advance one token per step through a sequence of ordinary kernels, and every
 // projection is an MFMA GEMM over all rows at once (v_mfma_f32_16x16x32_f16).
 //
-// Per layer:  resid+LN1 -> QKV GEMM -> self-attention (KV append) -> out GEMM -> resid+LN2 ->
-//             cross-q GEMM -> cross-attention chunks -> chunk merge -> cross-out GEMM -> resid+LN3 ->
-//             MLP1 GEMM -> GELU -> MLP2 GEMM
-// then resid+final LN -> tied logits GEMM -> selection partials -> selection merge (+ next token).
+// Per layer:  LN1 -> QKV GEMM (+bias) -> self-attention (KV append) -> out GEMM (x += .) -> LN2 ->
+//             cross-q GEMM (+bias) -> cross-attention chunks -> chunk merge -> cross-out GEMM (x += .)
+//             -> LN3 -> MLP1 GEMM (GELU) -> MLP2 GEMM (x += .)
+// then final LN -> tied logits GEMM -> selection partials -> selection merge (+ next token).
 //
 // Numerics.  Activations are fp32.  A GEMM stages its activation slice in LDS as two f16 parts,
 // hi = f16(a) and lo = f16(a - hi), and runs every MFMA twice (hi and lo) against the same f16
@@ -14,8 +14,11 @@
 // block, whose f16 scale is applied to the step's fp32 result.  The self-KV cache is f16, as in the
 // persistent step kernel; the current token's key and value are used in fp32.
 //
-// Output layout of a GEMM: partial sums per k slice, out[slice][row][N]; consumers (attention,
-// residual, GELU, selection) add the slices, so no GEMM needs a cross-workgroup reduction.
+// Split-K.  A GEMM splits K into slices (one workgroup per 64 output columns and slice).  Each
+// workgroup stores its partial sums with device-coherent stores, waits for them to complete and
+// counts itself in the column block's arrival counter; the last workgroup to arrive adds the
+// slices in slice order (so the result does not depend on arrival order), applies the epilogue
+// (bias; bias + residual add; bias + GELU) and resets the counter for the next GEMM.
 
 #include "w4h_kernels.h"
 
@@ -23,9 +26,11 @@ namespace w4h {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
-typedef int int2v __attribute__((ext_vector_type(2)));
 
 constexpr int kPadH = 8;  // halves of padding per LDS activation row (16 bytes: spreads banks)
+constexpr int kSliceBatch = 4;  // slices whose partials a reducing thread loads at once
+
+enum { EP_STORE = 0, EP_RESID = 1, EP_GELU = 2 };
 
 DEV half8 as_half8(uint4 u) {
   half8 h;
@@ -44,30 +49,82 @@ DEV half8 i8x8_to_h8(uint2 u) {
   return h;
 }
 
-// ------------------------------------------------------------------------------------------------
-// GEMM: grid (ceil(N / 64), slices), 256 threads.  Wave w of workgroup (nb, ks) owns output columns
-// nb*64 + w*16 + [0, 16) and the k range of slice ks.  Lane i holds weight row n = base + i%16 and,
-// for MFMA step b of block kb, the 8 k values kb*128 + 32b + 8(i/16) + [0, 8): 16 bytes (f16) or 8
-// bytes (int8) per load, 64 contiguous bytes per row per step.  Every weight fragment of the slice
-// is loaded into registers before the activation slice is staged, so the stream of weight bytes
-// overlaps the staging.  act rows >= S are staged as zeros.
+DEV void st_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+DEV float ld_dev(const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
-template <int MT, int WQ8, int KB>
-__global__ __launch_bounds__(256) void k_w_gemm(const void* __restrict__ w, const uint16_t* __restrict__ ws, int N, int K,
-                                                const float* __restrict__ act, int lda, int S, float* __restrict__ out) {
+struct GemmArgs {
+  const void* w;         // [N][K] f16, or int8 with f16 scales [N][K/32] in ws
+  const uint16_t* ws;
+  int N, K, ks;          // ks: number of k slices (gridDim.y)
+  const float* act;      // [Rp][lda] fp32 rows (rows >= S read as zero)
+  int lda, S;
+  float* part;           // [ks][Rp][N] partial sums (ks > 1)
+  unsigned* cnt;         // [ceil(N/64)] arrival counters, zero between GEMMs
+  int ep;                // EP_*
+  const float* bias;     // [N] or null
+  float* dst;            // [S][ldd]
+  int ldd;
+};
+
+DEV void epilogue(const GemmArgs& a, int r, int n, float v) {
+  const float b = a.bias ? a.bias[n] : 0.f;
+  float* o = a.dst + (size_t)r * a.ldd + n;
+  if (a.ep == EP_STORE) *o = v + b;
+  else if (a.ep == EP_RESID) *o = *o + (v + b);
+  else *o = gelu_f16(v + b);
+}
+
+// ------------------------------------------------------------------------------------------------
+// GEMM: grid (ceil(N / (16 NW)), ks), 256 threads = 4 waves as NW column groups x KW = 4/NW k parts.
+// Workgroup (nb, kz) owns columns nb*16*NW + [0, 16 NW) and the k range of slice kz
+// (KW*KB*128 values); wave w takes column group w % NW and k part w / NW (KB blocks of 128).  Lane
+// i holds weight row n = base + i%16 and, for MFMA step b of block kb, the 8 k values
+// kb*128 + 32b + 8(i/16) + [0, 8): 16 bytes (f16) or 8 bytes (int8) per load, 64 contiguous bytes per
+// row per step.  Every weight fragment of the wave's part is loaded into registers before the
+// activation slice is staged, so the stream of weight bytes overlaps the staging.  The k parts of a
+// column group are added through LDS in k order.
+
+template <int MT, int WQ8, int KB, int NW>
+__global__ __launch_bounds__(256) void k_w_gemm(GemmArgs a) {
   extern __shared__ __align__(16) uint16_t lds_h[];
+  __shared__ int s_last;
+  constexpr int KW = 4 / NW;
   constexpr int Rp = MT * 16;
-  constexpr int kslice = KB * kWideKBlock;
-  constexpr int rs = kslice + kPadH;  // halves per LDS row
+  constexpr int CB = 16 * NW;                // columns per workgroup
+  constexpr int kpart = KB * kWideKBlock;    // k per wave
+  constexpr int kslice = KW * kpart;         // k per workgroup
+  constexpr int rs = kslice + kPadH;         // halves per LDS row
   uint16_t* hi = lds_h;
   uint16_t* lo = lds_h + Rp * rs;
+  const int N = a.N, K = a.K;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g4 = lane >> 4, c16 = lane & 15;
-  const int n = blockIdx.x * kWideCols + wv * 16 + c16;
-  const int k0 = blockIdx.y * kslice;
-  const int nkb = min(kslice, K - k0) / kWideKBlock;
+  const int cg = wv % NW, kw = wv / NW;
+  const int n = blockIdx.x * CB + cg * 16 + c16;
+  const int k0 = blockIdx.y * kslice;        // workgroup's first k
+  const int kp0 = k0 + kw * kpart;           // wave's first k
+  const int nkb = max(0, min(kpart, K - kp0)) / kWideKBlock;
   const int nr = min(n, N - 1);
 
-  // 1. weight fragments of the whole slice
+  // 1. activation slice into registers first (L2 hits), so that waiting for it does not wait for
+  //    the weight loads issued after it; 8 consecutive k per task
+  constexpr int tasks_per_row = kslice / 8;
+  constexpr int TPT = Rp * tasks_per_row / 256;  // tasks per thread
+  float4 av[TPT][2];
+#pragma unroll
+  for (int q = 0; q < TPT; ++q) {
+    const int t = tid + 256 * q;
+    const int r = t / tasks_per_row, c8 = t - r * tasks_per_row;
+    const int k = k0 + c8 * 8;
+    if (r < a.S && k < K) {
+      av[q][0] = *reinterpret_cast<const float4*>(a.act + (size_t)r * a.lda + k);
+      av[q][1] = *reinterpret_cast<const float4*>(a.act + (size_t)r * a.lda + k + 4);
+    } else {
+      av[q][0] = make_float4(0.f, 0.f, 0.f, 0.f);
+      av[q][1] = av[q][0];
+    }
+  }
+
+  // 2. weight fragments of the wave's k part
   half8 bf[KB][4];
   uint2 bq[KB][4];
   float sc[KB][4];
@@ -75,33 +132,24 @@ __global__ __launch_bounds__(256) void k_w_gemm(const void* __restrict__ w, cons
   for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      const int k = k0 + kb * kWideKBlock + 32 * b + 8 * g4;
+      const int k = kp0 + kb * kWideKBlock + 32 * b + 8 * g4;
       if (kb < nkb) {
         if (!WQ8) {
-          bf[kb][b] = as_half8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(w) + (size_t)nr * K + k));
+          bf[kb][b] = as_half8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.w) + (size_t)nr * K + k));
         } else {
-          bq[kb][b] = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(w) + (size_t)nr * K + k);
-          sc[kb][b] = h2f(ws[(size_t)nr * (K >> 5) + (k >> 5)]);
+          bq[kb][b] = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(a.w) + (size_t)nr * K + k);
+          sc[kb][b] = h2f(a.ws[(size_t)nr * (K >> 5) + (k >> 5)]);
         }
       }
     }
   }
 
-  // 2. activation slice -> LDS (hi, lo); 8 consecutive k per task
-  constexpr int tasks_per_row = kslice / 8;
-  for (int t = tid; t < Rp * tasks_per_row; t += 256) {
-    const int r = t / tasks_per_row, c8 = t - r * tasks_per_row;
-    const int k = k0 + c8 * 8;
-    float v[8];
-    if (r < S && k < K) {
-      const float4 a0 = *reinterpret_cast<const float4*>(act + (size_t)r * lda + k);
-      const float4 a1 = *reinterpret_cast<const float4*>(act + (size_t)r * lda + k + 4);
-      v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
-      v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
-    } else {
+  // activation slice -> LDS as (hi, lo) f16 parts
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = 0.f;
-    }
+  for (int q = 0; q < TPT; ++q) {
+    const int t = tid + 256 * q;
+    const int r = t / tasks_per_row, c8 = t - r * tasks_per_row;
+    const float v[8] = {av[q][0].x, av[q][0].y, av[q][0].z, av[q][0].w, av[q][1].x, av[q][1].y, av[q][1].z, av[q][1].w};
     half8 h, l;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -113,7 +161,7 @@ __global__ __launch_bounds__(256) void k_w_gemm(const void* __restrict__ w, cons
   }
   lds_barrier();
 
-  // 3. MFMA over the slice
+  // 3. MFMA over the wave's k part
   floatx4 acc[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -122,7 +170,7 @@ __global__ __launch_bounds__(256) void k_w_gemm(const void* __restrict__ w, cons
     if (kb < nkb) {
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        const int kk = kb * kWideKBlock + 32 * b + 8 * g4;
+        const int kk = kw * kpart + kb * kWideKBlock + 32 * b + 8 * g4;
         const half8 B = WQ8 ? i8x8_to_h8(bq[kb][b]) : bf[kb][b];
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
@@ -141,61 +189,129 @@ __global__ __launch_bounds__(256) void k_w_gemm(const void* __restrict__ w, cons
     }
   }
 
-  // 4. partial sums of this slice: lane holds rows 4(i/16) + [0, 4) of each 16-row tile, column n
-  if (n < N) {
-    float* o = out + (size_t)blockIdx.y * Rp * N + n;
+  // 4. k parts of a column group added in k order through LDS (reusing the staging area)
+  if constexpr (KW > 1) {
+    float* red = reinterpret_cast<float*>(lds_h);  // [KW-1][NW][MT*4][64]
+    lds_barrier();
+    if (kw > 0)
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) red[(((kw - 1) * NW + cg) * MT * 4 + m * 4 + j) * 64 + lane] = acc[m][j];
+    lds_barrier();
+    if (kw == 0)
+#pragma unroll
+      for (int q = 1; q < KW; ++q)
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[m][j] += red[(((q - 1) * NW + cg) * MT * 4 + m * 4 + j) * 64 + lane];
+  }
+
+  // 5. lane holds rows 4(i/16) + [0, 4) of each 16-row tile, column n
+  if (a.ks == 1) {
+    if (kw == 0 && n < N) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = m * 16 + 4 * g4 + j;
+          if (r < a.S) epilogue(a, r, n, acc[m][j]);
+        }
+    }
+    return;
+  }
+  if (kw == 0 && n < N) {
+    float* o = a.part + (size_t)blockIdx.y * Rp * N + n;
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[(size_t)(m * 16 + 4 * g4 + j) * N] = acc[m][j];
+      for (int j = 0; j < 4; ++j)
+        if (m * 16 + 4 * g4 + j < a.S) st_dev(o + (size_t)(m * 16 + 4 * g4 + j) * N, acc[m][j]);
+  }
+  kv_drain();  // this wave's partial stores have completed
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(a.cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == (unsigned)(a.ks - 1);
+    if (s_last) __hip_atomic_store(a.cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // last arrival: thread (row group tid / CB, column tid % CB) adds the slices in slice order
+  constexpr int RG = 256 / CB;    // row groups
+  constexpr int RPT = Rp / RG;    // rows per thread
+  const int nc = blockIdx.x * CB + (tid % CB);
+  if (nc >= N) return;
+  float sum[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) sum[i] = 0.f;
+  for (int z0 = 0; z0 < a.ks; z0 += kSliceBatch) {
+    float t[RPT][kSliceBatch];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+#pragma unroll
+      for (int u = 0; u < kSliceBatch; ++u) {
+        const int r = tid / CB + RG * i;
+        t[i][u] = (z0 + u < a.ks && r < a.S) ? ld_dev(a.part + ((size_t)(z0 + u) * Rp + r) * N + nc) : 0.f;
+      }
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+#pragma unroll
+      for (int u = 0; u < kSliceBatch; ++u) sum[i] += t[i][u];
+  }
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int r = tid / CB + RG * i;
+    if (r < a.S) epilogue(a, r, nc, sum[i]);
   }
 }
 
-// Sum of the slices of a GEMM output at (row, col).
-DEV float slice_sum(const float* p, int ks, size_t sstride, size_t idx) {
-  float v = 0.f;
-  for (int j = 0; j < ks; ++j) v += p[j * sstride + idx];
-  return v;
-}
-
 // ------------------------------------------------------------------------------------------------
-// Residual update + LayerNorm, one workgroup per row.  Mode 0: x = token embedding + positional
-// row t.  Mode 1: x += bias + sum of the GEMM slices.  Then act[row] = LN(x) (when g != null).
-// LN: two passes, eps 1e-5, as nn/LayerNorm.java:5-31.
+// LayerNorm of the residual rows, one workgroup per row: act[row] = LN(x[row]).  With tokens, the
+// row is first set to token embedding + positional row pe (layer 0).  Two passes, eps 1e-5, as
+// nn/LayerNorm.java:5-31.
 
 constexpr int kWideVec = 8;  // d <= 8 * 256
 
-template <int WQ8>
-__global__ __launch_bounds__(256) void k_w_resid(int mode, const float* __restrict__ P, int ks, size_t sstride, const float* __restrict__ bias,
-                                                 const void* __restrict__ emb, const uint16_t* __restrict__ emb_s,
-                                                 const float* __restrict__ pos, int t, const int32_t* __restrict__ toks,
-                                                 float* __restrict__ x, int d, const float* __restrict__ g,
-                                                 const float* __restrict__ b, float* __restrict__ act, int lda) {
+template <int WQ8, int EMB>
+__global__ __launch_bounds__(256) void k_w_ln(const WideCtl* __restrict__ ctl, const int32_t* __restrict__ tokens0,
+                                              const int32_t* __restrict__ forced, const int32_t* __restrict__ next_tok, int S, int C,
+                                              const void* __restrict__ emb, const uint16_t* __restrict__ emb_s,
+                                              const float* __restrict__ pos, float* __restrict__ x, int d,
+                                              const float* __restrict__ g, const float* __restrict__ b, float* __restrict__ act,
+                                              int lda) {
   __shared__ float red[8];
   const int s = blockIdx.x, tid = threadIdx.x;
   float v[kWideVec];
   float sum = 0.f;
-  const int tk = mode == 0 ? toks[s] : 0;
+  int tk = 0, pe = 0;
+  if (EMB) {
+    // token of this step: the run's first tokens, the forced row, or the last step's argmax;
+    // positional row clamped as the reference
+    const int i = ctl->i, t = ctl->kv_len0 + i;
+    pe = t < C - 1 ? t : C - 1;
+    tk = i == 0 ? tokens0[s] : (ctl->forced_on ? forced[(size_t)(i - 1) * S + s] : next_tok[s]);
+  }
 #pragma unroll
   for (int i = 0; i < kWideVec; ++i) {
     const int j = tid + 256 * i;
     v[i] = 0.f;
     if (j < d) {
       float xv;
-      if (mode == 0) {
+      if (EMB) {
         float e;
         if (!WQ8) e = h2f(static_cast<const uint16_t*>(emb)[(size_t)tk * d + j]);
         else e = (float)static_cast<const int8_t*>(emb)[(size_t)tk * d + j] * h2f(emb_s[(size_t)tk * (d >> 5) + (j >> 5)]);
-        xv = e + pos[(size_t)t * d + j];
+        xv = e + pos[(size_t)pe * d + j];
+        x[(size_t)s * d + j] = xv;
       } else {
-        xv = x[(size_t)s * d + j] + (bias[j] + slice_sum(P, ks, sstride, (size_t)s * d + j));
+        xv = x[(size_t)s * d + j];
       }
-      x[(size_t)s * d + j] = xv;
       v[i] = xv;
       sum += xv;
     }
   }
-  if (g == nullptr) return;
   sum = wave_sum(sum);
   if ((tid & 63) == 0) red[tid >> 6] = sum;
   __syncthreads();
@@ -216,22 +332,25 @@ __global__ __launch_bounds__(256) void k_w_resid(int mode, const float* __restri
 }
 
 // ------------------------------------------------------------------------------------------------
-// Self-attention of one (row, head): q, k, v = bias + GEMM slices; k, v appended to the cache at
-// position t (f16); softmax over the t cached keys (row s reads position j from slot slots[s][j])
-// plus the current key (fp32); output -> act[s][h*64, +64).  8 lanes per key, 16 bytes each.
+// Self-attention of one (row, head): q, k, v from the QKV rows qkv[s][3d]; k, v appended to the
+// cache at position t (f16); softmax over the t cached keys (row s reads position j from slot
+// slots[s][j]) plus the current key (fp32); output -> act[s][h*64, +64).  8 lanes per key, 16 bytes
+// each; four keys per lane group in flight.
 
-__global__ __launch_bounds__(256) void k_w_self(const float* __restrict__ P, int ks, size_t sstride, int N, const float* __restrict__ bqkv,
-                                                int d, int H, int l, int S, int max_ctx, int t, uint16_t* __restrict__ kvk,
-                                                uint16_t* __restrict__ kvv, const int32_t* __restrict__ slots,
-                                                float* __restrict__ act, int lda) {
+constexpr int kKeysInFlight = 4;
+
+__global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl, const float* __restrict__ qkv, int d, int H, int l,
+                                                int S, int max_ctx, uint16_t* __restrict__ kvk, uint16_t* __restrict__ kvv,
+                                                const int32_t* __restrict__ slot_table, float* __restrict__ act, int lda) {
   extern __shared__ float sc[];  // [t + 1] scores, then probabilities
   __shared__ float q[64], kc[64], vc[64], red[4 * 64], stat[8];
   const int s = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int t = ctl->kv_len0 + ctl->i;  // position of the current token
+  const int32_t* slots = ctl->slots_on ? slot_table : nullptr;
   const size_t head_base = ((size_t)l * S * H) * max_ctx * kHeadDim;  // layer l
   if (tid < 192) {
     const int part = tid >> 6, e = tid & 63;
-    const int col = part * d + h * kHeadDim + e;
-    const float v = bqkv[col] + slice_sum(P, ks, sstride, (size_t)s * N + col);
+    const float v = qkv[(size_t)s * 3 * d + part * d + h * kHeadDim + e];
     if (part == 0) q[e] = v;
     else if (part == 1) kc[e] = v;
     else vc[e] = v;
@@ -246,22 +365,31 @@ __global__ __launch_bounds__(256) void k_w_self(const float* __restrict__ P, int
 #pragma unroll
   for (int e = 0; e < 8; ++e) qd[e] = q[dc * 8 + e];
   const int32_t* srow = slots ? slots + (size_t)s * max_ctx : nullptr;
-  for (int j0 = 0; j0 < t; j0 += 32) {
-    const int j = j0 + kg;
-    float dot = 0.f;
-    if (j < t) {
-      const int slot = srow ? srow[j] : s;
-      const uint4 u = *reinterpret_cast<const uint4*>(kvk + head_base + (((size_t)slot * H + h) * max_ctx + j) * kHeadDim + dc * 8);
-      const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+  auto kv_off = [&](int j) -> size_t {
+    const int slot = srow ? srow[j] : s;
+    return head_base + (((size_t)slot * H + h) * max_ctx + j) * kHeadDim + dc * 8;
+  };
+  for (int j0 = 0; j0 < t; j0 += 32 * kKeysInFlight) {
+    uint4 u[kKeysInFlight];
+#pragma unroll
+    for (int f = 0; f < kKeysInFlight; ++f) {
+      const int j = j0 + 32 * f + kg;
+      u[f] = j < t ? *reinterpret_cast<const uint4*>(kvk + kv_off(j)) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int f = 0; f < kKeysInFlight; ++f) {
+      const int j = j0 + 32 * f + kg;
+      const uint32_t uw[4] = {u[f].x, u[f].y, u[f].z, u[f].w};
+      float dot = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float2 f = h2x2(uw[e]);
-        dot = fmaf(qd[2 * e], f.x, dot);
-        dot = fmaf(qd[2 * e + 1], f.y, dot);
+        const float2 fv = h2x2(uw[e]);
+        dot = fmaf(qd[2 * e], fv.x, dot);
+        dot = fmaf(qd[2 * e + 1], fv.y, dot);
       }
+      dot = sum8(dot);
+      if (dc == 0 && j < t) sc[j] = dot * 0.125f;
     }
-    dot = sum8(dot);
-    if (dc == 0 && j < t) sc[j] = dot * 0.125f;
   }
   if (wv == 0) {
     const float cur = wave_sum(q[lane] * kc[lane]);
@@ -288,22 +416,30 @@ __global__ __launch_bounds__(256) void k_w_self(const float* __restrict__ P, int
   float o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = 0.f;
-  for (int j = kg; j < n; j += 32) {
-    const float p = sc[j];
-    if (j < t) {
-      const int slot = srow ? srow[j] : s;
-      const uint4 u = *reinterpret_cast<const uint4*>(kvv + head_base + (((size_t)slot * H + h) * max_ctx + j) * kHeadDim + dc * 8);
-      const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+  for (int j0 = 0; j0 < t; j0 += 32 * kKeysInFlight) {
+    uint4 u[kKeysInFlight];
+#pragma unroll
+    for (int f = 0; f < kKeysInFlight; ++f) {
+      const int j = j0 + 32 * f + kg;
+      u[f] = j < t ? *reinterpret_cast<const uint4*>(kvv + kv_off(j)) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int f = 0; f < kKeysInFlight; ++f) {
+      const int j = j0 + 32 * f + kg;
+      const float p = j < t ? sc[j] : 0.f;
+      const uint32_t uw[4] = {u[f].x, u[f].y, u[f].z, u[f].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float2 f = h2x2(uw[e]);
-        o[2 * e] = fmaf(p, f.x, o[2 * e]);
-        o[2 * e + 1] = fmaf(p, f.y, o[2 * e + 1]);
+        const float2 fv = h2x2(uw[e]);
+        o[2 * e] = fmaf(p, fv.x, o[2 * e]);
+        o[2 * e + 1] = fmaf(p, fv.y, o[2 * e + 1]);
       }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = fmaf(p, vc[dc * 8 + e], o[e]);
     }
+  }
+  if (kg == 0) {
+    const float p = sc[t];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = fmaf(p, vc[dc * 8 + e], o[e]);
   }
   // sum over the 8 key groups of a wave (lane bits 3..5), then over the 4 waves
 #pragma unroll
@@ -329,10 +465,9 @@ __global__ __launch_bounds__(256) void k_w_self(const float* __restrict__ P, int
 // shared encoder's K/V chunk is read once per group.  Partial (m, l, acc[64]) per row.
 
 template <int RG>
-__global__ __launch_bounds__(256) void k_w_cross(const float* __restrict__ P, int ks, size_t sstride, int d, const float* __restrict__ bcq,
-                                                 int H, int A, int l, int L, int S, int X, int chlen, int nch,
-                                                 const uint16_t* __restrict__ xk, const uint16_t* __restrict__ xv,
-                                                 float* __restrict__ cpart) {
+__global__ __launch_bounds__(256) void k_w_cross(const float* __restrict__ cq, int d, int H, int A, int l, int L, int S, int X,
+                                                 int chlen, int nch, const uint16_t* __restrict__ xk,
+                                                 const uint16_t* __restrict__ xv, float* __restrict__ cpart) {
   extern __shared__ float scs[];  // [RG][chlen]
   __shared__ float q[RG * 64], red[4 * RG * 64], rm[RG], rl[RG];
   const int e = blockIdx.x, h = blockIdx.y, c = blockIdx.z % nch, rg = blockIdx.z / nch;
@@ -347,37 +482,40 @@ __global__ __launch_bounds__(256) void k_w_cross(const float* __restrict__ P, in
   }
   for (int i = tid; i < nr * 64; i += 256) {
     const int r = i >> 6, k = i & 63;
-    const int col = h * kHeadDim + k;
-    q[i] = (bcq[col] + slice_sum(P, ks, sstride, (size_t)(r0 + r) * d + col)) * 0.125f;
+    q[i] = cq[(size_t)(r0 + r) * d + h * kHeadDim + k] * 0.125f;
   }
   __syncthreads();
   const int j0 = c * chlen, j1 = min(A, j0 + chlen), n = j1 - j0;
-  const size_t base = ((((size_t)e * L + l) * H + h) * A) * kHeadDim;
+  const uint16_t* kb = xk + ((((size_t)e * L + l) * H + h) * A + j0) * kHeadDim;
+  const uint16_t* vb = xv + ((((size_t)e * L + l) * H + h) * A + j0) * kHeadDim;
   const int kg = tid >> 3, dc = tid & 7;
-  for (int jj = 0; jj < n; jj += 32) {
-    const int j = jj + kg;
-    float kd[8];
-    if (j < n) {
-      const uint4 u = *reinterpret_cast<const uint4*>(xk + base + (size_t)(j0 + j) * kHeadDim + dc * 8);
-      const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+  for (int jj = 0; jj < n; jj += 32 * kKeysInFlight) {
+    uint4 u[kKeysInFlight];
 #pragma unroll
-      for (int q2 = 0; q2 < 4; ++q2) {
-        const float2 f = h2x2(uw[q2]);
-        kd[2 * q2] = f.x;
-        kd[2 * q2 + 1] = f.y;
-      }
-    } else {
-#pragma unroll
-      for (int q2 = 0; q2 < 8; ++q2) kd[q2] = 0.f;
+    for (int f = 0; f < kKeysInFlight; ++f) {
+      const int j = jj + 32 * f + kg;
+      u[f] = j < n ? *reinterpret_cast<const uint4*>(kb + (size_t)j * kHeadDim + dc * 8) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
-    for (int r = 0; r < RG; ++r) {
-      if (r < nr) {
-        float dot = 0.f;
+    for (int f = 0; f < kKeysInFlight; ++f) {
+      const int j = jj + 32 * f + kg;
+      float kd[8];
+      const uint32_t uw[4] = {u[f].x, u[f].y, u[f].z, u[f].w};
 #pragma unroll
-        for (int q2 = 0; q2 < 8; ++q2) dot = fmaf(q[r * 64 + dc * 8 + q2], kd[q2], dot);
-        dot = sum8(dot);
-        if (dc == 0 && j < n) scs[r * chlen + j] = dot;
+      for (int q2 = 0; q2 < 4; ++q2) {
+        const float2 fv = h2x2(uw[q2]);
+        kd[2 * q2] = fv.x;
+        kd[2 * q2 + 1] = fv.y;
+      }
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+        if (r < nr) {
+          float dot = 0.f;
+#pragma unroll
+          for (int q2 = 0; q2 < 8; ++q2) dot = fmaf(q[r * 64 + dc * 8 + q2], kd[q2], dot);
+          dot = sum8(dot);
+          if (dc == 0 && j < n) scs[r * chlen + j] = dot;
+        }
       }
     }
   }
@@ -404,22 +542,31 @@ __global__ __launch_bounds__(256) void k_w_cross(const float* __restrict__ P, in
   for (int r = 0; r < RG; ++r)
 #pragma unroll
     for (int q2 = 0; q2 < 8; ++q2) o[r][q2] = 0.f;
-  for (int j = kg; j < n; j += 32) {
-    const uint4 u = *reinterpret_cast<const uint4*>(xv + base + (size_t)(j0 + j) * kHeadDim + dc * 8);
-    const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
-    float vd[8];
+  for (int jj = 0; jj < n; jj += 32 * kKeysInFlight) {
+    uint4 u[kKeysInFlight];
 #pragma unroll
-    for (int q2 = 0; q2 < 4; ++q2) {
-      const float2 f = h2x2(uw[q2]);
-      vd[2 * q2] = f.x;
-      vd[2 * q2 + 1] = f.y;
+    for (int f = 0; f < kKeysInFlight; ++f) {
+      const int j = jj + 32 * f + kg;
+      u[f] = j < n ? *reinterpret_cast<const uint4*>(vb + (size_t)j * kHeadDim + dc * 8) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
-    for (int r = 0; r < RG; ++r) {
-      if (r < nr) {
-        const float p = scs[r * chlen + j];
+    for (int f = 0; f < kKeysInFlight; ++f) {
+      const int j = jj + 32 * f + kg;
+      float vd[8];
+      const uint32_t uw[4] = {u[f].x, u[f].y, u[f].z, u[f].w};
 #pragma unroll
-        for (int q2 = 0; q2 < 8; ++q2) o[r][q2] = fmaf(p, vd[q2], o[r][q2]);
+      for (int q2 = 0; q2 < 4; ++q2) {
+        const float2 fv = h2x2(uw[q2]);
+        vd[2 * q2] = fv.x;
+        vd[2 * q2 + 1] = fv.y;
+      }
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+        if (r < nr) {
+          const float p = j < n ? scs[r * chlen + j] : 0.f;
+#pragma unroll
+          for (int q2 = 0; q2 < 8; ++q2) o[r][q2] = fmaf(p, vd[q2], o[r][q2]);
+        }
       }
     }
   }
@@ -468,33 +615,28 @@ __global__ __launch_bounds__(64) void k_w_cmerge(const float* __restrict__ cpart
   act[(size_t)s * lda + h * kHeadDim + k] = o / Lsum;
 }
 
-// act[r][k] = GELU(bias[k] + sum of the MLP1 slices), r < S, k < n.
-__global__ __launch_bounds__(256) void k_w_gelu(const float* __restrict__ P, int ks, size_t sstride, const float* __restrict__ bias, int S,
-                                                int n, float* __restrict__ act, int lda) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= S * n) return;
-  const int r = i / n, k = i - r * n;
-  act[(size_t)r * lda + k] = gelu_f16(bias[k] + slice_sum(P, ks, sstride, (size_t)r * n + k));
-}
-
 // ------------------------------------------------------------------------------------------------
 // Selection.  Workgroup (s, b): 4 waves, wave w reduces entries [(4b + w) * 512, +512) of row s's
-// logits (sum of the logits GEMM slices) to one selection partial; the raw logits are copied out
-// when requested.  Then one wave per row merges the partials into the step result and the next
-// token (argmax, first index of the maximum).
+// logits to one selection partial; the raw logits are copied out when requested.  Then one wave
+// per row merges the partials into the step result and the next token (argmax, first index of the
+// maximum).
 
-__global__ __launch_bounds__(256) void k_w_select(const float* __restrict__ P, int ks, size_t sstride, int V, const uint32_t* mask,
-                                                  const uint32_t* mask2, int mw, int probe, int topk, float* __restrict__ selp,
-                                                  int nsel, float* __restrict__ logits_out) {
+__global__ __launch_bounds__(256) void k_w_select(const WideCtl* __restrict__ ctl, const float* __restrict__ lgt, int S, int V,
+                                                  const uint32_t* mask_buf, const uint32_t* mask2_buf, int mw,
+                                                  float* __restrict__ selp, int nsel, float* __restrict__ logits_buf) {
   __shared__ float lg[4][kWideSelChunk], rw[4][kWideSelChunk];
   __shared__ int idx[4][kWideSelChunk];
   const int s = blockIdx.x, wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t* mask = ctl->mask_on ? mask_buf : nullptr;
+  const uint32_t* mask2 = ctl->mask2_on ? mask2_buf : nullptr;
+  const int probe = ctl->probe, topk = ctl->topk;
+  float* logits_out = ctl->logits_on ? logits_buf + (size_t)ctl->i * S * V : nullptr;
   const int part = blockIdx.y * 4 + wv;
   const int v0 = part * kWideSelChunk;
   const int nl = max(0, min(kWideSelChunk, V - v0));
   for (int j = lane; j < nl; j += 64) {
     const int v = v0 + j;
-    const float x = slice_sum(P, ks, sstride, (size_t)s * V + v);
+    const float x = lgt[(size_t)s * V + v];
     rw[wv][j] = x;
     lg[wv][j] = (masked(mask, mw, s, v) || masked(mask2, mw, s, v)) ? -INFINITY : x;
     idx[wv][j] = v;
@@ -505,18 +647,30 @@ __global__ __launch_bounds__(256) void k_w_select(const float* __restrict__ P, i
   if (part < nsel) sel_partial(lg[wv], rw[wv], idx[wv], nl, probe, topk, selp + ((size_t)s * nsel + part) * kSelWords);
 }
 
-__global__ __launch_bounds__(64) void k_w_selmerge(const float* __restrict__ selp, int nsel, int topk, w4h_step_out* out,
-                                                   int32_t* __restrict__ next_tok) {
+__global__ __launch_bounds__(64) void k_w_selmerge(WideCtl* __restrict__ ctl, const float* __restrict__ selp, int S, int nsel,
+                                                   w4h_step_out* out_buf, int32_t* __restrict__ next_tok) {
   __shared__ float rec[kSelWords];
   const int s = blockIdx.x;
+  const int topk = ctl->topk, i = ctl->i;
   sel_merge(selp + (size_t)s * nsel * kSelWords, nsel, kSelWords, topk, rec);
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront", "local");
   if (threadIdx.x == 0) {
     const int bi = __float_as_int(rec[1]);
     next_tok[s] = (bi == 0x7fffffff) ? 0 : bi;
-    if (out) rec_to_out(rec, topk, out + s);
+    if (ctl->out_on) rec_to_out(rec, topk, out_buf + (size_t)i * S + s);
+    // the last row of the step to finish advances the step index (every row has read it)
+    const unsigned prev = __hip_atomic_fetch_add(&ctl->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == (unsigned)(S - 1)) {
+      __hip_atomic_store(&ctl->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&ctl->i, i + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
+}
+
+// Control block of a run (one thread).
+__global__ void k_w_setctl(WideCtl* ctl, WideCtl v) {
+  if (threadIdx.x == 0) *ctl = v;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -529,55 +683,111 @@ WideGemm wide_plan(const void* w, const uint16_t* ws, int N, int K, int n_cu) {
   g.N = N;
   g.K = K;
   const int kbt = K / kWideKBlock;
-  const int nblk = (N + kWideCols - 1) / kWideCols;
-  // largest slice (fewest partial sums) that still gives every compute unit two workgroups
-  int kb = 4;
-  while (kb > 1 && nblk * ((kbt + kb - 1) / kb) < 2 * n_cu) --kb;
-  g.kb = kb;
-  g.ks = (kbt + kb - 1) / kb;
+  // Candidates: NW column groups of 16 (KW = 4/NW k parts per workgroup) and KB blocks of 128 per
+  // part, with at most 4 blocks per workgroup (LDS).  Fewest k slices among the candidates that give
+  // at least one workgroup per compute unit; ties to the widest column tile (least activation
+  // staging per weight byte).  If none does, the most workgroups.
+  int best_nw = 4, best_kb = 1, best_ks = 1 << 30;
+  long best_wg = -1;
+  bool best_ok = false;
+  for (int nw : {4, 2, 1}) {
+    const int kw = 4 / nw;
+    for (int kb = 1; kb * kw <= 4; ++kb) {
+      const int ks = (kbt + kw * kb - 1) / (kw * kb);
+      const long wg = (long)((N + 16 * nw - 1) / (16 * nw)) * ks;
+      const bool ok = wg >= n_cu;
+      bool take;
+      if (ok != best_ok) take = ok;
+      else if (ok) take = ks < best_ks;
+      else take = wg > best_wg;
+      if (take) {
+        best_ok = ok;
+        best_nw = nw;
+        best_kb = kb;
+        best_ks = ks;
+        best_wg = wg;
+      }
+    }
+  }
+  g.nw = best_nw;
+  g.kb = best_kb;
+  g.ks = best_ks;
   return g;
 }
 
-template <int MT, int WQ8, int KB>
-static hipError_t gemm_kb(const WideGemm& g, const float* act, int lda, int S, float* out, hipStream_t st) {
-  const dim3 grid((g.N + kWideCols - 1) / kWideCols, g.ks);
-  const size_t lds = (size_t)2 * MT * 16 * (KB * kWideKBlock + kPadH) * sizeof(uint16_t);
-  static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w_gemm<MT, WQ8, KB>), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((k_w_gemm<MT, WQ8, KB>), grid, dim3(256), lds, st, g.w, g.ws, g.N, g.K, act, lda, S, out);
+template <int MT, int KB, int NW>
+constexpr size_t gemm_lds() {
+  return (size_t)2 * MT * 16 * ((4 / NW) * KB * kWideKBlock + kPadH) * sizeof(uint16_t);
+}
+
+template <int MT, int WQ8, int KB, int NW>
+static hipError_t gemm_attr() {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w_gemm<MT, WQ8, KB, NW>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)gemm_lds<MT, KB, NW>());
+}
+
+template <int MT, int WQ8, int KB, int NW>
+static hipError_t gemm_launch(const GemmArgs& a, hipStream_t st) {
+  const dim3 grid((a.N + 16 * NW - 1) / (16 * NW), a.ks);
+  constexpr size_t lds = gemm_lds<MT, KB, NW>();
+  hipLaunchKernelGGL((k_w_gemm<MT, WQ8, KB, NW>), grid, dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
 template <int MT, int WQ8>
-static hipError_t gemm_mt(const WideGemm& g, const float* act, int lda, int S, float* out, hipStream_t st) {
-  switch (g.kb) {
-    case 1: return gemm_kb<MT, WQ8, 1>(g, act, lda, S, out, st);
-    case 2: return gemm_kb<MT, WQ8, 2>(g, act, lda, S, out, st);
-    case 3: return gemm_kb<MT, WQ8, 3>(g, act, lda, S, out, st);
-    default: return gemm_kb<MT, WQ8, 4>(g, act, lda, S, out, st);
+static hipError_t gemm_mt(int nw, int kb, const GemmArgs& a, hipStream_t st) {
+  if (nw == 4) {
+    switch (kb) {
+      case 1: return gemm_launch<MT, WQ8, 1, 4>(a, st);
+      case 2: return gemm_launch<MT, WQ8, 2, 4>(a, st);
+      case 3: return gemm_launch<MT, WQ8, 3, 4>(a, st);
+      default: return gemm_launch<MT, WQ8, 4, 4>(a, st);
+    }
   }
+  if (nw == 2) return kb == 1 ? gemm_launch<MT, WQ8, 1, 2>(a, st) : gemm_launch<MT, WQ8, 2, 2>(a, st);
+  return gemm_launch<MT, WQ8, 1, 1>(a, st);
 }
 
-static hipError_t gemm(const WideParams& p, const WideGemm& g, float* out, hipStream_t st) {
-  const int lda = 4 * p.d;
-  if (p.Rp == 16) return p.wq8 ? gemm_mt<1, 1>(g, p.act, lda, p.S, out, st) : gemm_mt<1, 0>(g, p.act, lda, p.S, out, st);
-  return p.wq8 ? gemm_mt<2, 1>(g, p.act, lda, p.S, out, st) : gemm_mt<2, 0>(g, p.act, lda, p.S, out, st);
+// One GEMM of the step: act (GEMM input rows) times the weights, epilogue ep into dst.
+static hipError_t gemm(const WideParams& p, const WideGemm& g, const void* w, const uint16_t* ws, const float* act, int ep,
+                       const float* bias, float* dst, int ldd, hipStream_t st) {
+  GemmArgs a{};
+  a.w = w;
+  a.ws = ws;
+  a.N = g.N;
+  a.K = g.K;
+  a.ks = g.ks;
+  a.act = act;
+  a.lda = 4 * p.d;
+  a.S = p.S;
+  a.part = p.part;
+  a.cnt = p.cnt;
+  a.ep = ep;
+  a.bias = bias;
+  a.dst = dst;
+  a.ldd = ldd;
+  if (p.Rp == 16) return p.wq8 ? gemm_mt<1, 1>(g.nw, g.kb, a, st) : gemm_mt<1, 0>(g.nw, g.kb, a, st);
+  return p.wq8 ? gemm_mt<2, 1>(g.nw, g.kb, a, st) : gemm_mt<2, 0>(g.nw, g.kb, a, st);
 }
 
-static size_t sstride(const WideParams& p, const WideGemm& g) { return (size_t)p.Rp * g.N; }
-
-static hipError_t resid(const WideParams& p, int mode, const float* P, const WideGemm* g, const float* bias, int t,
-                        const int32_t* toks, const float* lg, const float* lb, hipStream_t st) {
+static hipError_t ln(const WideParams& p, bool emb, const float* g, const float* b, hipStream_t st) {
   const int lda = 4 * p.d;
-  const int ks = g ? g->ks : 0;
-  const size_t ss = g ? sstride(p, *g) : 0;
-  if (p.wq8)
-    hipLaunchKernelGGL(k_w_resid<1>, dim3(p.S), dim3(256), 0, st, mode, P, ks, ss, bias, p.emb, p.emb_s, p.pos, t, toks, p.x, p.d, lg, lb,
-                       p.act, lda);
-  else
-    hipLaunchKernelGGL(k_w_resid<0>, dim3(p.S), dim3(256), 0, st, mode, P, ks, ss, bias, p.emb, p.emb_s, p.pos, t, toks, p.x, p.d, lg, lb,
-                       p.act, lda);
+  const dim3 grid(p.S), blk(256);
+  if (p.wq8) {
+    if (emb)
+      hipLaunchKernelGGL((k_w_ln<1, 1>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos, p.x,
+                         p.d, g, b, p.act, lda);
+    else
+      hipLaunchKernelGGL((k_w_ln<1, 0>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos, p.x,
+                         p.d, g, b, p.act, lda);
+  } else {
+    if (emb)
+      hipLaunchKernelGGL((k_w_ln<0, 1>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos, p.x,
+                         p.d, g, b, p.act, lda);
+    else
+      hipLaunchKernelGGL((k_w_ln<0, 0>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos, p.x,
+                         p.d, g, b, p.act, lda);
+  }
   return hipGetLastError();
 }
 
@@ -587,74 +797,122 @@ static hipError_t resid(const WideParams& p, int mode, const float* P, const Wid
     if (e_ != hipSuccess) return e_;     \
   } while (0)
 
-hipError_t launch_wide(const WideParams& p, hipStream_t st) {
+template <int MT, int WQ8>
+static hipError_t prepare_mt() {
+  WCHK((gemm_attr<MT, WQ8, 1, 4>()));
+  WCHK((gemm_attr<MT, WQ8, 2, 4>()));
+  WCHK((gemm_attr<MT, WQ8, 3, 4>()));
+  WCHK((gemm_attr<MT, WQ8, 4, 4>()));
+  WCHK((gemm_attr<MT, WQ8, 1, 2>()));
+  WCHK((gemm_attr<MT, WQ8, 2, 2>()));
+  return gemm_attr<MT, WQ8, 1, 1>();
+}
+
+hipError_t wide_prepare(int Rp, int wq8) {
+  if (Rp == 16) return wq8 ? prepare_mt<1, 1>() : prepare_mt<1, 0>();
+  return wq8 ? prepare_mt<2, 1>() : prepare_mt<2, 0>();
+}
+
+// The kernels of one step; every per-step value comes from the control block.
+static hipError_t enqueue_step(const WideParams& p, hipStream_t st) {
   const int d = p.d, H = p.H, lda = 4 * d;
   const int rg_rows = (p.X == p.S) ? 1 : 8;
   const int ngroups = (p.X == p.S) ? 1 : (p.S + 7) / 8;
   const size_t cross_lds = (size_t)rg_rows * p.chlen * sizeof(float);
-  for (int i = 0; i < p.nsteps; ++i) {
-    const int t = p.kv_len0 + i;
-    const int pe = t < p.C - 1 ? t : p.C - 1;  // positional row, clamped as the reference
-    const int32_t* toks = i == 0 ? p.tokens0 : (p.forced ? p.forced + (size_t)(i - 1) * p.S : p.next_tok);
-    for (int l = 0; l < p.L; ++l) {
-      const LayerDev& lw = p.layers[l];
-      if (l == 0) {
-        WCHK(resid(p, 0, nullptr, nullptr, nullptr, pe, toks, lw.ln1_g, lw.ln1_b, st));
-      } else {
-        WCHK(resid(p, 1, p.pb, &p.g_2, p.layers[l - 1].b_2, t, toks, lw.ln1_g, lw.ln1_b, st));
-      }
-      WideGemm g = p.g_qkv;
-      g.w = lw.w_qkv;
-      g.ws = lw.s_qkv;
-      WCHK(gemm(p, g, p.pa, st));
-      hipLaunchKernelGGL(k_w_self, dim3(p.S, H), dim3(256), (size_t)(t + 1) * sizeof(float), st, p.pa, g.ks, sstride(p, g), 3 * d,
-                         lw.b_qkv, d, H, l, p.S, p.max_ctx, t, p.kv_k, p.kv_v, p.slots, p.act, lda);
-      WCHK(hipGetLastError());
-      g = p.g_o;
-      g.w = lw.w_o;
-      g.ws = lw.s_o;
-      WCHK(gemm(p, g, p.pa, st));
-      WCHK(resid(p, 1, p.pa, &g, lw.b_o, t, toks, lw.ln2_g, lw.ln2_b, st));
-      g = p.g_cq;
-      g.w = lw.w_cq;
-      g.ws = lw.s_cq;
-      WCHK(gemm(p, g, p.pa, st));
-      if (rg_rows == 1)
-        hipLaunchKernelGGL(k_w_cross<1>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.pa, g.ks, sstride(p, g), d, lw.b_cq, H,
-                           p.A, l, p.L, p.S, p.X, p.chlen, p.nch, p.xk, p.xv, p.cpart);
-      else
-        hipLaunchKernelGGL(k_w_cross<8>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.pa, g.ks, sstride(p, g), d, lw.b_cq, H,
-                           p.A, l, p.L, p.S, p.X, p.chlen, p.nch, p.xk, p.xv, p.cpart);
-      WCHK(hipGetLastError());
-      hipLaunchKernelGGL(k_w_cmerge, dim3(p.S, H), dim3(64), 0, st, p.cpart, H, p.nch, p.act, lda);
-      WCHK(hipGetLastError());
-      g = p.g_co;
-      g.w = lw.w_co;
-      g.ws = lw.s_co;
-      WCHK(gemm(p, g, p.pa, st));
-      WCHK(resid(p, 1, p.pa, &g, lw.b_co, t, toks, lw.ln3_g, lw.ln3_b, st));
-      g = p.g_1;
-      g.w = lw.w_1;
-      g.ws = lw.s_1;
-      WCHK(gemm(p, g, p.pa, st));
-      hipLaunchKernelGGL(k_w_gelu, dim3((p.S * 4 * d + 255) / 256), dim3(256), 0, st, p.pa, g.ks, sstride(p, g), lw.b_1, p.S, 4 * d, p.act,
-                         lda);
-      WCHK(hipGetLastError());
-      g = p.g_2;
-      g.w = lw.w_2;
-      g.ws = lw.s_2;
-      WCHK(gemm(p, g, p.pb, st));
-    }
-    WCHK(resid(p, 1, p.pb, &p.g_2, p.layers[p.L - 1].b_2, t, toks, p.lnf_g, p.lnf_b, st));
-    WCHK(gemm(p, p.g_v, p.pa, st));
-    const int nblk = (p.nsel + 3) / 4;
-    hipLaunchKernelGGL(k_w_select, dim3(p.S, nblk), dim3(256), 0, st, p.pa, p.g_v.ks, sstride(p, p.g_v), p.V, p.mask, p.mask2, p.mw,
-                       p.probe, p.topk, p.selp, p.nsel, p.logits_out ? p.logits_out + (size_t)i * p.S * p.V : nullptr);
+  const size_t self_lds = (size_t)(p.max_ctx + 1) * sizeof(float);
+  for (int l = 0; l < p.L; ++l) {
+    const LayerDev& lw = p.layers[l];
+    WCHK(ln(p, l == 0, lw.ln1_g, lw.ln1_b, st));
+    WCHK(gemm(p, p.g_qkv, lw.w_qkv, lw.s_qkv, p.act, EP_STORE, lw.b_qkv, p.qkv, 3 * d, st));
+    hipLaunchKernelGGL(k_w_self, dim3(p.S, H), dim3(256), self_lds, st, p.ctl, p.qkv, d, H, l, p.S, p.max_ctx, p.kv_k, p.kv_v, p.slots,
+                       p.act, lda);
     WCHK(hipGetLastError());
-    hipLaunchKernelGGL(k_w_selmerge, dim3(p.S), dim3(64), 0, st, p.selp, p.nsel, p.topk, p.out ? p.out + (size_t)i * p.S : nullptr,
-                       p.next_tok);
+    WCHK(gemm(p, p.g_o, lw.w_o, lw.s_o, p.act, EP_RESID, lw.b_o, p.x, d, st));
+    WCHK(ln(p, false, lw.ln2_g, lw.ln2_b, st));
+    WCHK(gemm(p, p.g_cq, lw.w_cq, lw.s_cq, p.act, EP_STORE, lw.b_cq, p.qkv, d, st));
+    if (rg_rows == 1)
+      hipLaunchKernelGGL(k_w_cross<1>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.qkv, d, H, p.A, l, p.L, p.S, p.X,
+                         p.chlen, p.nch, p.xk, p.xv, p.cpart);
+    else
+      hipLaunchKernelGGL(k_w_cross<8>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.qkv, d, H, p.A, l, p.L, p.S, p.X,
+                         p.chlen, p.nch, p.xk, p.xv, p.cpart);
     WCHK(hipGetLastError());
+    hipLaunchKernelGGL(k_w_cmerge, dim3(p.S, H), dim3(64), 0, st, p.cpart, H, p.nch, p.act, lda);
+    WCHK(hipGetLastError());
+    WCHK(gemm(p, p.g_co, lw.w_co, lw.s_co, p.act, EP_RESID, lw.b_co, p.x, d, st));
+    WCHK(ln(p, false, lw.ln3_g, lw.ln3_b, st));
+    WCHK(gemm(p, p.g_1, lw.w_1, lw.s_1, p.act, EP_GELU, lw.b_1, p.hid, lda, st));
+    WCHK(gemm(p, p.g_2, lw.w_2, lw.s_2, p.hid, EP_RESID, lw.b_2, p.x, d, st));
   }
+  WCHK(ln(p, false, p.lnf_g, p.lnf_b, st));
+  WCHK(gemm(p, p.g_v, p.emb, p.emb_s, p.act, EP_STORE, nullptr, p.lgt, p.V, st));
+  const int nblk = (p.nsel + 3) / 4;
+  hipLaunchKernelGGL(k_w_select, dim3(p.S, nblk), dim3(256), 0, st, p.ctl, p.lgt, p.S, p.V, p.mask, p.mask2, p.mw, p.selp, p.nsel,
+                     p.logits_out);
+  WCHK(hipGetLastError());
+  hipLaunchKernelGGL(k_w_selmerge, dim3(p.S), dim3(64), 0, st, p.ctl, p.selp, p.S, p.nsel, p.out, p.next_tok);
+  return hipGetLastError();
+}
+
+void wide_graph_release(WideGraph* g) {
+  if (g && g->exec) {
+    (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(g->exec));
+    g->exec = nullptr;
+  }
+}
+
+hipError_t launch_wide(const WideParams& p, hipStream_t st) {
+  WideCtl c{};
+  c.i = 0;
+  c.kv_len0 = p.kv_len0;
+  c.forced_on = p.forced != nullptr;
+  c.out_on = p.out != nullptr;
+  c.logits_on = p.logits_out != nullptr;
+  c.mask_on = p.mask != nullptr;
+  c.mask2_on = p.mask2 != nullptr;
+  c.slots_on = p.slots != nullptr;
+  c.topk = p.topk;
+  c.probe = p.probe;
+  c.done = 0;
+  hipLaunchKernelGGL(k_w_setctl, dim3(1), dim3(64), 0, st, p.ctl, c);
+  WCHK(hipGetLastError());
+  if (!p.graph) {
+    for (int i = 0; i < p.nsteps; ++i) WCHK(enqueue_step(p, st));
+    return hipSuccess;
+  }
+  // Buffers a step reads or writes that may be (re)allocated between runs: the captured step is
+  // valid while they stay where they were.
+  const void* key[8] = {p.tokens0, p.forced, p.out, p.logits_out, p.mask2, p.mask, p.slots, p.ctl};
+  bool same = p.graph->exec != nullptr;
+  for (int k = 0; k < 8 && same; ++k) same = key[k] == nullptr || key[k] == p.graph->key[k];
+  if (!same) {
+    // capture with every optional buffer present in the key, so later runs that leave some out
+    // (null: switched off in the control block) replay the same graph
+    WideParams q = p;
+    for (int k = 0; k < 8; ++k)
+      if (key[k] == nullptr) key[k] = p.graph->key[k];
+    q.tokens0 = static_cast<const int32_t*>(key[0]);
+    q.forced = static_cast<const int32_t*>(key[1]);
+    q.out = static_cast<w4h_step_out*>(const_cast<void*>(key[2]));
+    q.logits_out = static_cast<float*>(const_cast<void*>(key[3]));
+    q.mask2 = static_cast<const uint32_t*>(key[4]);
+    q.mask = static_cast<const uint32_t*>(key[5]);
+    q.slots = static_cast<const int32_t*>(key[6]);
+    wide_graph_release(p.graph);
+    hipGraph_t graph = nullptr;
+    WCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    const hipError_t ce = enqueue_step(q, st);
+    const hipError_t ee = hipStreamEndCapture(st, &graph);
+    WCHK(ce);
+    WCHK(ee);
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    WCHK(ie);
+    p.graph->exec = exec;
+    for (int k = 0; k < 8; ++k) p.graph->key[k] = key[k];
+  }
+  for (int i = 0; i < p.nsteps; ++i) WCHK(hipGraphLaunch(static_cast<hipGraphExec_t>(p.graph->exec), st));
   return hipSuccess;
 }
 
