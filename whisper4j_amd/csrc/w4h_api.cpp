@@ -416,7 +416,7 @@ struct w4h_session {
   bool wide = false;
   int Rp = 0, nch = 0, chlen = 0, nsel = 0;
   WideGemm g_qkv{}, g_o{}, g_cq{}, g_co{}, g_1{}, g_2{}, g_v{};
-  DevBuf wx, wact, whid, wqkv, wlgt, wpart, wcnt, wcpart, wselp, wnext, wctl;
+  DevBuf wx, wact, whid, wpart, wcpart, wselp, wnext, wctl;
   WideGraph wgraph;
   bool use_graph = true;
 };
@@ -500,10 +500,7 @@ static WideParams wide_params(w4h_session* s) {
   p.x = s->wx.as<float>();
   p.act = s->wact.as<float>();
   p.hid = s->whid.as<float>();
-  p.qkv = s->wqkv.as<float>();
-  p.lgt = s->wlgt.as<float>();
   p.part = s->wpart.as<float>();
-  p.cnt = s->wcnt.as<unsigned>();
   p.cpart = s->wcpart.as<float>();
   p.selp = s->wselp.as<float>();
   p.next_tok = s->wnext.as<int32_t>();
@@ -681,12 +678,7 @@ int create_wide(std::unique_ptr<w4h_session>& s, const hipDeviceProp_t& prop, w4
   HIPCHK(hipMemset(s->wact.p, 0, sizeof(float) * (size_t)s->Rp * 4 * d));
   if ((rc = s->whid.alloc(sizeof(float) * (size_t)s->Rp * 4 * d))) return rc;
   HIPCHK(hipMemset(s->whid.p, 0, sizeof(float) * (size_t)s->Rp * 4 * d));
-  if ((rc = s->wqkv.alloc(sizeof(float) * (size_t)s->S * 3 * d))) return rc;
-  if ((rc = s->wlgt.alloc(sizeof(float) * (size_t)s->S * V))) return rc;
   if ((rc = s->wpart.alloc(sizeof(float) * pmax))) return rc;
-  const size_t ncnt = (size_t)(std::max(V, 4 * d) + 15) / 16 + 16;  // column blocks of the widest GEMM
-  if ((rc = s->wcnt.alloc(sizeof(unsigned) * ncnt))) return rc;
-  HIPCHK(hipMemset(s->wcnt.p, 0, sizeof(unsigned) * ncnt));
   if ((rc = s->wcpart.alloc(sizeof(float) * (size_t)s->S * H * s->nch * kPartWords))) return rc;
   if ((rc = s->wselp.alloc(sizeof(float) * (size_t)s->S * s->nsel * kSelWords))) return rc;
   if ((rc = s->wnext.alloc(sizeof(int32_t) * s->S))) return rc;

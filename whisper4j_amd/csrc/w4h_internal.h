@@ -78,14 +78,15 @@ constexpr int kWideMaxRows = 32;
 constexpr int kWideCols = 64;        // output columns per GEMM workgroup (16 per wave)
 constexpr int kWideKBlock = 128;     // k per block: four 16x16x32 MFMA steps
 constexpr int kWideSelChunk = 512;   // vocabulary entries per selection partial (one wave)
+constexpr int kWideMaxSlices = 16;   // k slices per GEMM at most (consumers add every slice)
 
 // One GEMM of the wide engine: out[ks][Rp][N] = act[:, ks-th k slice] . W[N][K]^T.
 struct WideGemm {
   const void* w;         // [N][K] f16, or int8 with f16 scales [N][K/32] in ws
   const uint16_t* ws;
   int N, K;
-  int nw;                // column groups of 16 per workgroup (4, 2, 1); the 4 / nw waves of a
-                         // column group split the workgroup's k range
+  int nw;                // column groups of 16 per workgroup (4: one per wave); with fewer, the
+                         // 4 / nw waves of a column group split the workgroup's k range
   int kb;                // 128-blocks per wave; a workgroup covers (4 / nw) * kb blocks
   int ks;                // number of k slices (workgroups per column block)
 };
@@ -121,10 +122,7 @@ struct WideParams {
   float* x;                 // [S][d] residual stream
   float* act;               // [Rp][4d] GEMM input rows: LN outputs, attention outputs
   float* hid;               // [Rp][4d] MLP hidden rows (GELU output, MLP2 input)
-  float* qkv;               // [S][3d] QKV projection rows, then cross-attention query rows
-  float* lgt;               // [S][V] logits
   float* part;              // GEMM split-K partial sums [slices][Rp][N] (largest GEMM)
-  unsigned* cnt;            // split-K arrival counters, one per 64-column block (zero at rest)
   float* cpart;             // [S][H][nch][kPartWords] cross-attention chunk partials
   float* selp;              // [S][nsel][kSelWords] selection partials
   int32_t* next_tok;        // [S] argmax of the last step (greedy feedback)

@@ -2,10 +2,10 @@
 // streams, up to 32) advance one token per step through a sequence of ordinary kernels, and every
 // projection is an MFMA GEMM over all rows at once (v_mfma_f32_16x16x32_f16).
 //
-// Per layer:  LN1 -> QKV GEMM (+bias) -> self-attention (KV append) -> out GEMM (x += .) -> LN2 ->
-//             cross-q GEMM (+bias) -> cross-attention chunks -> chunk merge -> cross-out GEMM (x += .)
-//             -> LN3 -> MLP1 GEMM (GELU) -> MLP2 GEMM (x += .)
-// then final LN -> tied logits GEMM -> selection partials -> selection merge (+ next token).
+// Per layer:  residual + LN1 -> QKV GEMM -> self-attention (KV append) -> out GEMM -> residual + LN2 ->
+//             cross-q GEMM -> cross-attention chunks -> chunk merge -> cross-out GEMM -> residual + LN3
+//             -> MLP1 GEMM -> GELU -> MLP2 GEMM
+// then residual + final LN -> tied logits GEMM -> selection partials -> selection merge (+ next token).
 //
 // Numerics.  Activations are fp32.  A GEMM stages its activation slice in LDS as two f16 parts,
 // hi = f16(a) and lo = f16(a - hi), and runs every MFMA twice (hi and lo) against the same f16
@@ -14,11 +14,10 @@
 // block, whose f16 scale is applied to the step's fp32 result.  The self-KV cache is f16, as in the
 // persistent step kernel; the current token's key and value are used in fp32.
 //
-// Split-K.  A GEMM splits K into slices (one workgroup per 64 output columns and slice).  Each
-// workgroup stores its partial sums with device-coherent stores, waits for them to complete and
-// counts itself in the column block's arrival counter; the last workgroup to arrive adds the
-// slices in slice order (so the result does not depend on arrival order), applies the epilogue
-// (bias; bias + residual add; bias + GELU) and resets the counter for the next GEMM.
+// Split-K.  A GEMM splits K into slices (one workgroup per 64 output columns and slice) and stores
+// one partial sum per slice, out[slice][row][N]; the next kernel, which reads every value anyway,
+// adds the slices in slice order together with the bias (and residual, GELU), so a GEMM ends with
+// its stores and no workgroup waits for another.
 
 #include "w4h_kernels.h"
 
@@ -29,8 +28,6 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPadH = 8;  // halves of padding per LDS activation row (16 bytes: spreads banks)
 constexpr int kSliceBatch = 4;  // slices whose partials a reducing thread loads at once
-
-enum { EP_STORE = 0, EP_RESID = 1, EP_GELU = 2 };
 
 DEV half8 as_half8(uint4 u) {
   half8 h;
@@ -49,29 +46,27 @@ DEV half8 i8x8_to_h8(uint2 u) {
   return h;
 }
 
-DEV void st_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-DEV float ld_dev(const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-
 struct GemmArgs {
   const void* w;         // [N][K] f16, or int8 with f16 scales [N][K/32] in ws
   const uint16_t* ws;
-  int N, K, ks;          // ks: number of k slices (gridDim.y)
+  int N, K;
   const float* act;      // [Rp][lda] fp32 rows (rows >= S read as zero)
   int lda, S;
-  float* part;           // [ks][Rp][N] partial sums (ks > 1)
-  unsigned* cnt;         // [ceil(N/64)] arrival counters, zero between GEMMs
-  int ep;                // EP_*
-  const float* bias;     // [N] or null
-  float* dst;            // [S][ldd]
-  int ldd;
+  float* part;           // [slices][Rp][N] partial sums (rows < S written)
 };
 
-DEV void epilogue(const GemmArgs& a, int r, int n, float v) {
-  const float b = a.bias ? a.bias[n] : 0.f;
-  float* o = a.dst + (size_t)r * a.ldd + n;
-  if (a.ep == EP_STORE) *o = v + b;
-  else if (a.ep == EP_RESID) *o = *o + (v + b);
-  else *o = gelu_f16(v + b);
+// Sum of the ks slices of a GEMM output at p[j * ss + idx]: kSliceBatch loads in flight, added in
+// slice order.
+DEV float slice_sum(const float* p, int ks, size_t ss, size_t idx) {
+  float v = 0.f;
+  for (int j = 0; j < ks; j += kSliceBatch) {
+    float t[kSliceBatch];
+#pragma unroll
+    for (int u = 0; u < kSliceBatch; ++u) t[u] = j + u < ks ? p[(size_t)(j + u) * ss + idx] : 0.f;
+#pragma unroll
+    for (int u = 0; u < kSliceBatch; ++u) v += t[u];
+  }
+  return v;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -87,7 +82,6 @@ DEV void epilogue(const GemmArgs& a, int r, int n, float v) {
 template <int MT, int WQ8, int KB, int NW>
 __global__ __launch_bounds__(256) void k_w_gemm(GemmArgs a) {
   extern __shared__ __align__(16) uint16_t lds_h[];
-  __shared__ int s_last;
   constexpr int KW = 4 / NW;
   constexpr int Rp = MT * 16;
   constexpr int CB = 16 * NW;                // columns per workgroup
@@ -208,110 +202,85 @@ __global__ __launch_bounds__(256) void k_w_gemm(GemmArgs a) {
           for (int j = 0; j < 4; ++j) acc[m][j] += red[(((q - 1) * NW + cg) * MT * 4 + m * 4 + j) * 64 + lane];
   }
 
-  // 5. lane holds rows 4(i/16) + [0, 4) of each 16-row tile, column n
-  if (a.ks == 1) {
-    if (kw == 0 && n < N) {
-#pragma unroll
-      for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r = m * 16 + 4 * g4 + j;
-          if (r < a.S) epilogue(a, r, n, acc[m][j]);
-        }
-    }
-    return;
-  }
+  // 5. partial sums of this slice: lane holds rows 4(i/16) + [0, 4) of each 16-row tile, column n
   if (kw == 0 && n < N) {
     float* o = a.part + (size_t)blockIdx.y * Rp * N + n;
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        if (m * 16 + 4 * g4 + j < a.S) st_dev(o + (size_t)(m * 16 + 4 * g4 + j) * N, acc[m][j]);
-  }
-  kv_drain();  // this wave's partial stores have completed
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(a.cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == (unsigned)(a.ks - 1);
-    if (s_last) __hip_atomic_store(a.cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  // last arrival: thread (row group tid / CB, column tid % CB) adds the slices in slice order
-  constexpr int RG = 256 / CB;    // row groups
-  constexpr int RPT = Rp / RG;    // rows per thread
-  const int nc = blockIdx.x * CB + (tid % CB);
-  if (nc >= N) return;
-  float sum[RPT];
-#pragma unroll
-  for (int i = 0; i < RPT; ++i) sum[i] = 0.f;
-  for (int z0 = 0; z0 < a.ks; z0 += kSliceBatch) {
-    float t[RPT][kSliceBatch];
-#pragma unroll
-    for (int i = 0; i < RPT; ++i)
-#pragma unroll
-      for (int u = 0; u < kSliceBatch; ++u) {
-        const int r = tid / CB + RG * i;
-        t[i][u] = (z0 + u < a.ks && r < a.S) ? ld_dev(a.part + ((size_t)(z0 + u) * Rp + r) * N + nc) : 0.f;
-      }
-#pragma unroll
-    for (int i = 0; i < RPT; ++i)
-#pragma unroll
-      for (int u = 0; u < kSliceBatch; ++u) sum[i] += t[i][u];
-  }
-#pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    const int r = tid / CB + RG * i;
-    if (r < a.S) epilogue(a, r, nc, sum[i]);
+        if (m * 16 + 4 * g4 + j < a.S) o[(size_t)(m * 16 + 4 * g4 + j) * N] = acc[m][j];
   }
 }
 
 // ------------------------------------------------------------------------------------------------
-// LayerNorm of the residual rows, one workgroup per row: act[row] = LN(x[row]).  With tokens, the
-// row is first set to token embedding + positional row pe (layer 0).  Two passes, eps 1e-5, as
-// nn/LayerNorm.java:5-31.
+// Residual update + LayerNorm, one workgroup per row.  EMB: x = token embedding + positional row
+// (layer 0).  Otherwise x += bias + the slices of the last GEMM (out-projection, cross-out or MLP2).
+// Then act[row] = LN(x[row]), two passes, eps 1e-5, as nn/LayerNorm.java:5-31.
 
 constexpr int kWideVec = 8;  // d <= 8 * 256
 
 template <int WQ8, int EMB>
-__global__ __launch_bounds__(256) void k_w_ln(const WideCtl* __restrict__ ctl, const int32_t* __restrict__ tokens0,
-                                              const int32_t* __restrict__ forced, const int32_t* __restrict__ next_tok, int S, int C,
-                                              const void* __restrict__ emb, const uint16_t* __restrict__ emb_s,
-                                              const float* __restrict__ pos, float* __restrict__ x, int d,
-                                              const float* __restrict__ g, const float* __restrict__ b, float* __restrict__ act,
-                                              int lda) {
+__global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl, const int32_t* __restrict__ tokens0,
+                                                 const int32_t* __restrict__ forced, const int32_t* __restrict__ next_tok, int S, int C,
+                                                 const void* __restrict__ emb, const uint16_t* __restrict__ emb_s,
+                                                 const float* __restrict__ pos, const float* __restrict__ P, int ks, size_t ss,
+                                                 const float* __restrict__ bias, float* __restrict__ x, int d,
+                                                 const float* __restrict__ g, const float* __restrict__ b, float* __restrict__ act,
+                                                 int lda) {
   __shared__ float red[8];
   const int s = blockIdx.x, tid = threadIdx.x;
   float v[kWideVec];
-  float sum = 0.f;
-  int tk = 0, pe = 0;
   if (EMB) {
     // token of this step: the run's first tokens, the forced row, or the last step's argmax;
     // positional row clamped as the reference
-    const int i = ctl->i, t = ctl->kv_len0 + i;
-    pe = t < C - 1 ? t : C - 1;
-    tk = i == 0 ? tokens0[s] : (ctl->forced_on ? forced[(size_t)(i - 1) * S + s] : next_tok[s]);
-  }
+    const int i0 = ctl->i, t = ctl->kv_len0 + i0;
+    const int pe = t < C - 1 ? t : C - 1;
+    const int tk = i0 == 0 ? tokens0[s] : (ctl->forced_on ? forced[(size_t)(i0 - 1) * S + s] : next_tok[s]);
 #pragma unroll
-  for (int i = 0; i < kWideVec; ++i) {
-    const int j = tid + 256 * i;
-    v[i] = 0.f;
-    if (j < d) {
-      float xv;
-      if (EMB) {
+    for (int i = 0; i < kWideVec; ++i) {
+      const int j = tid + 256 * i;
+      v[i] = 0.f;
+      if (j < d) {
         float e;
         if (!WQ8) e = h2f(static_cast<const uint16_t*>(emb)[(size_t)tk * d + j]);
         else e = (float)static_cast<const int8_t*>(emb)[(size_t)tk * d + j] * h2f(emb_s[(size_t)tk * (d >> 5) + (j >> 5)]);
-        xv = e + pos[(size_t)pe * d + j];
-        x[(size_t)s * d + j] = xv;
-      } else {
-        xv = x[(size_t)s * d + j];
+        v[i] = e + pos[(size_t)pe * d + j];
+        x[(size_t)s * d + j] = v[i];
       }
-      v[i] = xv;
-      sum += xv;
+    }
+  } else {
+    // slices added in slice order, kSliceBatch slices of every element in flight
+    float acc[kWideVec];
+#pragma unroll
+    for (int i = 0; i < kWideVec; ++i) acc[i] = 0.f;
+    for (int z = 0; z < ks; z += kSliceBatch) {
+      float t[kWideVec][kSliceBatch];
+#pragma unroll
+      for (int i = 0; i < kWideVec; ++i)
+#pragma unroll
+        for (int u = 0; u < kSliceBatch; ++u) {
+          const int j = tid + 256 * i;
+          t[i][u] = (j < d && z + u < ks) ? P[(size_t)(z + u) * ss + (size_t)s * d + j] : 0.f;
+        }
+#pragma unroll
+      for (int i = 0; i < kWideVec; ++i)
+#pragma unroll
+        for (int u = 0; u < kSliceBatch; ++u) acc[i] += t[i][u];
+    }
+#pragma unroll
+    for (int i = 0; i < kWideVec; ++i) {
+      const int j = tid + 256 * i;
+      v[i] = 0.f;
+      if (j < d) {
+        v[i] = x[(size_t)s * d + j] + (bias[j] + acc[i]);
+        x[(size_t)s * d + j] = v[i];
+      }
     }
   }
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < kWideVec; ++i) sum += v[i];
   sum = wave_sum(sum);
   if ((tid & 63) == 0) red[tid >> 6] = sum;
   __syncthreads();
@@ -331,16 +300,26 @@ __global__ __launch_bounds__(256) void k_w_ln(const WideCtl* __restrict__ ctl, c
   }
 }
 
+// act[r][k] = GELU(bias[k] + the slices of the MLP1 GEMM), r < S, k < n.
+__global__ __launch_bounds__(256) void k_w_gelu(const float* __restrict__ P, int ks, size_t ss, const float* __restrict__ bias, int S,
+                                                int n, float* __restrict__ act, int lda) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= S * n) return;
+  const int r = i / n, k = i - r * n;
+  act[(size_t)r * lda + k] = gelu_f16(bias[k] + slice_sum(P, ks, ss, (size_t)r * n + k));
+}
+
 // ------------------------------------------------------------------------------------------------
-// Self-attention of one (row, head): q, k, v from the QKV rows qkv[s][3d]; k, v appended to the
+// Self-attention of one (row, head): q, k, v = bias + the QKV GEMM slices; k, v appended to the
 // cache at position t (f16); softmax over the t cached keys (row s reads position j from slot
 // slots[s][j]) plus the current key (fp32); output -> act[s][h*64, +64).  8 lanes per key, 16 bytes
 // each; four keys per lane group in flight.
 
 constexpr int kKeysInFlight = 4;
 
-__global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl, const float* __restrict__ qkv, int d, int H, int l,
-                                                int S, int max_ctx, uint16_t* __restrict__ kvk, uint16_t* __restrict__ kvv,
+__global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl, const float* __restrict__ P, int ks, size_t ss,
+                                                const float* __restrict__ bqkv, int d, int H, int l, int S, int max_ctx,
+                                                uint16_t* __restrict__ kvk, uint16_t* __restrict__ kvv,
                                                 const int32_t* __restrict__ slot_table, float* __restrict__ act, int lda) {
   extern __shared__ float sc[];  // [t + 1] scores, then probabilities
   __shared__ float q[64], kc[64], vc[64], red[4 * 64], stat[8];
@@ -350,7 +329,8 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
   const size_t head_base = ((size_t)l * S * H) * max_ctx * kHeadDim;  // layer l
   if (tid < 192) {
     const int part = tid >> 6, e = tid & 63;
-    const float v = qkv[(size_t)s * 3 * d + part * d + h * kHeadDim + e];
+    const int col = part * d + h * kHeadDim + e;
+    const float v = bqkv[col] + slice_sum(P, ks, ss, (size_t)s * 3 * d + col);
     if (part == 0) q[e] = v;
     else if (part == 1) kc[e] = v;
     else vc[e] = v;
@@ -465,8 +445,9 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
 // shared encoder's K/V chunk is read once per group.  Partial (m, l, acc[64]) per row.
 
 template <int RG>
-__global__ __launch_bounds__(256) void k_w_cross(const float* __restrict__ cq, int d, int H, int A, int l, int L, int S, int X,
-                                                 int chlen, int nch, const uint16_t* __restrict__ xk,
+__global__ __launch_bounds__(256) void k_w_cross(const float* __restrict__ P, int ks, size_t ss, const float* __restrict__ bcq, int d,
+                                                 int H, int A, int l, int L, int S, int X, int chlen, int nch,
+                                                 const uint16_t* __restrict__ xk,
                                                  const uint16_t* __restrict__ xv, float* __restrict__ cpart) {
   extern __shared__ float scs[];  // [RG][chlen]
   __shared__ float q[RG * 64], red[4 * RG * 64], rm[RG], rl[RG];
@@ -482,7 +463,8 @@ __global__ __launch_bounds__(256) void k_w_cross(const float* __restrict__ cq, i
   }
   for (int i = tid; i < nr * 64; i += 256) {
     const int r = i >> 6, k = i & 63;
-    q[i] = cq[(size_t)(r0 + r) * d + h * kHeadDim + k] * 0.125f;
+    const int col = h * kHeadDim + k;
+    q[i] = (bcq[col] + slice_sum(P, ks, ss, (size_t)(r0 + r) * d + col)) * 0.125f;
   }
   __syncthreads();
   const int j0 = c * chlen, j1 = min(A, j0 + chlen), n = j1 - j0;
@@ -621,7 +603,8 @@ __global__ __launch_bounds__(64) void k_w_cmerge(const float* __restrict__ cpart
 // per row merges the partials into the step result and the next token (argmax, first index of the
 // maximum).
 
-__global__ __launch_bounds__(256) void k_w_select(const WideCtl* __restrict__ ctl, const float* __restrict__ lgt, int S, int V,
+__global__ __launch_bounds__(256) void k_w_select(const WideCtl* __restrict__ ctl, const float* __restrict__ P, int ks, size_t ss,
+                                                  int S, int V,
                                                   const uint32_t* mask_buf, const uint32_t* mask2_buf, int mw,
                                                   float* __restrict__ selp, int nsel, float* __restrict__ logits_buf) {
   __shared__ float lg[4][kWideSelChunk], rw[4][kWideSelChunk];
@@ -636,7 +619,7 @@ __global__ __launch_bounds__(256) void k_w_select(const WideCtl* __restrict__ ct
   const int nl = max(0, min(kWideSelChunk, V - v0));
   for (int j = lane; j < nl; j += 64) {
     const int v = v0 + j;
-    const float x = lgt[(size_t)s * V + v];
+    const float x = slice_sum(P, ks, ss, (size_t)s * V + v);
     rw[wv][j] = x;
     lg[wv][j] = (masked(mask, mw, s, v) || masked(mask2, mw, s, v)) ? -INFINITY : x;
     idx[wv][j] = v;
@@ -683,35 +666,16 @@ WideGemm wide_plan(const void* w, const uint16_t* ws, int N, int K, int n_cu) {
   g.N = N;
   g.K = K;
   const int kbt = K / kWideKBlock;
-  // Candidates: NW column groups of 16 (KW = 4/NW k parts per workgroup) and KB blocks of 128 per
-  // part, with at most 4 blocks per workgroup (LDS).  Fewest k slices among the candidates that give
-  // at least one workgroup per compute unit; ties to the widest column tile (least activation
-  // staging per weight byte).  If none does, the most workgroups.
-  int best_nw = 4, best_kb = 1, best_ks = 1 << 30;
-  long best_wg = -1;
-  bool best_ok = false;
-  for (int nw : {4, 2, 1}) {
-    const int kw = 4 / nw;
-    for (int kb = 1; kb * kw <= 4; ++kb) {
-      const int ks = (kbt + kw * kb - 1) / (kw * kb);
-      const long wg = (long)((N + 16 * nw - 1) / (16 * nw)) * ks;
-      const bool ok = wg >= n_cu;
-      bool take;
-      if (ok != best_ok) take = ok;
-      else if (ok) take = ks < best_ks;
-      else take = wg > best_wg;
-      if (take) {
-        best_ok = ok;
-        best_nw = nw;
-        best_kb = kb;
-        best_ks = ks;
-        best_wg = wg;
-      }
-    }
-  }
-  g.nw = best_nw;
-  g.kb = best_kb;
-  g.ks = best_ks;
+  const int nblk = (N + kWideCols - 1) / kWideCols;
+  // Workgroups of 64 columns (4 waves of 16).  Slices of kb blocks of 128: the longest slice that
+  // still gives every compute unit two workgroups, but no more than kWideMaxSlices slices (each
+  // consumer adds every slice).
+  int kb = 4;
+  while (kb > 1 && nblk * ((kbt + kb - 1) / kb) < 2 * n_cu) --kb;
+  while (kb < 4 && (kbt + kb - 1) / kb > kWideMaxSlices) ++kb;
+  g.nw = 4;
+  g.kb = kb;
+  g.ks = (kbt + kb - 1) / kb;
   return g;
 }
 
@@ -727,66 +691,61 @@ static hipError_t gemm_attr() {
 }
 
 template <int MT, int WQ8, int KB, int NW>
-static hipError_t gemm_launch(const GemmArgs& a, hipStream_t st) {
-  const dim3 grid((a.N + 16 * NW - 1) / (16 * NW), a.ks);
+static hipError_t gemm_launch(const GemmArgs& a, int ks, hipStream_t st) {
+  const dim3 grid((a.N + 16 * NW - 1) / (16 * NW), ks);
   constexpr size_t lds = gemm_lds<MT, KB, NW>();
   hipLaunchKernelGGL((k_w_gemm<MT, WQ8, KB, NW>), grid, dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
 template <int MT, int WQ8>
-static hipError_t gemm_mt(int nw, int kb, const GemmArgs& a, hipStream_t st) {
-  if (nw == 4) {
-    switch (kb) {
-      case 1: return gemm_launch<MT, WQ8, 1, 4>(a, st);
-      case 2: return gemm_launch<MT, WQ8, 2, 4>(a, st);
-      case 3: return gemm_launch<MT, WQ8, 3, 4>(a, st);
-      default: return gemm_launch<MT, WQ8, 4, 4>(a, st);
-    }
+static hipError_t gemm_mt(int kb, const GemmArgs& a, int ks, hipStream_t st) {
+  switch (kb) {
+    case 1: return gemm_launch<MT, WQ8, 1, 4>(a, ks, st);
+    case 2: return gemm_launch<MT, WQ8, 2, 4>(a, ks, st);
+    case 3: return gemm_launch<MT, WQ8, 3, 4>(a, ks, st);
+    default: return gemm_launch<MT, WQ8, 4, 4>(a, ks, st);
   }
-  if (nw == 2) return kb == 1 ? gemm_launch<MT, WQ8, 1, 2>(a, st) : gemm_launch<MT, WQ8, 2, 2>(a, st);
-  return gemm_launch<MT, WQ8, 1, 1>(a, st);
 }
 
-// One GEMM of the step: act (GEMM input rows) times the weights, epilogue ep into dst.
-static hipError_t gemm(const WideParams& p, const WideGemm& g, const void* w, const uint16_t* ws, const float* act, int ep,
-                       const float* bias, float* dst, int ldd, hipStream_t st) {
+// One GEMM of the step: act rows (row stride 4d) times the weights -> partial sums in p.part.
+static hipError_t gemm(const WideParams& p, const WideGemm& g, const void* w, const uint16_t* ws, const float* act, hipStream_t st) {
   GemmArgs a{};
   a.w = w;
   a.ws = ws;
   a.N = g.N;
   a.K = g.K;
-  a.ks = g.ks;
   a.act = act;
   a.lda = 4 * p.d;
   a.S = p.S;
   a.part = p.part;
-  a.cnt = p.cnt;
-  a.ep = ep;
-  a.bias = bias;
-  a.dst = dst;
-  a.ldd = ldd;
-  if (p.Rp == 16) return p.wq8 ? gemm_mt<1, 1>(g.nw, g.kb, a, st) : gemm_mt<1, 0>(g.nw, g.kb, a, st);
-  return p.wq8 ? gemm_mt<2, 1>(g.nw, g.kb, a, st) : gemm_mt<2, 0>(g.nw, g.kb, a, st);
+  if (p.Rp == 16) return p.wq8 ? gemm_mt<1, 1>(g.kb, a, g.ks, st) : gemm_mt<1, 0>(g.kb, a, g.ks, st);
+  return p.wq8 ? gemm_mt<2, 1>(g.kb, a, g.ks, st) : gemm_mt<2, 0>(g.kb, a, g.ks, st);
 }
 
-static hipError_t ln(const WideParams& p, bool emb, const float* g, const float* b, hipStream_t st) {
+static size_t sstride(const WideParams& p, const WideGemm& g) { return (size_t)p.Rp * g.N; }
+
+// Residual update (or layer-0 embedding when g_prev is null) + LayerNorm (lg, lb) -> act.
+static hipError_t resid(const WideParams& p, const WideGemm* g_prev, const float* bias, const float* lg, const float* lb,
+                        hipStream_t st) {
   const int lda = 4 * p.d;
   const dim3 grid(p.S), blk(256);
+  const int ks = g_prev ? g_prev->ks : 0;
+  const size_t ss = g_prev ? sstride(p, *g_prev) : 0;
   if (p.wq8) {
-    if (emb)
-      hipLaunchKernelGGL((k_w_ln<1, 1>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos, p.x,
-                         p.d, g, b, p.act, lda);
+    if (!g_prev)
+      hipLaunchKernelGGL((k_w_resid<1, 1>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos,
+                         p.part, ks, ss, bias, p.x, p.d, lg, lb, p.act, lda);
     else
-      hipLaunchKernelGGL((k_w_ln<1, 0>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos, p.x,
-                         p.d, g, b, p.act, lda);
+      hipLaunchKernelGGL((k_w_resid<1, 0>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos,
+                         p.part, ks, ss, bias, p.x, p.d, lg, lb, p.act, lda);
   } else {
-    if (emb)
-      hipLaunchKernelGGL((k_w_ln<0, 1>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos, p.x,
-                         p.d, g, b, p.act, lda);
+    if (!g_prev)
+      hipLaunchKernelGGL((k_w_resid<0, 1>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos,
+                         p.part, ks, ss, bias, p.x, p.d, lg, lb, p.act, lda);
     else
-      hipLaunchKernelGGL((k_w_ln<0, 0>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos, p.x,
-                         p.d, g, b, p.act, lda);
+      hipLaunchKernelGGL((k_w_resid<0, 0>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos,
+                         p.part, ks, ss, bias, p.x, p.d, lg, lb, p.act, lda);
   }
   return hipGetLastError();
 }
@@ -802,10 +761,7 @@ static hipError_t prepare_mt() {
   WCHK((gemm_attr<MT, WQ8, 1, 4>()));
   WCHK((gemm_attr<MT, WQ8, 2, 4>()));
   WCHK((gemm_attr<MT, WQ8, 3, 4>()));
-  WCHK((gemm_attr<MT, WQ8, 4, 4>()));
-  WCHK((gemm_attr<MT, WQ8, 1, 2>()));
-  WCHK((gemm_attr<MT, WQ8, 2, 2>()));
-  return gemm_attr<MT, WQ8, 1, 1>();
+  return gemm_attr<MT, WQ8, 4, 4>();
 }
 
 hipError_t wide_prepare(int Rp, int wq8) {
@@ -822,33 +778,37 @@ static hipError_t enqueue_step(const WideParams& p, hipStream_t st) {
   const size_t self_lds = (size_t)(p.max_ctx + 1) * sizeof(float);
   for (int l = 0; l < p.L; ++l) {
     const LayerDev& lw = p.layers[l];
-    WCHK(ln(p, l == 0, lw.ln1_g, lw.ln1_b, st));
-    WCHK(gemm(p, p.g_qkv, lw.w_qkv, lw.s_qkv, p.act, EP_STORE, lw.b_qkv, p.qkv, 3 * d, st));
-    hipLaunchKernelGGL(k_w_self, dim3(p.S, H), dim3(256), self_lds, st, p.ctl, p.qkv, d, H, l, p.S, p.max_ctx, p.kv_k, p.kv_v, p.slots,
-                       p.act, lda);
+    if (l == 0) WCHK(resid(p, nullptr, nullptr, lw.ln1_g, lw.ln1_b, st));
+    else WCHK(resid(p, &p.g_2, p.layers[l - 1].b_2, lw.ln1_g, lw.ln1_b, st));
+    WCHK(gemm(p, p.g_qkv, lw.w_qkv, lw.s_qkv, p.act, st));
+    hipLaunchKernelGGL(k_w_self, dim3(p.S, H), dim3(256), self_lds, st, p.ctl, p.part, p.g_qkv.ks, sstride(p, p.g_qkv), lw.b_qkv, d, H,
+                       l, p.S, p.max_ctx, p.kv_k, p.kv_v, p.slots, p.act, lda);
     WCHK(hipGetLastError());
-    WCHK(gemm(p, p.g_o, lw.w_o, lw.s_o, p.act, EP_RESID, lw.b_o, p.x, d, st));
-    WCHK(ln(p, false, lw.ln2_g, lw.ln2_b, st));
-    WCHK(gemm(p, p.g_cq, lw.w_cq, lw.s_cq, p.act, EP_STORE, lw.b_cq, p.qkv, d, st));
+    WCHK(gemm(p, p.g_o, lw.w_o, lw.s_o, p.act, st));
+    WCHK(resid(p, &p.g_o, lw.b_o, lw.ln2_g, lw.ln2_b, st));
+    WCHK(gemm(p, p.g_cq, lw.w_cq, lw.s_cq, p.act, st));
     if (rg_rows == 1)
-      hipLaunchKernelGGL(k_w_cross<1>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.qkv, d, H, p.A, l, p.L, p.S, p.X,
-                         p.chlen, p.nch, p.xk, p.xv, p.cpart);
+      hipLaunchKernelGGL(k_w_cross<1>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.part, p.g_cq.ks, sstride(p, p.g_cq),
+                         lw.b_cq, d, H, p.A, l, p.L, p.S, p.X, p.chlen, p.nch, p.xk, p.xv, p.cpart);
     else
-      hipLaunchKernelGGL(k_w_cross<8>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.qkv, d, H, p.A, l, p.L, p.S, p.X,
-                         p.chlen, p.nch, p.xk, p.xv, p.cpart);
+      hipLaunchKernelGGL(k_w_cross<8>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.part, p.g_cq.ks, sstride(p, p.g_cq),
+                         lw.b_cq, d, H, p.A, l, p.L, p.S, p.X, p.chlen, p.nch, p.xk, p.xv, p.cpart);
     WCHK(hipGetLastError());
     hipLaunchKernelGGL(k_w_cmerge, dim3(p.S, H), dim3(64), 0, st, p.cpart, H, p.nch, p.act, lda);
     WCHK(hipGetLastError());
-    WCHK(gemm(p, p.g_co, lw.w_co, lw.s_co, p.act, EP_RESID, lw.b_co, p.x, d, st));
-    WCHK(ln(p, false, lw.ln3_g, lw.ln3_b, st));
-    WCHK(gemm(p, p.g_1, lw.w_1, lw.s_1, p.act, EP_GELU, lw.b_1, p.hid, lda, st));
-    WCHK(gemm(p, p.g_2, lw.w_2, lw.s_2, p.hid, EP_RESID, lw.b_2, p.x, d, st));
+    WCHK(gemm(p, p.g_co, lw.w_co, lw.s_co, p.act, st));
+    WCHK(resid(p, &p.g_co, lw.b_co, lw.ln3_g, lw.ln3_b, st));
+    WCHK(gemm(p, p.g_1, lw.w_1, lw.s_1, p.act, st));
+    hipLaunchKernelGGL(k_w_gelu, dim3((p.S * 4 * d + 255) / 256), dim3(256), 0, st, p.part, p.g_1.ks, sstride(p, p.g_1), lw.b_1, p.S,
+                       4 * d, p.hid, lda);
+    WCHK(hipGetLastError());
+    WCHK(gemm(p, p.g_2, lw.w_2, lw.s_2, p.hid, st));
   }
-  WCHK(ln(p, false, p.lnf_g, p.lnf_b, st));
-  WCHK(gemm(p, p.g_v, p.emb, p.emb_s, p.act, EP_STORE, nullptr, p.lgt, p.V, st));
+  WCHK(resid(p, &p.g_2, p.layers[p.L - 1].b_2, p.lnf_g, p.lnf_b, st));
+  WCHK(gemm(p, p.g_v, p.emb, p.emb_s, p.act, st));
   const int nblk = (p.nsel + 3) / 4;
-  hipLaunchKernelGGL(k_w_select, dim3(p.S, nblk), dim3(256), 0, st, p.ctl, p.lgt, p.S, p.V, p.mask, p.mask2, p.mw, p.selp, p.nsel,
-                     p.logits_out);
+  hipLaunchKernelGGL(k_w_select, dim3(p.S, nblk), dim3(256), 0, st, p.ctl, p.part, p.g_v.ks, sstride(p, p.g_v), p.S, p.V, p.mask,
+                     p.mask2, p.mw, p.selp, p.nsel, p.logits_out);
   WCHK(hipGetLastError());
   hipLaunchKernelGGL(k_w_selmerge, dim3(p.S), dim3(64), 0, st, p.ctl, p.selp, p.S, p.nsel, p.out, p.next_tok);
   return hipGetLastError();
