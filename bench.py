@@ -204,12 +204,15 @@ def other_configs(w4h, synth):
     out["tiny.en greedy b=1, 224 forced steps"] = {"tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
                                                    "roofline_frac": round(frac, 4)}
     sps, hps, us, steps = measure_beam(w4h, synth, "small", 224, 5)
-    out["small beam 5, 224 steps (library beam driver, EOT suppressed)"] = {
+    out["small beam 5, 224 steps (library beam driver: device step + host candidate sort + KV reorder; EOT suppressed)"] = {
         "steps_per_s": round(sps, 1), "hypothesis_tokens_per_s": round(hps, 1), "us_per_step": round(us, 2),
         "steps": steps}
-    tps, us, frac = measure_forced(w4h, synth, "large-v3-turbo", "f16", 224, 2, n_rows=4, n_encoders=4,
-                                   n_sessions=8)
-    out["large-v3-turbo 32 streams, 224 forced steps (8 sessions x 4 streams, run one after another)"] = {
+    tps, us, frac = measure_forced(w4h, synth, "small", "f16", 224, 2, n_rows=5, n_encoders=1)
+    out["small 5 beam rows on one encoder, 224 forced steps in one run (device step only)"] = {
+        "steps_per_s": round(1e6 / us, 1), "hypothesis_tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
+        "roofline_frac": round(frac, 4)}
+    tps, us, frac = measure_forced(w4h, synth, "large-v3-turbo", "f16", 224, 2, n_rows=32, n_encoders=32)
+    out["large-v3-turbo 32 streams (own encoder each) in lockstep, 224 forced steps (batched MFMA engine)"] = {
         "tokens_per_s": round(tps, 1), "us_per_step": round(us, 2), "roofline_frac": round(frac, 4)}
     tps, us, frac = measure_forced(w4h, synth, "medium", "q8_0", 444, 2)
     out["medium q8_0 greedy b=1, 444 forced steps"] = {"tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
@@ -226,6 +229,8 @@ def main():
     ap.add_argument("--cpu-max-sweeps", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the tiny/small/turbo/medium lines")
+    ap.add_argument("--only", choices=["turbo", "small-beam-rows"],
+                    help="run only this other workload (one JSON line; for profiling the batched engine)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run a plain copy of this many MiB (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -241,6 +246,17 @@ def main():
 
     import whisper4j_amd as w4h
     from whisper4j_amd import synth
+
+    if args.only:
+        if args.only == "turbo":
+            tps, us, frac = measure_forced(w4h, synth, "large-v3-turbo", "f16", 224, 2, n_rows=32, n_encoders=32)
+            work = "large-v3-turbo 32 streams (own encoder each) in lockstep, 224 forced steps"
+        else:
+            tps, us, frac = measure_forced(w4h, synth, "small", "f16", 224, 2, n_rows=5, n_encoders=1)
+            work = "small 5 beam rows on one encoder, 224 forced steps"
+        print(json.dumps({"workload": work, "tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
+                          "roofline_frac": round(frac, 4)}))
+        return
 
     dims = synth.SHAPES["base.en"]
     T = synth.make_decoder(dims, seed=0, wtype="f16")

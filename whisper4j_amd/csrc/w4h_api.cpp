@@ -118,6 +118,32 @@ struct DevBuf {
   }
 };
 
+// Page-locked host staging buffer (hipHostMalloc): per-step copies between the caller's arrays
+// and the device go through these, so they are true asynchronous DMA copies.
+struct PinnedBuf {
+  void* p = nullptr;
+  size_t n = 0;
+  PinnedBuf() = default;
+  PinnedBuf(const PinnedBuf&) = delete;
+  PinnedBuf& operator=(const PinnedBuf&) = delete;
+  ~PinnedBuf() {
+    if (p) (void)hipHostFree(p);
+  }
+  int ensure(size_t bytes) {
+    if (n >= bytes) return W4H_OK;
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    n = 0;
+    hipError_t e = hipHostMalloc(&p, bytes, hipHostMallocDefault);
+    if (e != hipSuccess) {
+      p = nullptr;
+      return fail(W4H_ERR_OOM, "hipHostMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    }
+    n = bytes;
+    return W4H_OK;
+  }
+};
+
 int upload(DevBuf& b, const void* src, size_t bytes) {
   int rc = b.alloc(bytes);
   if (rc) return rc;
@@ -402,7 +428,16 @@ struct w4h_session {
   int nres = 0;
   size_t lds = 0;
   hipStream_t stream = nullptr;
-  DevBuf kvk, kvv, xk, xv, slots, ll, err, out, toks, forced, mask, mask2, logits, xa_tmp, trace;
+  DevBuf kvk, kvv, xk, xv, ll, out, forced, mask, logits, xa_tmp, trace;
+  // Per-step inputs in one device area (error word, tokens, extra mask, slot table) filled by one
+  // copy from its page-locked staging twin; forced rows and results are staged separately.
+  DevBuf in;
+  PinnedBuf h_in, h_forced, h_out;
+  size_t o_toks = 0, o_mask2 = 0, o_slots = 0, in_bytes = 0;
+  template <class T>
+  T* in_at(size_t off) const {
+    return reinterpret_cast<T*>(static_cast<char*>(in.p) + off);
+  }
   u64 *qkv = nullptr, *sp = nullptr, *x1 = nullptr, *cq = nullptr, *cp = nullptr, *x2 = nullptr, *hm = nullptr,
       *x3 = nullptr, *lp = nullptr, *lpa = nullptr;
   int kv_len = 0;
@@ -446,7 +481,7 @@ static StepParams base_params(w4h_session* s) {
   p.kv_v = s->kvv.as<uint16_t>();
   p.xk = s->xk.as<uint16_t>();
   p.xv = s->xv.as<uint16_t>();
-  p.slots = s->slots_identity ? nullptr : s->slots.as<int32_t>();
+  p.slots = s->slots_identity ? nullptr : s->in_at<int32_t>(s->o_slots);
   p.qkv = s->qkv;
   p.sp = s->sp;
   p.x1 = s->x1;
@@ -463,7 +498,7 @@ static StepParams base_params(w4h_session* s) {
   p.mask = s->has_mask ? s->mask.as<uint32_t>() : nullptr;
   p.mw = s->mw;
   p.probe = s->probe;
-  p.err = s->err.as<unsigned>();
+  p.err = s->in_at<unsigned>(0);
   p.rows_per_wg = s->rpw;
   p.ngroups = s->ngroups;
   p.rep_stride = s->rep_stride;
@@ -496,7 +531,7 @@ static WideParams wide_params(w4h_session* s) {
   p.kv_v = s->kvv.as<uint16_t>();
   p.xk = s->xk.as<uint16_t>();
   p.xv = s->xv.as<uint16_t>();
-  p.slots = s->slots_identity ? nullptr : s->slots.as<int32_t>();
+  p.slots = s->slots_identity ? nullptr : s->in_at<int32_t>(s->o_slots);
   p.x = s->wx.as<float>();
   p.act = s->wact.as<float>();
   p.hid = s->whid.as<float>();
@@ -527,6 +562,25 @@ static int ensure(DevBuf& b, size_t bytes) {
   return b.alloc(bytes);
 }
 
+// Copy the step results (and the error word) back through the page-locked staging buffer, wait for
+// the stream, and hand them to the caller's arrays.
+static int copy_back(w4h_session* s, int n_steps, w4h_step_out* out, float* logits, unsigned* herr) {
+  const int V = s->m->dims.n_vocab;
+  const size_t b_err = 256, b_out = out ? sizeof(w4h_step_out) * (size_t)n_steps * s->S : 0;
+  const size_t b_lg = logits ? sizeof(float) * (size_t)n_steps * s->S * V : 0;
+  int rc;
+  if ((rc = s->h_out.ensure(b_err + b_out + b_lg))) return rc;
+  char* hp = static_cast<char*>(s->h_out.p);
+  if (herr) HIPCHK(hipMemcpyAsync(hp, s->in.p, sizeof(unsigned), hipMemcpyDeviceToHost, s->stream));
+  if (b_out) HIPCHK(hipMemcpyAsync(hp + b_err, s->out.p, b_out, hipMemcpyDeviceToHost, s->stream));
+  if (b_lg) HIPCHK(hipMemcpyAsync(hp + b_err + b_out, s->logits.p, b_lg, hipMemcpyDeviceToHost, s->stream));
+  HIPCHK(hipStreamSynchronize(s->stream));
+  if (herr) memcpy(herr, hp, sizeof(unsigned));
+  if (b_out) memcpy(out, hp + b_err, b_out);
+  if (b_lg) memcpy(logits, hp + b_err + b_out, b_lg);
+  return W4H_OK;
+}
+
 // Launch n_steps steps; tokens/forced are host arrays.  Results (if out) are copied back.
 int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int n_steps, const uint32_t* extra_mask,
               int topk, w4h_step_out* out, float* logits, float* ms, uint64_t* trace = nullptr) {
@@ -544,34 +598,33 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
   if ((uint64_t)s->next_tag + (uint64_t)n_steps >= 0xfffffff0ull) return fail(W4H_ERR_INVALID, "tag space exhausted; recreate the session");
   HIPCHK(hipSetDevice(s->m->device));
   int rc;
-  if ((rc = ensure(s->toks, sizeof(int32_t) * s->S))) return rc;
-  HIPCHK(hipMemcpyAsync(s->toks.p, tokens, sizeof(int32_t) * s->S, hipMemcpyHostToDevice, s->stream));
+  // per-step inputs: one asynchronous copy of the leading part of the input area that changed
+  char* hp = static_cast<char*>(s->h_in.p);
+  *reinterpret_cast<unsigned*>(hp) = 0u;  // error word
+  memcpy(hp + s->o_toks, tokens, sizeof(int32_t) * s->S);
+  if (extra_mask) memcpy(hp + s->o_mask2, extra_mask, sizeof(uint32_t) * (size_t)s->S * s->mw);
+  if (s->slots_dirty) memcpy(hp + s->o_slots, s->slots_host.data(), sizeof(int32_t) * s->slots_host.size());
+  const size_t in_len = s->slots_dirty ? s->in_bytes : (extra_mask ? s->o_slots : s->o_mask2);
+  HIPCHK(hipMemcpyAsync(s->in.p, hp, in_len, hipMemcpyHostToDevice, s->stream));
+  s->slots_dirty = false;
   if (forced && n_steps > 1) {
-    if ((rc = ensure(s->forced, sizeof(int32_t) * (size_t)(n_steps - 1) * s->S))) return rc;
-    HIPCHK(hipMemcpyAsync(s->forced.p, forced, sizeof(int32_t) * (size_t)(n_steps - 1) * s->S, hipMemcpyHostToDevice, s->stream));
-  }
-  if (extra_mask) {
-    if ((rc = ensure(s->mask2, sizeof(uint32_t) * (size_t)s->S * s->mw))) return rc;
-    HIPCHK(hipMemcpyAsync(s->mask2.p, extra_mask, sizeof(uint32_t) * (size_t)s->S * s->mw, hipMemcpyHostToDevice, s->stream));
-  }
-  if (s->slots_dirty) {
-    HIPCHK(hipMemcpyAsync(s->slots.p, s->slots_host.data(), sizeof(int32_t) * s->slots_host.size(), hipMemcpyHostToDevice,
-                          s->stream));
-    s->slots_dirty = false;
+    const size_t b_forced = sizeof(int32_t) * (size_t)(n_steps - 1) * s->S;
+    if ((rc = ensure(s->forced, b_forced)) || (rc = s->h_forced.ensure(b_forced))) return rc;
+    memcpy(s->h_forced.p, forced, b_forced);
+    HIPCHK(hipMemcpyAsync(s->forced.p, s->h_forced.p, b_forced, hipMemcpyHostToDevice, s->stream));
   }
   if (out && (rc = ensure(s->out, sizeof(w4h_step_out) * (size_t)n_steps * s->S))) return rc;
   if (logits && (rc = ensure(s->logits, sizeof(float) * (size_t)n_steps * s->S * V))) return rc;
   const size_t trace_n = (size_t)n_steps * (6 * s->m->dims.n_text_layer + 2) * 4 * s->grid;
   if (trace && (rc = ensure(s->trace, trace_n * sizeof(uint64_t)))) return rc;
-  HIPCHK(hipMemsetAsync(s->err.p, 0, sizeof(unsigned), s->stream));
   if (s->wide) {
     if (trace) return fail(W4H_ERR_INVALID, "phase traces are recorded by the persistent step kernel only");
     WideParams wp = wide_params(s);
     wp.nsteps = n_steps;
     wp.kv_len0 = s->kv_len;
-    wp.tokens0 = s->toks.as<int32_t>();
+    wp.tokens0 = s->in_at<int32_t>(s->o_toks);
     wp.forced = (forced && n_steps > 1) ? s->forced.as<int32_t>() : nullptr;
-    wp.mask2 = extra_mask ? s->mask2.as<uint32_t>() : nullptr;
+    wp.mask2 = extra_mask ? s->in_at<uint32_t>(s->o_mask2) : nullptr;
     wp.topk = topk;
     wp.out = out ? s->out.as<w4h_step_out>() : nullptr;
     wp.logits_out = logits ? s->logits.as<float>() : nullptr;
@@ -584,10 +637,7 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
     hipError_t le = launch_wide(wp, s->stream);
     if (le != hipSuccess) return fail(W4H_ERR_DEVICE, "batched step launch failed: %s", hipGetErrorString(le));
     if (ms) HIPCHK(hipEventRecord(e1, s->stream));
-    if (out) HIPCHK(hipMemcpyAsync(out, s->out.p, sizeof(w4h_step_out) * (size_t)n_steps * s->S, hipMemcpyDeviceToHost, s->stream));
-    if (logits)
-      HIPCHK(hipMemcpyAsync(logits, s->logits.p, sizeof(float) * (size_t)n_steps * s->S * V, hipMemcpyDeviceToHost, s->stream));
-    HIPCHK(hipStreamSynchronize(s->stream));
+    if ((rc = copy_back(s, n_steps, out, logits, nullptr))) return rc;
     if (ms) {
       HIPCHK(hipEventElapsedTime(ms, e0, e1));
       (void)hipEventDestroy(e0);
@@ -600,9 +650,9 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
   p.nsteps = n_steps;
   p.kv_len0 = s->kv_len;
   p.tag0 = s->next_tag;
-  p.tokens0 = s->toks.as<int32_t>();
+  p.tokens0 = s->in_at<int32_t>(s->o_toks);
   p.forced = (forced && n_steps > 1) ? s->forced.as<int32_t>() : nullptr;
-  p.mask2 = extra_mask ? s->mask2.as<uint32_t>() : nullptr;
+  p.mask2 = extra_mask ? s->in_at<uint32_t>(s->o_mask2) : nullptr;
   p.topk = topk;
   p.out = out ? s->out.as<w4h_step_out>() : nullptr;
   p.logits_out = logits ? s->logits.as<float>() : nullptr;
@@ -618,12 +668,8 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
   s->next_tag += (uint32_t)n_steps;
   if (ms) HIPCHK(hipEventRecord(e1, s->stream));
   unsigned herr = 0;
-  HIPCHK(hipMemcpyAsync(&herr, s->err.p, sizeof(unsigned), hipMemcpyDeviceToHost, s->stream));
-  if (out) HIPCHK(hipMemcpyAsync(out, s->out.p, sizeof(w4h_step_out) * (size_t)n_steps * s->S, hipMemcpyDeviceToHost, s->stream));
-  if (logits)
-    HIPCHK(hipMemcpyAsync(logits, s->logits.p, sizeof(float) * (size_t)n_steps * s->S * V, hipMemcpyDeviceToHost, s->stream));
   if (trace) HIPCHK(hipMemcpyAsync(trace, s->trace.p, trace_n * sizeof(uint64_t), hipMemcpyDeviceToHost, s->stream));
-  HIPCHK(hipStreamSynchronize(s->stream));
+  if ((rc = copy_back(s, n_steps, out, logits, &herr))) return rc;
   if (ms) {
     HIPCHK(hipEventElapsedTime(ms, e0, e1));
     (void)hipEventDestroy(e0);
@@ -631,6 +677,22 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
   }
   if (herr) return fail(W4H_ERR_TIMEOUT, "a device-side wait expired during the step (code %u); step aborted", herr);
   s->kv_len += n_steps;
+  return W4H_OK;
+}
+
+// The per-step input area: [error word | tokens | extra mask | slot table], each 256-byte aligned,
+// with its page-locked staging twin; zero error word and tokens, identity slot table.
+static int init_inputs(w4h_session* s) {
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  s->o_toks = 256;
+  s->o_mask2 = s->o_toks + al(sizeof(int32_t) * s->S);
+  s->o_slots = s->o_mask2 + al(sizeof(uint32_t) * (size_t)s->S * s->mw);
+  s->in_bytes = s->o_slots + al(sizeof(int32_t) * s->slots_host.size());
+  int rc;
+  if ((rc = s->in.alloc(s->in_bytes)) || (rc = s->h_in.ensure(s->in_bytes))) return rc;
+  memset(s->h_in.p, 0, s->in_bytes);
+  memcpy(static_cast<char*>(s->h_in.p) + s->o_slots, s->slots_host.data(), sizeof(int32_t) * s->slots_host.size());
+  HIPCHK(hipMemcpy(s->in.p, s->h_in.p, s->in_bytes, hipMemcpyHostToDevice));
   return W4H_OK;
 }
 
@@ -657,7 +719,9 @@ int create_wide(std::unique_ptr<w4h_session>& s, const hipDeviceProp_t& prop, w4
   // cross-attention chunks: enough (encoder, head, chunk) workgroups for two per compute unit,
   // chunks of at least 64 keys
   const int ngroups = s->X == s->S ? 1 : (s->S + 7) / 8;
-  int nch = (2 * ncu + s->X * H * ngroups - 1) / (s->X * H * ngroups);
+  int per_cu = 2;  // W4H_XWG overrides the cross-attention workgroups per compute unit (tuning)
+  if (const char* e = getenv("W4H_XWG")) per_cu = std::max(1, std::min(16, atoi(e)));
+  int nch = (per_cu * ncu + s->X * H * ngroups - 1) / (s->X * H * ngroups);
   nch = std::max(1, std::min(nch, A / 64));
   s->chlen = (A + nch - 1) / nch;
   s->nch = (A + s->chlen - 1) / s->chlen;
@@ -672,7 +736,7 @@ int create_wide(std::unique_ptr<w4h_session>& s, const hipDeviceProp_t& prop, w4
   s->slots_host.resize((size_t)s->S * s->max_ctx);
   for (int r = 0; r < s->S; r++)
     for (int q = 0; q < s->max_ctx; q++) s->slots_host[(size_t)r * s->max_ctx + q] = r;
-  if ((rc = upload(s->slots, s->slots_host.data(), s->slots_host.size() * 4))) return rc;
+  if ((rc = init_inputs(s.get()))) return rc;
   if ((rc = s->wx.alloc(sizeof(float) * (size_t)s->S * d))) return rc;
   if ((rc = s->wact.alloc(sizeof(float) * (size_t)s->Rp * 4 * d))) return rc;
   HIPCHK(hipMemset(s->wact.p, 0, sizeof(float) * (size_t)s->Rp * 4 * d));
@@ -688,8 +752,6 @@ int create_wide(std::unique_ptr<w4h_session>& s, const hipDeviceProp_t& prop, w4
   // One step is captured as a HIP graph and replayed per step; W4H_GRAPH=0 launches every kernel.
   if (const char* e = getenv("W4H_GRAPH")) s->use_graph = atoi(e) != 0;
   HIPCHK(hipStreamCreate(&s->stream));
-  if ((rc = s->err.alloc(256))) return rc;
-  HIPCHK(hipMemset(s->err.p, 0, 256));
   if ((rc = s->mask.alloc(sizeof(uint32_t) * (size_t)s->S * s->mw))) return rc;
   HIPCHK(hipDeviceSynchronize());
   m->refs.fetch_add(1);
@@ -726,9 +788,11 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   hipDeviceProp_t prop;
   HIPCHK(hipGetDeviceProperties(&prop, m->device));
   s->grid = prop.multiProcessorCount;
-  // Engine: the persistent step kernel for up to kMaxRows rows, the batched MFMA engine beyond
-  // (W4H_ENGINE=wide or persistent overrides where both apply).
-  s->wide = s->S > kMaxRows;
+  // Engine: the persistent step kernel for few rows, the batched MFMA engine for more (measured on
+  // MI355X: the batched engine is faster from 5 rows at d = 512 and from 3 rows at d = 768; the
+  // persistent kernel holds at most kMaxRows).  W4H_ENGINE=wide or persistent overrides where both
+  // apply.
+  s->wide = s->S > kMaxRows || s->S >= 5 || (s->S >= 3 && d >= 768);
   if (const char* e = getenv("W4H_ENGINE")) {
     if (!strcmp(e, "wide")) s->wide = true;
     else if (!strcmp(e, "persistent") && s->S <= kMaxRows) s->wide = false;
@@ -780,7 +844,7 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   s->slots_host.resize((size_t)s->S * s->max_ctx);
   for (int r = 0; r < s->S; r++)
     for (int q = 0; q < s->max_ctx; q++) s->slots_host[(size_t)r * s->max_ctx + q] = r;
-  if ((rc = upload(s->slots, s->slots_host.data(), s->slots_host.size() * 4))) return rc;
+  if ((rc = init_inputs(s.get()))) return rc;
   // tagged exchange buffers, one allocation
   const size_t n_qkv = (size_t)L * s->S * 3 * d, n_sp = (size_t)L * s->ncs_max * s->S * H * kPartWords,
                n_vec = (size_t)L * s->S * d, n_cp = (size_t)L * s->ncc * s->S * H * kPartWords, n_hm = (size_t)L * s->S * 4 * d,
@@ -801,7 +865,6 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   s->lpa = b;
   HIPCHK(hipStreamCreate(&s->stream));
   HIPCHK(launch_fill_u64(s->ll.as<u64>(), total * kRep, s->stream));
-  if ((rc = s->err.alloc(256))) return rc;
   if ((rc = s->mask.alloc(sizeof(uint32_t) * (size_t)s->S * s->mw))) return rc;
   HIPCHK(hipStreamSynchronize(s->stream));
   m->refs.fetch_add(1);

@@ -250,23 +250,23 @@ __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl
       }
     }
   } else {
-    // slices added in slice order, kSliceBatch slices of every element in flight
+    // slices added in slice order; every slice (kWideMaxSlices) of every element in flight at once
     float acc[kWideVec];
 #pragma unroll
     for (int i = 0; i < kWideVec; ++i) acc[i] = 0.f;
-    for (int z = 0; z < ks; z += kSliceBatch) {
-      float t[kWideVec][kSliceBatch];
+    for (int z = 0; z < ks; z += kWideMaxSlices) {
+      float t[kWideVec][kWideMaxSlices];
 #pragma unroll
       for (int i = 0; i < kWideVec; ++i)
 #pragma unroll
-        for (int u = 0; u < kSliceBatch; ++u) {
+        for (int u = 0; u < kWideMaxSlices; ++u) {
           const int j = tid + 256 * i;
           t[i][u] = (j < d && z + u < ks) ? P[(size_t)(z + u) * ss + (size_t)s * d + j] : 0.f;
         }
 #pragma unroll
       for (int i = 0; i < kWideVec; ++i)
 #pragma unroll
-        for (int u = 0; u < kSliceBatch; ++u) acc[i] += t[i][u];
+        for (int u = 0; u < kWideMaxSlices; ++u) acc[i] += t[i][u];
     }
 #pragma unroll
     for (int i = 0; i < kWideVec; ++i) {
@@ -313,9 +313,34 @@ __global__ __launch_bounds__(256) void k_w_gelu(const float* __restrict__ P, int
 // Self-attention of one (row, head): q, k, v = bias + the QKV GEMM slices; k, v appended to the
 // cache at position t (f16); softmax over the t cached keys (row s reads position j from slot
 // slots[s][j]) plus the current key (fp32); output -> act[s][h*64, +64).  8 lanes per key, 16 bytes
-// each; four keys per lane group in flight.
+// each.  The cached keys and values of the first kSelfBlock positions are loaded before q is
+// formed (they do not depend on it), so one memory round trip covers them; longer contexts loop.
 
-constexpr int kKeysInFlight = 4;
+constexpr int kKeysInFlight = 4;   // keys per lane group in flight (cross-attention loops)
+constexpr int kSelfKF = 16;        // keys per lane group loaded up front (self-attention)
+constexpr int kSelfBlock = 32 * kSelfKF;
+
+DEV float dot8h(const float* qd, uint4 u) {
+  const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+  float dot = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float2 fv = h2x2(uw[e]);
+    dot = fmaf(qd[2 * e], fv.x, dot);
+    dot = fmaf(qd[2 * e + 1], fv.y, dot);
+  }
+  return dot;
+}
+
+DEV void axpy8h(float p, uint4 u, float* o) {
+  const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float2 fv = h2x2(uw[e]);
+    o[2 * e] = fmaf(p, fv.x, o[2 * e]);
+    o[2 * e + 1] = fmaf(p, fv.y, o[2 * e + 1]);
+  }
+}
 
 __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl, const float* __restrict__ P, int ks, size_t ss,
                                                 const float* __restrict__ bqkv, int d, int H, int l, int S, int max_ctx,
@@ -325,8 +350,27 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
   __shared__ float q[64], kc[64], vc[64], red[4 * 64], stat[8];
   const int s = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int t = ctl->kv_len0 + ctl->i;  // position of the current token
-  const int32_t* slots = ctl->slots_on ? slot_table : nullptr;
+  const int32_t* srow = ctl->slots_on ? slot_table + (size_t)s * max_ctx : nullptr;
   const size_t head_base = ((size_t)l * S * H) * max_ctx * kHeadDim;  // layer l
+  const int kg = tid >> 3, dc = tid & 7;
+  auto kv_off = [&](int j) -> size_t {
+    const int slot = srow ? srow[j] : s;
+    return head_base + (((size_t)slot * H + h) * max_ctx + j) * kHeadDim + dc * 8;
+  };
+  // cached keys and values of the first block, before q exists
+  uint4 kr[kSelfKF], vr[kSelfKF];
+#pragma unroll
+  for (int f = 0; f < kSelfKF; ++f) {
+    const int j = 32 * f + kg;
+    if (j < t) {
+      const size_t o = kv_off(j);
+      kr[f] = *reinterpret_cast<const uint4*>(kvk + o);
+      vr[f] = *reinterpret_cast<const uint4*>(kvv + o);
+    } else {
+      kr[f] = make_uint4(0, 0, 0, 0);
+      vr[f] = kr[f];
+    }
+  }
   if (tid < 192) {
     const int part = tid >> 6, e = tid & 63;
     const int col = part * d + h * kHeadDim + e;
@@ -340,16 +384,16 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
     }
   }
   __syncthreads();
-  const int kg = tid >> 3, dc = tid & 7;
   float qd[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) qd[e] = q[dc * 8 + e];
-  const int32_t* srow = slots ? slots + (size_t)s * max_ctx : nullptr;
-  auto kv_off = [&](int j) -> size_t {
-    const int slot = srow ? srow[j] : s;
-    return head_base + (((size_t)slot * H + h) * max_ctx + j) * kHeadDim + dc * 8;
-  };
-  for (int j0 = 0; j0 < t; j0 += 32 * kKeysInFlight) {
+#pragma unroll
+  for (int f = 0; f < kSelfKF; ++f) {
+    const int j = 32 * f + kg;
+    const float dot = sum8(dot8h(qd, kr[f]));
+    if (dc == 0 && j < t) sc[j] = dot * 0.125f;
+  }
+  for (int j0 = kSelfBlock; j0 < t; j0 += 32 * kKeysInFlight) {  // positions past the first block
     uint4 u[kKeysInFlight];
 #pragma unroll
     for (int f = 0; f < kKeysInFlight; ++f) {
@@ -359,15 +403,7 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
 #pragma unroll
     for (int f = 0; f < kKeysInFlight; ++f) {
       const int j = j0 + 32 * f + kg;
-      const uint32_t uw[4] = {u[f].x, u[f].y, u[f].z, u[f].w};
-      float dot = 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float2 fv = h2x2(uw[e]);
-        dot = fmaf(qd[2 * e], fv.x, dot);
-        dot = fmaf(qd[2 * e + 1], fv.y, dot);
-      }
-      dot = sum8(dot);
+      const float dot = sum8(dot8h(qd, u[f]));
       if (dc == 0 && j < t) sc[j] = dot * 0.125f;
     }
   }
@@ -396,7 +432,12 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
   float o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = 0.f;
-  for (int j0 = 0; j0 < t; j0 += 32 * kKeysInFlight) {
+#pragma unroll
+  for (int f = 0; f < kSelfKF; ++f) {
+    const int j = 32 * f + kg;
+    axpy8h(j < t ? sc[j] : 0.f, vr[f], o);
+  }
+  for (int j0 = kSelfBlock; j0 < t; j0 += 32 * kKeysInFlight) {
     uint4 u[kKeysInFlight];
 #pragma unroll
     for (int f = 0; f < kKeysInFlight; ++f) {
@@ -406,14 +447,7 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
 #pragma unroll
     for (int f = 0; f < kKeysInFlight; ++f) {
       const int j = j0 + 32 * f + kg;
-      const float p = j < t ? sc[j] : 0.f;
-      const uint32_t uw[4] = {u[f].x, u[f].y, u[f].z, u[f].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float2 fv = h2x2(uw[e]);
-        o[2 * e] = fmaf(p, fv.x, o[2 * e]);
-        o[2 * e + 1] = fmaf(p, fv.y, o[2 * e + 1]);
-      }
+      axpy8h(j < t ? sc[j] : 0.f, u[f], o);
     }
   }
   if (kg == 0) {
@@ -461,22 +495,30 @@ __global__ __launch_bounds__(256) void k_w_cross(const float* __restrict__ P, in
     r0 = rg * RG;
     nr = min(RG, S - r0);
   }
+  const int j0 = c * chlen, j1 = min(A, j0 + chlen), n = j1 - j0;
+  const uint16_t* kb = xk + ((((size_t)e * L + l) * H + h) * A + j0) * kHeadDim;
+  const uint16_t* vb = xv + ((((size_t)e * L + l) * H + h) * A + j0) * kHeadDim;
+  const int kg = tid >> 3, dc = tid & 7;
+  // keys and values of the chunk's first 32 * kKeysInFlight positions, before the query exists
+  uint4 u0[kKeysInFlight], v0[kKeysInFlight];
+#pragma unroll
+  for (int f = 0; f < kKeysInFlight; ++f) {
+    const int j = 32 * f + kg;
+    u0[f] = j < n ? *reinterpret_cast<const uint4*>(kb + (size_t)j * kHeadDim + dc * 8) : make_uint4(0, 0, 0, 0);
+    v0[f] = j < n ? *reinterpret_cast<const uint4*>(vb + (size_t)j * kHeadDim + dc * 8) : make_uint4(0, 0, 0, 0);
+  }
   for (int i = tid; i < nr * 64; i += 256) {
     const int r = i >> 6, k = i & 63;
     const int col = h * kHeadDim + k;
     q[i] = (bcq[col] + slice_sum(P, ks, ss, (size_t)(r0 + r) * d + col)) * 0.125f;
   }
   __syncthreads();
-  const int j0 = c * chlen, j1 = min(A, j0 + chlen), n = j1 - j0;
-  const uint16_t* kb = xk + ((((size_t)e * L + l) * H + h) * A + j0) * kHeadDim;
-  const uint16_t* vb = xv + ((((size_t)e * L + l) * H + h) * A + j0) * kHeadDim;
-  const int kg = tid >> 3, dc = tid & 7;
   for (int jj = 0; jj < n; jj += 32 * kKeysInFlight) {
     uint4 u[kKeysInFlight];
 #pragma unroll
     for (int f = 0; f < kKeysInFlight; ++f) {
       const int j = jj + 32 * f + kg;
-      u[f] = j < n ? *reinterpret_cast<const uint4*>(kb + (size_t)j * kHeadDim + dc * 8) : make_uint4(0, 0, 0, 0);
+      u[f] = jj == 0 ? u0[f] : (j < n ? *reinterpret_cast<const uint4*>(kb + (size_t)j * kHeadDim + dc * 8) : make_uint4(0, 0, 0, 0));
     }
 #pragma unroll
     for (int f = 0; f < kKeysInFlight; ++f) {
@@ -529,7 +571,7 @@ __global__ __launch_bounds__(256) void k_w_cross(const float* __restrict__ P, in
 #pragma unroll
     for (int f = 0; f < kKeysInFlight; ++f) {
       const int j = jj + 32 * f + kg;
-      u[f] = j < n ? *reinterpret_cast<const uint4*>(vb + (size_t)j * kHeadDim + dc * 8) : make_uint4(0, 0, 0, 0);
+      u[f] = jj == 0 ? v0[f] : (j < n ? *reinterpret_cast<const uint4*>(vb + (size_t)j * kHeadDim + dc * 8) : make_uint4(0, 0, 0, 0));
     }
 #pragma unroll
     for (int f = 0; f < kKeysInFlight; ++f) {
@@ -582,17 +624,24 @@ __global__ __launch_bounds__(256) void k_w_cross(const float* __restrict__ P, in
   }
 }
 
-// Merge the chunk partials of (row, head) into act[row][h*64, +64).  64 threads.
+// Merge the chunk partials of (row, head) into act[row][h*64, +64).  64 threads; lane c holds chunk
+// c's (max, sum) (nch <= 64), then every lane adds its output element over the chunks in chunk order
+// with eight loads in flight.
 __global__ __launch_bounds__(64) void k_w_cmerge(const float* __restrict__ cpart, int H, int nch, float* __restrict__ act, int lda) {
   const int s = blockIdx.x, h = blockIdx.y, k = threadIdx.x;
   const float* p = cpart + ((size_t)s * H + h) * nch * kPartWords;
-  float M = -INFINITY;
-  for (int c = 0; c < nch; ++c) M = fmaxf(M, p[c * kPartWords]);
-  float Lsum = 0.f, o = 0.f;
-  for (int c = 0; c < nch; ++c) {
-    const float f = __expf(p[c * kPartWords] - M);
-    Lsum = fmaf(f, p[c * kPartWords + 1], Lsum);
-    o = fmaf(f, p[c * kPartWords + 2 + k], o);
+  const float mc = k < nch ? p[k * kPartWords] : -INFINITY;
+  const float lc = k < nch ? p[k * kPartWords + 1] : 0.f;
+  const float M = wave_max(mc);
+  const float f = k < nch ? __expf(mc - M) : 0.f;
+  const float Lsum = wave_sum(f * lc);
+  float o = 0.f;
+  for (int c0 = 0; c0 < nch; c0 += 8) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) t[u] = c0 + u < nch ? p[(c0 + u) * kPartWords + 2 + k] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) o = fmaf(__shfl(f, c0 + u), t[u], o);
   }
   act[(size_t)s * lda + h * kHeadDim + k] = o / Lsum;
 }
