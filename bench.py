@@ -231,6 +231,7 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the tiny/small/turbo/medium lines")
     ap.add_argument("--only", choices=["turbo", "small-beam-rows"],
                     help="run only this other workload (one JSON line; for profiling the batched engine)")
+    ap.add_argument("--only-steps", type=int, default=224, help="forced steps of the --only workload")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run a plain copy of this many MiB (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -248,12 +249,15 @@ def main():
     from whisper4j_amd import synth
 
     if args.only:
+        n = args.only_steps
         if args.only == "turbo":
-            tps, us, frac = measure_forced(w4h, synth, "large-v3-turbo", "f16", 224, 2, n_rows=32, n_encoders=32)
-            work = "large-v3-turbo 32 streams (own encoder each) in lockstep, 224 forced steps"
+            tps, us, frac = measure_forced(w4h, synth, "large-v3-turbo", "f16", n, 2, n_rows=32, n_encoders=32)
+            work = f"large-v3-turbo 32 streams (own encoder each) in lockstep, {n} forced steps"
         else:
-            tps, us, frac = measure_forced(w4h, synth, "small", "f16", 224, 2, n_rows=5, n_encoders=1)
-            work = "small 5 beam rows on one encoder, 224 forced steps"
+            tps, us, frac = measure_forced(w4h, synth, "small", "f16", n, 2, n_rows=5, n_encoders=1)
+            work = f"small 5 beam rows on one encoder, {n} forced steps"
+        if args.copy_mib:
+            copy_calibration(args.copy_mib)
         print(json.dumps({"workload": work, "tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
                           "roofline_frac": round(frac, 4)}))
         return
