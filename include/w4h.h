@@ -96,7 +96,9 @@ int w4h_ggml_read_tensor(const char* path, const char* name, int32_t* type, int3
 typedef struct w4h_session w4h_session;
 
 typedef struct {
-  int32_t n_rows;     /* S: rows decoded in lockstep (1 greedy, beam size, or independent streams) */
+  int32_t n_rows;     /* S: rows decoded in lockstep (1 greedy, beam size, or independent streams), 1..32;
+                         from 5 rows (3 when n_text_state >= 768) every projection is one MFMA GEMM over
+                         all rows, fewer rows run on the persistent single-launch step kernel */
   int32_t n_encoders; /* 1 (rows share one encoder output: greedy, beam) or n_rows (independent streams) */
   int32_t max_ctx;    /* self-KV capacity in positions (>= n_text_ctx is typical) */
 } w4h_session_desc;
