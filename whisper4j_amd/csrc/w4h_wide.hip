@@ -476,13 +476,15 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
 // Cross-attention chunk partials.  Workgroup (e, h, z): encoder e, head h, key chunk z % nch, row
 // group z / nch (up to RG rows that read encoder e: the one row e when every row has its own
 // encoder, else rows of the shared encoder).  Keys are scored for every row of the group, so a
-// shared encoder's K/V chunk is read once per group.  Partial (m, l, acc[64]) per row.
+// shared encoder's K/V chunk is read once per group.  Partial (m, l, acc[64]) per row, or, with a
+// single chunk, the normalised output written to act directly.
 
 template <int RG>
 __global__ __launch_bounds__(256) void k_w_cross(const float* __restrict__ P, int ks, size_t ss, const float* __restrict__ bcq, int d,
                                                  int H, int A, int l, int L, int S, int X, int chlen, int nch,
                                                  const uint16_t* __restrict__ xk,
-                                                 const uint16_t* __restrict__ xv, float* __restrict__ cpart) {
+                                                 const uint16_t* __restrict__ xv, float* __restrict__ cpart,
+                                                 float* __restrict__ act, int lda) {
   extern __shared__ float scs[];  // [RG][chlen]
   __shared__ float q[RG * 64], red[4 * RG * 64], rm[RG], rl[RG];
   const int e = blockIdx.x, h = blockIdx.y, c = blockIdx.z % nch, rg = blockIdx.z / nch;
@@ -615,6 +617,10 @@ __global__ __launch_bounds__(256) void k_w_cross(const float* __restrict__ P, in
     const int r = i >> 6, k = i & 63;
     const float v = red[(0 * RG + r) * 64 + k] + red[(1 * RG + r) * 64 + k] + red[(2 * RG + r) * 64 + k] +
                     red[(3 * RG + r) * 64 + k];
+    if (nch == 1) {  // one chunk: the normalised output goes straight to the out-projection's input
+      act[(size_t)(r0 + r) * lda + h * kHeadDim + k] = v / rl[r];
+      continue;
+    }
     float* dst = cpart + (((size_t)(r0 + r) * H + h) * nch + c) * kPartWords;
     dst[2 + k] = v;
     if (k == 0) {
@@ -838,13 +844,15 @@ static hipError_t enqueue_step(const WideParams& p, hipStream_t st) {
     WCHK(gemm(p, p.g_cq, lw.w_cq, lw.s_cq, p.act, st));
     if (rg_rows == 1)
       hipLaunchKernelGGL(k_w_cross<1>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.part, p.g_cq.ks, sstride(p, p.g_cq),
-                         lw.b_cq, d, H, p.A, l, p.L, p.S, p.X, p.chlen, p.nch, p.xk, p.xv, p.cpart);
+                         lw.b_cq, d, H, p.A, l, p.L, p.S, p.X, p.chlen, p.nch, p.xk, p.xv, p.cpart, p.act, lda);
     else
       hipLaunchKernelGGL(k_w_cross<8>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.part, p.g_cq.ks, sstride(p, p.g_cq),
-                         lw.b_cq, d, H, p.A, l, p.L, p.S, p.X, p.chlen, p.nch, p.xk, p.xv, p.cpart);
+                         lw.b_cq, d, H, p.A, l, p.L, p.S, p.X, p.chlen, p.nch, p.xk, p.xv, p.cpart, p.act, lda);
     WCHK(hipGetLastError());
-    hipLaunchKernelGGL(k_w_cmerge, dim3(p.S, H), dim3(64), 0, st, p.cpart, H, p.nch, p.act, lda);
-    WCHK(hipGetLastError());
+    if (p.nch > 1) {
+      hipLaunchKernelGGL(k_w_cmerge, dim3(p.S, H), dim3(64), 0, st, p.cpart, H, p.nch, p.act, lda);
+      WCHK(hipGetLastError());
+    }
     WCHK(gemm(p, p.g_co, lw.w_co, lw.s_co, p.act, st));
     WCHK(resid(p, &p.g_co, lw.b_co, lw.ln3_g, lw.ln3_b, st));
     WCHK(gemm(p, p.g_1, lw.w_1, lw.s_1, p.act, st));
