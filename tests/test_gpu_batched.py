@@ -178,3 +178,27 @@ def test_batched_graph_replay_matches_eager(gpu, monkeypatch):
             np.testing.assert_array_equal(a, b)
         else:
             assert a == b
+
+
+@pytest.mark.parametrize("beam,max_tokens,ts_begin,eot", [(5, 45, -1, 999), (5, 20, 901, 900), (3, 40, -1, 999),
+                                                          (2, 70, 901, 900)])
+def test_device_beam_search_matches_oracle(gpu, orc, monkeypatch, beam, max_tokens, ts_begin, eot):
+    """Beam search run on the device (batched session: candidate sort, finished list, n-gram and
+    timestamp masks and the slot-table reorder in k_w_beam), over more than one 32-step launch,
+    against the oracle's beam search: same tokens, avg log-prob within 1e-3."""
+    monkeypatch.setenv("W4H_ENGINE", "wide")
+    dims = synth.Dims(n_vocab=1000, n_text_ctx=96, n_text_state=384, n_text_head=6, n_text_layer=2, n_audio_ctx=50)
+    T = synth.make_decoder(dims, seed=46 + beam, ln_random=True)
+    xa = synth.encoder_output(dims, 46 + beam)
+    om = orc.Model(dims, T)
+    m = gpu.Model.from_tensors(dims, T)
+    sup = [1, 2, 3, 220]
+    dec = gpu.WhisperDecoder(m, beam_size=beam, max_ctx=dims.n_text_ctx)
+    for _ in range(2):  # a second search on the same session starts from a clean state
+        b = dec.decode_beam(xa, [10, 11, 12], eot, max_tokens, sup, timestamp_begin=ts_begin, beam_size=beam)
+        ob = om.decode_beam(xa, [10, 11, 12], eot=eot, max_tokens=max_tokens, suppress=sup, ts_begin=ts_begin, beam=beam)
+        say(f"beam {beam} max {max_tokens} ts {ts_begin}: {len(b.tokens)} tokens")
+        assert b.tokens == ob["tokens"]
+        assert b.avg_logprob == pytest.approx(ob["avg_logprob"], abs=1e-3)
+    dec.close()
+    m.close()

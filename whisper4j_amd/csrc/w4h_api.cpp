@@ -452,7 +452,8 @@ struct w4h_session {
   int Rp = 0, nch = 0, chlen = 0, nsel = 0;
   WideGemm g_qkv{}, g_o{}, g_cq{}, g_co{}, g_1{}, g_2{}, g_v{};
   DevBuf wx, wact, whid, wpart, wcpart, wselp, wnext, wctl;
-  WideGraph wgraph;
+  WideGraph wgraph, wgraph_beam;
+  DevBuf wbeam, wbsup;
   bool use_graph = true;
 };
 
@@ -879,6 +880,7 @@ int w4h_session_destroy(w4h_session* s) {
   if (s->stream) {
     (void)hipStreamSynchronize(s->stream);
     wide_graph_release(&s->wgraph);
+    wide_graph_release(&s->wgraph_beam);
     (void)hipStreamDestroy(s->stream);
   }
   delete s;
@@ -1095,5 +1097,90 @@ int w4h_op_select(const float* logits, int32_t rows, int32_t n, const uint32_t* 
 
 namespace w4h {
 int session_rows(const w4h_session* s) { return s->S; }
+bool session_device_beam(const w4h_session* s) { return s->wide && s->S <= kBeamMax; }
+
+int device_beam_search(w4h_session* s, const BeamSearchIn& in, BeamSearchOut* out) {
+  if (!s->wide || in.beam != s->S || in.beam > kBeamMax) return fail(W4H_ERR_INVALID, "device beam search needs a batched session");
+  if (in.max_steps < 0 || in.max_steps >= kBeamTokMax) return fail(W4H_ERR_INVALID, "max_steps outside [0, %d)", kBeamTokMax);
+  const int B = in.beam, V = s->m->dims.n_vocab;
+  int rc;
+  HIPCHK(hipSetDevice(s->m->device));
+  if ((rc = ensure(s->wbeam, sizeof(BeamDev)))) return rc;
+  if ((rc = ensure(s->wbsup, sizeof(int32_t) * (size_t)std::max(1, in.n_suppress)))) return rc;
+  // initial state: one token per beam, nothing finished
+  std::vector<char> hb(sizeof(BeamDev), 0);
+  BeamDev* h = reinterpret_cast<BeamDev*>(hb.data());
+  for (int b = 0; b < B; b++) {
+    h->len[0][b] = 1;
+    h->toks[0][b][0] = in.first_tokens[b];
+    h->lps[b] = in.first_lps[b];
+  }
+  HIPCHK(hipMemcpy(s->wbeam.p, hb.data(), sizeof(BeamDev), hipMemcpyHostToDevice));
+  if (in.n_suppress > 0)
+    HIPCHK(hipMemcpy(s->wbsup.p, in.suppress, sizeof(int32_t) * in.n_suppress, hipMemcpyHostToDevice));
+  // first run's inputs (tokens, mask, slot table) through the staging area
+  char* hp = static_cast<char*>(s->h_in.p);
+  *reinterpret_cast<unsigned*>(hp) = 0u;
+  memcpy(hp + s->o_toks, in.first_tokens, sizeof(int32_t) * B);
+  memcpy(hp + s->o_mask2, in.first_mask, sizeof(uint32_t) * (size_t)B * s->mw);
+  memcpy(hp + s->o_slots, s->slots_host.data(), sizeof(int32_t) * s->slots_host.size());
+  HIPCHK(hipMemcpyAsync(s->in.p, hp, s->in_bytes, hipMemcpyHostToDevice, s->stream));
+  s->slots_dirty = false;
+  constexpr int kChunk = 32;  // steps per launch; the host checks for the end of the search between launches
+  if ((rc = ensure(s->out, sizeof(w4h_step_out) * (size_t)kChunk * B))) return rc;
+  int remaining = in.max_steps;
+  bool first = true;
+  while (remaining > 0) {
+    const int n = std::min(kChunk, remaining);
+    if (s->kv_len + n > s->max_ctx)
+      return fail(W4H_ERR_CAPACITY, "self-KV capacity %d exceeded (kv_len %d + %d steps)", s->max_ctx, s->kv_len, n);
+    WideParams wp = wide_params(s);
+    wp.nsteps = n;
+    wp.kv_len0 = s->kv_len;
+    wp.tokens0 = s->in_at<int32_t>(s->o_toks);
+    wp.forced = nullptr;
+    wp.mask2 = s->in_at<uint32_t>(s->o_mask2);
+    wp.slots = s->in_at<int32_t>(s->o_slots);
+    wp.topk = B + 1;
+    wp.out = s->out.as<w4h_step_out>();
+    wp.logits_out = nullptr;
+    wp.beam_dev = s->wbeam.as<BeamDev>();
+    wp.beam_sup = s->wbsup.as<int32_t>();
+    wp.beam_nsup = in.n_suppress;
+    wp.beam_eot = in.eot;
+    wp.beam_tsb = in.timestamp_begin;
+    wp.tok_dev = first ? 0 : 1;
+    wp.graph = s->use_graph ? &s->wgraph_beam : nullptr;
+    hipError_t le = launch_wide(wp, s->stream);
+    if (le != hipSuccess) return fail(W4H_ERR_DEVICE, "beam step launch failed: %s", hipGetErrorString(le));
+    WideCtl c{};
+    HIPCHK(hipMemcpyAsync(&c, s->wctl.p, sizeof(WideCtl), hipMemcpyDeviceToHost, s->stream));
+    HIPCHK(hipStreamSynchronize(s->stream));
+    s->kv_len += c.i;  // steps that ran (each appended its KV row)
+    remaining -= n;
+    first = false;
+    if (c.stop) break;
+  }
+  // results, and the slot table the device left behind
+  HIPCHK(hipMemcpy(hb.data(), s->wbeam.p, sizeof(BeamDev), hipMemcpyDeviceToHost));
+  HIPCHK(hipMemcpy(s->slots_host.data(), s->in_at<int32_t>(s->o_slots), sizeof(int32_t) * s->slots_host.size(),
+                   hipMemcpyDeviceToHost));
+  s->slots_identity = false;
+  s->slots_dirty = false;
+  out->fin.clear();
+  out->fin_lp.clear();
+  for (int f = 0; f < h->nfin; f++) {
+    out->fin.emplace_back(h->fin_toks[f], h->fin_toks[f] + h->fin_len[f]);
+    out->fin_lp.push_back(h->fin_lp[f]);
+  }
+  out->toks.assign(B, {});
+  out->lps.assign(B, 0.0);
+  for (int b = 0; b < B; b++) {
+    out->toks[b].assign(h->toks[h->cur][b], h->toks[h->cur][b] + h->len[h->cur][b]);
+    out->lps[b] = h->lps[b];
+  }
+  (void)V;
+  return W4H_OK;
+}
 w4h_dims session_dims(const w4h_session* s) { return s->m->dims; }
 }  // namespace w4h

@@ -277,7 +277,34 @@ int w4h_decode_beam(w4h_session* s, const w4h_decode_opts* o, w4h_decode_result*
     double score;
     int beam, tok;
   };
-  for (int step = 1; step < o->max_tokens; step++) {
+  if (w4h::session_device_beam(s) && o->max_tokens > 1) {
+    // batched session: the whole search runs on the device (k_w_beam after every step), the host
+    // supplies the first beams and the first step's mask (the same rules as below)
+    mask.clear();
+    for (int b = 0; b < B; b++) {
+      tok[b] = toks[b].back();
+      apply_suppress(mask, b, o->suppress, o->n_suppress);
+      repetition_penalty(mask, b, toks[b]);
+      if (o->timestamp_begin > 0) timestamp_rules(mask, b, toks[b], o->timestamp_begin, o->eot, false);
+    }
+    w4h::BeamSearchIn in{};
+    in.beam = B;
+    in.eot = o->eot;
+    in.timestamp_begin = o->timestamp_begin;
+    in.max_steps = o->max_tokens - 1;
+    in.suppress = o->suppress;
+    in.n_suppress = o->n_suppress;
+    in.first_tokens = tok.data();
+    in.first_lps = lps.data();
+    in.first_mask = mask.bits.data();
+    w4h::BeamSearchOut res;
+    if ((rc = w4h::device_beam_search(s, in, &res))) return rc;
+    fin_t = res.fin;
+    fin_lp = res.fin_lp;
+    toks = res.toks;
+    lps = res.lps;
+  }
+  for (int step = w4h::session_device_beam(s) ? o->max_tokens : 1; step < o->max_tokens; step++) {
     mask.clear();
     std::vector<bool> live(B);
     for (int b = 0; b < B; b++) {

@@ -3,6 +3,8 @@
 
 #include <stdint.h>
 
+#include <vector>
+
 #include "../../include/w4h.h"
 
 namespace w4h {
@@ -11,4 +13,22 @@ float half_to_float(uint16_t h);
 uint16_t float_to_half(float f);
 int session_rows(const w4h_session* s);
 w4h_dims session_dims(const w4h_session* s);
+
+// Beam search run on the device by a batched-engine session (rows = beams): the first beams come
+// from the host (prompt step), then up to max_steps device steps, each ending with the device beam
+// step.  Returns the finished hypotheses and the last live beams.
+bool session_device_beam(const w4h_session* s);
+struct BeamSearchIn {
+  int beam, eot, timestamp_begin, max_steps;
+  const int32_t* suppress;
+  int n_suppress;
+  const int32_t* first_tokens;  // [beam]
+  const double* first_lps;      // [beam]
+  const uint32_t* first_mask;   // [beam][(n_vocab + 31) / 32] suppression mask of the first device step
+};
+struct BeamSearchOut {
+  std::vector<std::vector<int32_t>> fin, toks;
+  std::vector<double> fin_lp, lps;
+};
+int device_beam_search(w4h_session* s, const BeamSearchIn& in, BeamSearchOut* out);
 }  // namespace w4h

@@ -98,12 +98,30 @@ struct WideCtl {
   int kv_len0;     // KV length before the run
   int forced_on, out_on, logits_on, mask_on, mask2_on, slots_on, topk, probe;
   unsigned done;   // selection-merge arrivals in the current step
+  int tok_dev;     // the run's first tokens come from next_tok (a continued device beam search)
+  int stop;        // set by the device beam step when the search has ended: later kernels return
+};
+
+// Device beam search state (rows are beams; beam <= kBeamMax): token histories double-buffered
+// by step parity, cumulative log-probabilities in double as the reference keeps them, and the
+// finished list (tokens without the end token).
+constexpr int kBeamMax = W4H_TOPK_MAX - 1;
+constexpr int kBeamTokMax = 1024;
+struct BeamDev {
+  double lps[kBeamMax];
+  double fin_lp[kBeamMax];
+  int len[2][kBeamMax];
+  int fin_len[kBeamMax];
+  int nfin, cur, done;
+  int toks[2][kBeamMax][kBeamTokMax];
+  int fin_toks[kBeamMax][kBeamTokMax];
 };
 
 // Captured step of a session (HIP graph exec) and the buffer addresses it was captured with.
 struct WideGraph {
   void* exec = nullptr;
   const void* key[8] = {};
+  uintptr_t bkey[6] = {};
 };
 
 struct WideParams {
@@ -128,6 +146,10 @@ struct WideParams {
   int32_t* next_tok;        // [S] argmax of the last step (greedy feedback)
   int nch, chlen, nsel;
   WideCtl* ctl;             // device control block
+  // device beam search (beam_dev != null): one k_w_beam per step after the selection
+  BeamDev* beam_dev;
+  const int32_t* beam_sup;  // suppressed token ids [beam_nsup]
+  int beam_nsup, beam_eot, beam_tsb, tok_dev;
   WideGraph* graph;         // host cache of the captured step, or null to launch every kernel
   WideGemm g_qkv, g_o, g_cq, g_co, g_1, g_2, g_v;  // per-layer shapes and slicing; g_v = logits
   // control

@@ -53,6 +53,7 @@ struct GemmArgs {
   const float* act;      // [Rp][lda] fp32 rows (rows >= S read as zero)
   int lda, S;
   float* part;           // [slices][Rp][N] partial sums (rows < S written)
+  const WideCtl* ctl;    // a stopped run (ended beam search) returns at once
 };
 
 // Sum of the ks slices of a GEMM output at p[j * ss + idx]: kSliceBatch loads in flight, added in
@@ -82,6 +83,7 @@ DEV float slice_sum(const float* p, int ks, size_t ss, size_t idx) {
 template <int MT, int WQ8, int KB, int NW>
 __global__ __launch_bounds__(256) void k_w_gemm(GemmArgs a) {
   extern __shared__ __align__(16) uint16_t lds_h[];
+  if (a.ctl->stop) return;
   constexpr int KW = 4 / NW;
   constexpr int Rp = MT * 16;
   constexpr int CB = 16 * NW;                // columns per workgroup
@@ -229,6 +231,7 @@ __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl
                                                  const float* __restrict__ g, const float* __restrict__ b, float* __restrict__ act,
                                                  int lda) {
   __shared__ float red[8];
+  if (ctl->stop) return;
   const int s = blockIdx.x, tid = threadIdx.x;
   float v[kWideVec];
   if (EMB) {
@@ -236,7 +239,8 @@ __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl
     // positional row clamped as the reference
     const int i0 = ctl->i, t = ctl->kv_len0 + i0;
     const int pe = t < C - 1 ? t : C - 1;
-    const int tk = i0 == 0 ? tokens0[s] : (ctl->forced_on ? forced[(size_t)(i0 - 1) * S + s] : next_tok[s]);
+    const int tk = (i0 == 0 && !ctl->tok_dev) ? tokens0[s]
+                                              : (ctl->forced_on ? forced[(size_t)(i0 - 1) * S + s] : next_tok[s]);
 #pragma unroll
     for (int i = 0; i < kWideVec; ++i) {
       const int j = tid + 256 * i;
@@ -301,8 +305,9 @@ __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl
 }
 
 // act[r][k] = GELU(bias[k] + the slices of the MLP1 GEMM), r < S, k < n.
-__global__ __launch_bounds__(256) void k_w_gelu(const float* __restrict__ P, int ks, size_t ss, const float* __restrict__ bias, int S,
-                                                int n, float* __restrict__ act, int lda) {
+__global__ __launch_bounds__(256) void k_w_gelu(const WideCtl* __restrict__ ctl, const float* __restrict__ P, int ks, size_t ss,
+                                                const float* __restrict__ bias, int S, int n, float* __restrict__ act, int lda) {
+  if (ctl->stop) return;
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= S * n) return;
   const int r = i / n, k = i - r * n;
@@ -348,6 +353,7 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
                                                 const int32_t* __restrict__ slot_table, float* __restrict__ act, int lda) {
   extern __shared__ float sc[];  // [t + 1] scores, then probabilities
   __shared__ float q[64], kc[64], vc[64], red[4 * 64], stat[8];
+  if (ctl->stop) return;
   const int s = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int t = ctl->kv_len0 + ctl->i;  // position of the current token
   const int32_t* srow = ctl->slots_on ? slot_table + (size_t)s * max_ctx : nullptr;
@@ -480,13 +486,15 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
 // single chunk, the normalised output written to act directly.
 
 template <int RG>
-__global__ __launch_bounds__(256) void k_w_cross(const float* __restrict__ P, int ks, size_t ss, const float* __restrict__ bcq, int d,
+__global__ __launch_bounds__(256) void k_w_cross(const WideCtl* __restrict__ ctl, const float* __restrict__ P, int ks, size_t ss,
+                                                 const float* __restrict__ bcq, int d,
                                                  int H, int A, int l, int L, int S, int X, int chlen, int nch,
                                                  const uint16_t* __restrict__ xk,
                                                  const uint16_t* __restrict__ xv, float* __restrict__ cpart,
                                                  float* __restrict__ act, int lda) {
   extern __shared__ float scs[];  // [RG][chlen]
   __shared__ float q[RG * 64], red[4 * RG * 64], rm[RG], rl[RG];
+  if (ctl->stop) return;
   const int e = blockIdx.x, h = blockIdx.y, c = blockIdx.z % nch, rg = blockIdx.z / nch;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   int r0, nr;
@@ -633,7 +641,9 @@ __global__ __launch_bounds__(256) void k_w_cross(const float* __restrict__ P, in
 // Merge the chunk partials of (row, head) into act[row][h*64, +64).  64 threads; lane c holds chunk
 // c's (max, sum) (nch <= 64), then every lane adds its output element over the chunks in chunk order
 // with eight loads in flight.
-__global__ __launch_bounds__(64) void k_w_cmerge(const float* __restrict__ cpart, int H, int nch, float* __restrict__ act, int lda) {
+__global__ __launch_bounds__(64) void k_w_cmerge(const WideCtl* __restrict__ ctl, const float* __restrict__ cpart, int H, int nch,
+                                                  float* __restrict__ act, int lda) {
+  if (ctl->stop) return;
   const int s = blockIdx.x, h = blockIdx.y, k = threadIdx.x;
   const float* p = cpart + ((size_t)s * H + h) * nch * kPartWords;
   const float mc = k < nch ? p[k * kPartWords] : -INFINITY;
@@ -664,6 +674,7 @@ __global__ __launch_bounds__(256) void k_w_select(const WideCtl* __restrict__ ct
                                                   float* __restrict__ selp, int nsel, float* __restrict__ logits_buf) {
   __shared__ float lg[4][kWideSelChunk], rw[4][kWideSelChunk];
   __shared__ int idx[4][kWideSelChunk];
+  if (ctl->stop) return;
   const int s = blockIdx.x, wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const uint32_t* mask = ctl->mask_on ? mask_buf : nullptr;
   const uint32_t* mask2 = ctl->mask2_on ? mask2_buf : nullptr;
@@ -688,6 +699,7 @@ __global__ __launch_bounds__(256) void k_w_select(const WideCtl* __restrict__ ct
 __global__ __launch_bounds__(64) void k_w_selmerge(WideCtl* __restrict__ ctl, const float* __restrict__ selp, int S, int nsel,
                                                    w4h_step_out* out_buf, int32_t* __restrict__ next_tok) {
   __shared__ float rec[kSelWords];
+  if (ctl->stop) return;
   const int s = blockIdx.x;
   const int topk = ctl->topk, i = ctl->i;
   sel_merge(selp + (size_t)s * nsel * kSelWords, nsel, kSelWords, topk, rec);
@@ -703,6 +715,190 @@ __global__ __launch_bounds__(64) void k_w_selmerge(WideCtl* __restrict__ ctl, co
       __hip_atomic_store(&ctl->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&ctl->i, i + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+  }
+}
+
+
+// ------------------------------------------------------------------------------------------------
+// One step of beam search on the device (WhisperDecoder.decodeBeam, main/nn/WhisperDecoder.java:
+// 278-394, the same steps as the host driver): candidates (beam b, rank k) of the live beams score
+// lps[b] + (topk_logit - logsumexp); a stable descending sort; end tokens go to the finished list
+// (until beam_size are finished), the first beam_size others become the new beams, leftover beams
+// continue from the first; the slot table is regathered from the parents; the next step's tokens
+// and suppression mask (suppress list, 3- and 4-gram repeats, timestamp rules) are written.  When
+// the search ends (nothing saved, or enough finished) the beams are left as they were and ctl->stop
+// makes the later steps of the run return at once.  One workgroup.
+
+constexpr int kBeamCand = kBeamMax * (kBeamMax + 1);
+constexpr int kSlotChunk = 1024;
+
+DEV void mask_set(uint32_t* row, int V, int t) {
+  if (t >= 0 && t < V) atomicOr(row + (t >> 5), 1u << (t & 31));
+}
+
+__global__ __launch_bounds__(256) void k_w_beam(WideCtl* __restrict__ ctl, BeamDev* __restrict__ bd, const w4h_step_out* out_buf,
+                                                int B, int eot, int tsb, const int32_t* __restrict__ sup, int nsup, int V, int mw,
+                                                uint32_t* __restrict__ mask2, int32_t* __restrict__ slots, int max_ctx,
+                                                int32_t* __restrict__ next_tok) {
+  if (ctl->stop) return;
+  __shared__ double csc[kBeamCand];
+  __shared__ int ctok[kBeamCand], cbeam[kBeamCand], clive[kBeamCand], order[kBeamCand];
+  __shared__ int psrc[kBeamMax], ptok[kBeamMax], fsrc[kBeamMax];
+  __shared__ double plp[kBeamMax], fsc[kBeamMax];
+  __shared__ int s_nf0, s_nf, s_saved, s_done;
+  __shared__ int32_t sl[kBeamMax * kSlotChunk];
+  const int tid = threadIdx.x;
+  const int step = ctl->i - 1;  // the selection merge of this step has advanced the index
+  const int kv = ctl->kv_len0 + step + 1;  // KV length after this step
+  const int cur = bd->cur, nxt = cur ^ 1;
+  const int nc = B * (B + 1);
+  // candidates in the host driver's order (beam-major, then rank)
+  if (tid < nc) {
+    const int b = tid / (B + 1), k = tid - b * (B + 1);
+    const int lb = bd->len[cur][b];
+    const bool live = bd->toks[cur][b][lb - 1] != eot;
+    const w4h_step_out& o = out_buf[(size_t)step * B + b];
+    const bool ok = o.topk_logits[k] > -INFINITY;
+    const float lp = ok ? o.topk_logits[k] - o.logsumexp : -INFINITY;
+    csc[tid] = bd->lps[b] + (double)lp;
+    ctok[tid] = ok ? o.topk_ids[k] : 0;
+    cbeam[tid] = b;
+    clive[tid] = live;
+  }
+  __syncthreads();
+  // stable descending sort of the live candidates: rank = #(better or equal-and-earlier)
+  if (tid < nc && clive[tid]) {
+    int rank = 0;
+    for (int c = 0; c < nc; ++c)
+      if (clive[c] && (csc[c] > csc[tid] || (csc[c] == csc[tid] && c < tid))) ++rank;
+    order[rank] = tid;
+  }
+  if (tid == 0) {
+    int nl = 0;
+    for (int c = 0; c < nc; ++c) nl += clive[c];
+    s_saved = nl;  // number of live candidates, replaced below
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const int nlive = s_saved;
+    int nf = bd->nfin, saved = 0;
+    s_nf0 = nf;
+    for (int q = 0; q < nlive; ++q) {
+      const int c = order[q];
+      if (ctok[c] == eot) {
+        fsrc[nf] = cbeam[c];
+        fsc[nf] = csc[c];
+        ++nf;
+        if (nf >= B) break;
+        continue;
+      }
+      if (saved >= B) continue;
+      psrc[saved] = cbeam[c];
+      ptok[saved] = ctok[c];
+      plp[saved] = csc[c];
+      ++saved;
+    }
+    const int done = (nlive == 0 || saved == 0 || nf >= B) ? 1 : 0;
+    for (int j = saved; j < B && saved > 0; ++j) {  // leftover beams continue from the first
+      psrc[j] = psrc[0];
+      ptok[j] = ptok[0];
+      plp[j] = plp[0];
+    }
+    s_nf = nf;
+    s_saved = saved;
+    s_done = done;
+  }
+  __syncthreads();
+  // finished entries of this step: the source beam's tokens (without the end token)
+  for (int f = s_nf0; f < s_nf; ++f) {
+    const int b = fsrc[f], lb = bd->len[cur][b];
+    for (int q = tid; q < lb; q += 256) bd->fin_toks[f][q] = bd->toks[cur][b][q];
+    if (tid == 0) {
+      bd->fin_len[f] = lb;
+      bd->fin_lp[f] = fsc[f];
+    }
+  }
+  if (s_done) {
+    if (tid == 0) {
+      bd->nfin = s_nf;
+      bd->done = 1;
+      __hip_atomic_store(&ctl->stop, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
+  // new beams
+  for (int j = 0; j < B; ++j) {
+    const int b = psrc[j], lb = bd->len[cur][b];
+    for (int q = tid; q < lb; q += 256) bd->toks[nxt][j][q] = bd->toks[cur][b][q];
+    if (tid == 0) {
+      bd->toks[nxt][j][lb] = ptok[j];
+      bd->len[nxt][j] = lb + 1;
+      bd->lps[j] = plp[j];
+      next_tok[j] = ptok[j];
+    }
+  }
+  // slot table: row j continues parent psrc[j] over positions [0, kv)
+  for (int p0 = 0; p0 < kv; p0 += kSlotChunk) {
+    const int np = min(kSlotChunk, kv - p0);
+    for (int e = tid; e < B * np; e += 256) {
+      const int r = e / np, q = e - r * np;
+      sl[r * kSlotChunk + q] = slots[(size_t)r * max_ctx + p0 + q];
+    }
+    __syncthreads();
+    for (int e = tid; e < B * np; e += 256) {
+      const int r = e / np, q = e - r * np;
+      slots[(size_t)r * max_ctx + p0 + q] = sl[psrc[r] * kSlotChunk + q];
+    }
+    __syncthreads();
+  }
+  // next step's suppression mask per beam
+  for (int e = tid; e < B * mw; e += 256) mask2[e] = 0u;
+  __syncthreads();
+  for (int j = 0; j < B; ++j) {
+    uint32_t* row = mask2 + (size_t)j * mw;
+    const int* g = bd->toks[nxt][j];
+    const int cnt = bd->len[cur][psrc[j]] + 1;
+    for (int q = tid; q < nsup; q += 256) mask_set(row, V, sup[q]);
+    // n-gram repeats (n = 3, 4): a match of the last n-1 tokens at i blocks the token after it
+    for (int nn = 3; nn <= 4; ++nn) {
+      for (int i = tid; i <= cnt - nn; i += 256) {
+        bool match = true;
+        for (int q = 0; q < nn - 1; ++q) match &= g[i + q] == g[cnt - (nn - 1) + q];
+        if (match) mask_set(row, V, g[i + nn - 1]);
+      }
+    }
+    if (tsb > 0) {  // timestamp rules (not the first step)
+      if (tid == 0) mask_set(row, V, tsb - 1);
+      const bool last_ts = g[cnt - 1] >= tsb;
+      const bool pen_ts = cnt < 2 || g[cnt - 2] >= tsb;
+      int lastTs = -1;
+      for (int q = cnt - 1; q >= 0; --q)
+        if (g[q] >= tsb) {
+          lastTs = g[q];
+          break;
+        }
+      int lo1 = 0, hi1 = 0, lo2 = 0, hi2 = 0;
+      if (last_ts) {
+        if (pen_ts) {
+          lo1 = tsb;
+          hi1 = V;
+        } else {
+          lo1 = 0;
+          hi1 = eot;
+        }
+      }
+      if (lastTs >= 0) {
+        lo2 = tsb;
+        hi2 = (last_ts && !pen_ts) ? lastTs + 1 : lastTs;
+      }
+      for (int t = lo1 + tid; t < hi1; t += 256) mask_set(row, V, t);
+      for (int t = lo2 + tid; t < hi2; t += 256) mask_set(row, V, t);
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    bd->nfin = s_nf;
+    bd->cur = nxt;
   }
 }
 
@@ -774,6 +970,7 @@ static hipError_t gemm(const WideParams& p, const WideGemm& g, const void* w, co
   a.lda = 4 * p.d;
   a.S = p.S;
   a.part = p.part;
+  a.ctl = p.ctl;
   if (p.Rp == 16) return p.wq8 ? gemm_mt<1, 1>(g.kb, a, g.ks, st) : gemm_mt<1, 0>(g.kb, a, g.ks, st);
   return p.wq8 ? gemm_mt<2, 1>(g.kb, a, g.ks, st) : gemm_mt<2, 0>(g.kb, a, g.ks, st);
 }
@@ -843,20 +1040,20 @@ static hipError_t enqueue_step(const WideParams& p, hipStream_t st) {
     WCHK(resid(p, &p.g_o, lw.b_o, lw.ln2_g, lw.ln2_b, st));
     WCHK(gemm(p, p.g_cq, lw.w_cq, lw.s_cq, p.act, st));
     if (rg_rows == 1)
-      hipLaunchKernelGGL(k_w_cross<1>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.part, p.g_cq.ks, sstride(p, p.g_cq),
+      hipLaunchKernelGGL(k_w_cross<1>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.ctl, p.part, p.g_cq.ks, sstride(p, p.g_cq),
                          lw.b_cq, d, H, p.A, l, p.L, p.S, p.X, p.chlen, p.nch, p.xk, p.xv, p.cpart, p.act, lda);
     else
-      hipLaunchKernelGGL(k_w_cross<8>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.part, p.g_cq.ks, sstride(p, p.g_cq),
+      hipLaunchKernelGGL(k_w_cross<8>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.ctl, p.part, p.g_cq.ks, sstride(p, p.g_cq),
                          lw.b_cq, d, H, p.A, l, p.L, p.S, p.X, p.chlen, p.nch, p.xk, p.xv, p.cpart, p.act, lda);
     WCHK(hipGetLastError());
     if (p.nch > 1) {
-      hipLaunchKernelGGL(k_w_cmerge, dim3(p.S, H), dim3(64), 0, st, p.cpart, H, p.nch, p.act, lda);
+      hipLaunchKernelGGL(k_w_cmerge, dim3(p.S, H), dim3(64), 0, st, p.ctl, p.cpart, H, p.nch, p.act, lda);
       WCHK(hipGetLastError());
     }
     WCHK(gemm(p, p.g_co, lw.w_co, lw.s_co, p.act, st));
     WCHK(resid(p, &p.g_co, lw.b_co, lw.ln3_g, lw.ln3_b, st));
     WCHK(gemm(p, p.g_1, lw.w_1, lw.s_1, p.act, st));
-    hipLaunchKernelGGL(k_w_gelu, dim3((p.S * 4 * d + 255) / 256), dim3(256), 0, st, p.part, p.g_1.ks, sstride(p, p.g_1), lw.b_1, p.S,
+    hipLaunchKernelGGL(k_w_gelu, dim3((p.S * 4 * d + 255) / 256), dim3(256), 0, st, p.ctl, p.part, p.g_1.ks, sstride(p, p.g_1), lw.b_1, p.S,
                        4 * d, p.hid, lda);
     WCHK(hipGetLastError());
     WCHK(gemm(p, p.g_2, lw.w_2, lw.s_2, p.hid, st));
@@ -868,6 +1065,12 @@ static hipError_t enqueue_step(const WideParams& p, hipStream_t st) {
                      p.mask2, p.mw, p.selp, p.nsel, p.logits_out);
   WCHK(hipGetLastError());
   hipLaunchKernelGGL(k_w_selmerge, dim3(p.S), dim3(64), 0, st, p.ctl, p.selp, p.S, p.nsel, p.out, p.next_tok);
+  WCHK(hipGetLastError());
+  if (p.beam_dev) {
+    hipLaunchKernelGGL(k_w_beam, dim3(1), dim3(256), 0, st, p.ctl, p.beam_dev, p.out, p.S, p.beam_eot, p.beam_tsb, p.beam_sup,
+                       p.beam_nsup, p.V, p.mw, const_cast<uint32_t*>(p.mask2), const_cast<int32_t*>(p.slots), p.max_ctx, p.next_tok);
+    WCHK(hipGetLastError());
+  }
   return hipGetLastError();
 }
 
@@ -891,6 +1094,8 @@ hipError_t launch_wide(const WideParams& p, hipStream_t st) {
   c.topk = p.topk;
   c.probe = p.probe;
   c.done = 0;
+  c.tok_dev = p.tok_dev;
+  c.stop = 0;
   hipLaunchKernelGGL(k_w_setctl, dim3(1), dim3(64), 0, st, p.ctl, c);
   WCHK(hipGetLastError());
   if (!p.graph) {
@@ -900,8 +1105,12 @@ hipError_t launch_wide(const WideParams& p, hipStream_t st) {
   // Buffers a step reads or writes that may be (re)allocated between runs: the captured step is
   // valid while they stay where they were.
   const void* key[8] = {p.tokens0, p.forced, p.out, p.logits_out, p.mask2, p.mask, p.slots, p.ctl};
+  // and the beam-search arguments baked into the captured beam kernel (compared exactly)
+  const uintptr_t bkey[6] = {(uintptr_t)p.beam_dev, (uintptr_t)p.beam_sup, (uintptr_t)p.beam_nsup, (uintptr_t)p.beam_eot,
+                             (uintptr_t)p.beam_tsb, (uintptr_t)1};
   bool same = p.graph->exec != nullptr;
   for (int k = 0; k < 8 && same; ++k) same = key[k] == nullptr || key[k] == p.graph->key[k];
+  for (int k = 0; k < 6 && same; ++k) same = bkey[k] == p.graph->bkey[k];
   if (!same) {
     // capture with every optional buffer present in the key, so later runs that leave some out
     // (null: switched off in the control block) replay the same graph
@@ -928,6 +1137,7 @@ hipError_t launch_wide(const WideParams& p, hipStream_t st) {
     WCHK(ie);
     p.graph->exec = exec;
     for (int k = 0; k < 8; ++k) p.graph->key[k] = key[k];
+    for (int k = 0; k < 6; ++k) p.graph->bkey[k] = bkey[k];
   }
   for (int i = 0; i < p.nsteps; ++i) WCHK(hipGraphLaunch(static_cast<hipGraphExec_t>(p.graph->exec), st));
   return hipSuccess;
