@@ -1049,10 +1049,76 @@ DEV void attn_rx(const KVRegs<KPT>& r, int n, const float (&Q)[8], float scale, 
 // kSelWords floats: [max, argmax, sumexp(masked - max), raw max, raw sumexp, probe, topk values[8],
 // topk ids[8]].  Ties go to the lower vocabulary id everywhere.
 
+// Top-k helpers: every lane keeps its own best W4H_TOPK_MAX (value descending, lower id on ties) in
+// registers; the wave then pops the best lane head k times.  Entries at -inf never enter.
+struct TopList {
+  float v[W4H_TOPK_MAX];
+  int i[W4H_TOPK_MAX];
+};
+
+DEV void top_init(TopList& t) {
+#pragma unroll
+  for (int k = 0; k < W4H_TOPK_MAX; ++k) {
+    t.v[k] = -INFINITY;
+    t.i[k] = 0x7fffffff;
+  }
+}
+
+DEV bool top_better(float v, int id, float w, int jd) { return v > w || (v == w && id < jd); }
+
+// Insert (v, id) into the lane's sorted list (no-op unless it beats the last entry).
+DEV void top_insert(TopList& t, float v, int id) {
+  if (!(v > -INFINITY) || !top_better(v, id, t.v[W4H_TOPK_MAX - 1], t.i[W4H_TOPK_MAX - 1])) return;
+#pragma unroll
+  for (int k = W4H_TOPK_MAX - 1; k > 0; --k) {
+    const bool shift = top_better(v, id, t.v[k - 1], t.i[k - 1]);
+    const bool here = !shift && top_better(v, id, t.v[k], t.i[k]);
+    if (shift) {
+      t.v[k] = t.v[k - 1];
+      t.i[k] = t.i[k - 1];
+    } else if (here) {
+      t.v[k] = v;
+      t.i[k] = id;
+    }
+  }
+  if (top_better(v, id, t.v[0], t.i[0])) {
+    t.v[0] = v;
+    t.i[0] = id;
+  }
+}
+
+// k rounds: the wave's best lane head is taken and that lane advances.  tv/ti (every lane) get the
+// wave's top k in order.
+DEV void top_pop(TopList& t, int topk, float* tv, int* ti) {
+  int head = 0;
+  for (int k = 0; k < W4H_TOPK_MAX; ++k) {
+    tv[k] = -INFINITY;
+    ti[k] = 0x7fffffff;
+  }
+  for (int k = 0; k < topk; ++k) {
+    float hv = -INFINITY;
+    int hi = 0x7fffffff;
+#pragma unroll
+    for (int q = 0; q < W4H_TOPK_MAX; ++q)
+      if (q == head) {
+        hv = t.v[q];
+        hi = t.i[q];
+      }
+    float bv = hv;
+    int bi = hi;
+    wave_argmax(bv, bi);
+    tv[k] = bv;
+    ti[k] = bv > -INFINITY ? bi : 0x7fffffff;
+    if (bv > -INFINITY && hi == bi && hv == bv) ++head;
+  }
+}
+
 DEV void sel_partial(const float* lg, const float* rw, const int* idx, int n, int probe, int topk, float* rec) {
   const int lane = threadIdx.x & 63;
   float bv = -INFINITY, rv = -INFINITY, pv = -INFINITY;
   int bi = 0x7fffffff;
+  TopList tl;
+  top_init(tl);
   for (int j = lane; j < n; j += 64) {
     const float v = lg[j];
     const int id = idx[j];
@@ -1062,6 +1128,7 @@ DEV void sel_partial(const float* lg, const float* rw, const int* idx, int n, in
     }
     rv = fmaxf(rv, rw[j]);
     if (id == probe) pv = rw[j];
+    if (topk > 0) top_insert(tl, v, id);
   }
   wave_argmax(bv, bi);
   rv = wave_max(rv);
@@ -1075,27 +1142,7 @@ DEV void sel_partial(const float* lg, const float* rw, const int* idx, int n, in
   re = wave_sum(re);
   float tv[W4H_TOPK_MAX];
   int ti[W4H_TOPK_MAX];
-  for (int k = 0; k < W4H_TOPK_MAX; ++k) {
-    tv[k] = -INFINITY;
-    ti[k] = 0x7fffffff;
-  }
-  for (int k = 0; k < topk; ++k) {
-    float cv = -INFINITY;
-    int ci = 0x7fffffff;
-    for (int j = lane; j < n; j += 64) {
-      const float v = lg[j];
-      const int id = idx[j];
-      bool taken = false;
-      for (int q = 0; q < k; ++q) taken |= (ti[q] == id);
-      if (!taken && v > -INFINITY && (v > cv || (v == cv && id < ci))) {
-        cv = v;
-        ci = id;
-      }
-    }
-    wave_argmax(cv, ci);
-    tv[k] = cv;
-    ti[k] = ci;
-  }
+  top_pop(tl, topk, tv, ti);
   if (lane == 0) {
     rec[0] = bv;
     rec[1] = __int_as_float(bi);
@@ -1128,10 +1175,13 @@ DEV int sel_argmax(const float* recs, int n, int stride) {
 }
 
 // Merge n selection partials (stride floats apart) into one partial of the same layout, one wave.
+// The partials cover disjoint vocabulary ranges, so their top-k lists hold distinct ids.
 DEV void sel_merge(const float* recs, int n, int stride, int topk, float* out_rec) {
   const int lane = threadIdx.x & 63;
   float bv = -INFINITY, rv = -INFINITY, pv = -INFINITY;
   int bi = 0x7fffffff;
+  TopList tl;
+  top_init(tl);
   for (int g = lane; g < n; g += 64) {
     const float* r = recs + (size_t)g * stride;
     const int id = __float_as_int(r[1]);
@@ -1141,6 +1191,7 @@ DEV void sel_merge(const float* recs, int n, int stride, int topk, float* out_re
     }
     rv = fmaxf(rv, r[3]);
     pv = fmaxf(pv, r[5]);
+    for (int q = 0; q < topk; ++q) top_insert(tl, r[6 + q], __float_as_int(r[6 + W4H_TOPK_MAX + q]));
   }
   wave_argmax(bv, bi);
   rv = wave_max(rv);
@@ -1155,28 +1206,7 @@ DEV void sel_merge(const float* recs, int n, int stride, int topk, float* out_re
   re = wave_sum(re);
   float tv[W4H_TOPK_MAX];
   int ti[W4H_TOPK_MAX];
-  for (int k = 0; k < W4H_TOPK_MAX; ++k) {
-    tv[k] = -INFINITY;
-    ti[k] = 0x7fffffff;
-  }
-  for (int k = 0; k < topk; ++k) {
-    float cv = -INFINITY;
-    int ci = 0x7fffffff;
-    for (int c = lane; c < n * W4H_TOPK_MAX; c += 64) {
-      const int g = c / W4H_TOPK_MAX, q = c % W4H_TOPK_MAX;
-      const float v = recs[(size_t)g * stride + 6 + q];
-      const int id = __float_as_int(recs[(size_t)g * stride + 6 + W4H_TOPK_MAX + q]);
-      bool taken = false;
-      for (int p = 0; p < k; ++p) taken |= (ti[p] == id);
-      if (!taken && v > -INFINITY && (v > cv || (v == cv && id < ci))) {
-        cv = v;
-        ci = id;
-      }
-    }
-    wave_argmax(cv, ci);
-    tv[k] = cv;
-    ti[k] = ci;
-  }
+  top_pop(tl, topk, tv, ti);
   if (lane == 0) {
     out_rec[0] = bv;
     out_rec[1] = __int_as_float(bi);

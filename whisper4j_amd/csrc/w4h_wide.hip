@@ -732,149 +732,180 @@ __global__ __launch_bounds__(64) void k_w_selmerge(WideCtl* __restrict__ ctl, co
 constexpr int kBeamCand = kBeamMax * (kBeamMax + 1);
 constexpr int kSlotChunk = 1024;
 
-DEV void mask_set(uint32_t* row, int V, int t) {
-  if (t >= 0 && t < V) atomicOr(row + (t >> 5), 1u << (t & 31));
+// Dynamic LDS of k_w_beam: the slot-table chunk, then reused for the next step's masks.
+inline size_t beam_lds_bytes(int B, int mw) {
+  const size_t a = sizeof(int32_t) * (size_t)kBeamMax * kSlotChunk, b = sizeof(uint32_t) * (size_t)B * mw;
+  return a > b ? a : b;
 }
 
 __global__ __launch_bounds__(256) void k_w_beam(WideCtl* __restrict__ ctl, BeamDev* __restrict__ bd, const w4h_step_out* out_buf,
                                                 int B, int eot, int tsb, const int32_t* __restrict__ sup, int nsup, int V, int mw,
                                                 uint32_t* __restrict__ mask2, int32_t* __restrict__ slots, int max_ctx,
                                                 int32_t* __restrict__ next_tok) {
-  if (ctl->stop) return;
+  extern __shared__ int32_t dyn[];  // slot chunk [kBeamMax][kSlotChunk], later masks [B][mw]
+  __shared__ int stoks[kBeamMax][kBeamTokMax];
+  __shared__ int slen[kBeamMax];
+  __shared__ double slps[kBeamMax];
+  __shared__ float stl[kBeamCand], slse[kBeamMax];
+  __shared__ int sti[kBeamCand];
   __shared__ double csc[kBeamCand];
-  __shared__ int ctok[kBeamCand], cbeam[kBeamCand], clive[kBeamCand], order[kBeamCand];
+  __shared__ int clive[kBeamCand], order[kBeamCand];
   __shared__ int psrc[kBeamMax], ptok[kBeamMax], fsrc[kBeamMax];
   __shared__ double plp[kBeamMax], fsc[kBeamMax];
-  __shared__ int s_nf0, s_nf, s_saved, s_done;
-  __shared__ int32_t sl[kBeamMax * kSlotChunk];
+  __shared__ int s_nf0, s_nf, s_done, s_cur, s_maxlen;
+  if (ctl->stop) return;
   const int tid = threadIdx.x;
-  const int step = ctl->i - 1;  // the selection merge of this step has advanced the index
+  const int step = ctl->i - 1;             // the selection merge of this step has advanced the index
   const int kv = ctl->kv_len0 + step + 1;  // KV length after this step
-  const int cur = bd->cur, nxt = cur ^ 1;
   const int nc = B * (B + 1);
-  // candidates in the host driver's order (beam-major, then rank)
+  // 1. beam state and this step's records into LDS
+  if (tid == 0) {
+    s_cur = bd->cur;
+    s_nf0 = bd->nfin;
+  }
+  if (tid < B) {
+    const w4h_step_out& o = out_buf[(size_t)step * B + tid];
+    slse[tid] = o.logsumexp;
+    slps[tid] = bd->lps[tid];
+  }
   if (tid < nc) {
     const int b = tid / (B + 1), k = tid - b * (B + 1);
-    const int lb = bd->len[cur][b];
-    const bool live = bd->toks[cur][b][lb - 1] != eot;
     const w4h_step_out& o = out_buf[(size_t)step * B + b];
-    const bool ok = o.topk_logits[k] > -INFINITY;
-    const float lp = ok ? o.topk_logits[k] - o.logsumexp : -INFINITY;
-    csc[tid] = bd->lps[b] + (double)lp;
-    ctok[tid] = ok ? o.topk_ids[k] : 0;
-    cbeam[tid] = b;
-    clive[tid] = live;
+    stl[tid] = o.topk_logits[k];
+    sti[tid] = o.topk_ids[k];
   }
   __syncthreads();
-  // stable descending sort of the live candidates: rank = #(better or equal-and-earlier)
+  const int cur = s_cur, nxt = cur ^ 1;
+  if (tid < B) slen[tid] = bd->len[cur][tid];
+  __syncthreads();
+  if (tid == 0) {
+    int m = 0;
+    for (int b = 0; b < B; ++b) m = max(m, slen[b]);
+    s_maxlen = m;
+  }
+  __syncthreads();
+  for (int e = tid; e < B * s_maxlen; e += 256) {
+    const int b = e / s_maxlen, q = e - b * s_maxlen;
+    if (q < slen[b]) stoks[b][q] = bd->toks[cur][b][q];
+  }
+  __syncthreads();
+  // 2. candidates in the host driver's order (beam-major, then rank) and their stable sort
+  if (tid < nc) {
+    const int b = tid / (B + 1);
+    const bool ok = stl[tid] > -INFINITY;
+    const float lp = ok ? stl[tid] - slse[b] : -INFINITY;
+    csc[tid] = slps[b] + (double)lp;
+    if (!ok) sti[tid] = 0;
+    clive[tid] = stoks[b][slen[b] - 1] != eot;
+  }
+  __syncthreads();
   if (tid < nc && clive[tid]) {
     int rank = 0;
     for (int c = 0; c < nc; ++c)
       if (clive[c] && (csc[c] > csc[tid] || (csc[c] == csc[tid] && c < tid))) ++rank;
     order[rank] = tid;
   }
-  if (tid == 0) {
-    int nl = 0;
-    for (int c = 0; c < nc; ++c) nl += clive[c];
-    s_saved = nl;  // number of live candidates, replaced below
-  }
   __syncthreads();
   if (tid == 0) {
-    const int nlive = s_saved;
-    int nf = bd->nfin, saved = 0;
-    s_nf0 = nf;
+    int nlive = 0;
+    for (int c = 0; c < nc; ++c) nlive += clive[c];
+    int nf = s_nf0, saved = 0;
     for (int q = 0; q < nlive; ++q) {
-      const int c = order[q];
-      if (ctok[c] == eot) {
-        fsrc[nf] = cbeam[c];
+      const int c = order[q], b = c / (B + 1);
+      if (sti[c] == eot) {
+        fsrc[nf] = b;
         fsc[nf] = csc[c];
         ++nf;
         if (nf >= B) break;
         continue;
       }
       if (saved >= B) continue;
-      psrc[saved] = cbeam[c];
-      ptok[saved] = ctok[c];
+      psrc[saved] = b;
+      ptok[saved] = sti[c];
       plp[saved] = csc[c];
       ++saved;
     }
-    const int done = (nlive == 0 || saved == 0 || nf >= B) ? 1 : 0;
     for (int j = saved; j < B && saved > 0; ++j) {  // leftover beams continue from the first
       psrc[j] = psrc[0];
       ptok[j] = ptok[0];
       plp[j] = plp[0];
     }
     s_nf = nf;
-    s_saved = saved;
-    s_done = done;
+    s_done = (nlive == 0 || saved == 0 || nf >= B) ? 1 : 0;
   }
   __syncthreads();
-  // finished entries of this step: the source beam's tokens (without the end token)
+  // 3. finished entries of this step: the source beam's tokens (without the end token)
   for (int f = s_nf0; f < s_nf; ++f) {
-    const int b = fsrc[f], lb = bd->len[cur][b];
-    for (int q = tid; q < lb; q += 256) bd->fin_toks[f][q] = bd->toks[cur][b][q];
-    if (tid == 0) {
-      bd->fin_len[f] = lb;
+    const int b = fsrc[f];
+    for (int q = tid; q < slen[b]; q += 256) bd->fin_toks[f][q] = stoks[b][q];
+  }
+  if (tid == 0) {
+    for (int f = s_nf0; f < s_nf; ++f) {
+      bd->fin_len[f] = slen[fsrc[f]];
       bd->fin_lp[f] = fsc[f];
     }
+    bd->nfin = s_nf;
   }
   if (s_done) {
     if (tid == 0) {
-      bd->nfin = s_nf;
       bd->done = 1;
       __hip_atomic_store(&ctl->stop, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     return;
   }
-  // new beams
-  for (int j = 0; j < B; ++j) {
-    const int b = psrc[j], lb = bd->len[cur][b];
-    for (int q = tid; q < lb; q += 256) bd->toks[nxt][j][q] = bd->toks[cur][b][q];
-    if (tid == 0) {
-      bd->toks[nxt][j][lb] = ptok[j];
-      bd->len[nxt][j] = lb + 1;
-      bd->lps[j] = plp[j];
-      next_tok[j] = ptok[j];
-    }
+  // 4. new beams
+  for (int e = tid; e < B * (s_maxlen + 1); e += 256) {
+    const int j = e / (s_maxlen + 1), q = e - j * (s_maxlen + 1);
+    const int b = psrc[j], lb = slen[b];
+    if (q < lb) bd->toks[nxt][j][q] = stoks[b][q];
+    else if (q == lb) bd->toks[nxt][j][q] = ptok[j];
   }
-  // slot table: row j continues parent psrc[j] over positions [0, kv)
+  if (tid < B) {
+    bd->len[nxt][tid] = slen[psrc[tid]] + 1;
+    bd->lps[tid] = plp[tid];
+    next_tok[tid] = ptok[tid];
+  }
+  // 5. slot table: row j continues parent psrc[j] over positions [0, kv)
   for (int p0 = 0; p0 < kv; p0 += kSlotChunk) {
     const int np = min(kSlotChunk, kv - p0);
     for (int e = tid; e < B * np; e += 256) {
       const int r = e / np, q = e - r * np;
-      sl[r * kSlotChunk + q] = slots[(size_t)r * max_ctx + p0 + q];
+      dyn[r * kSlotChunk + q] = slots[(size_t)r * max_ctx + p0 + q];
     }
     __syncthreads();
     for (int e = tid; e < B * np; e += 256) {
       const int r = e / np, q = e - r * np;
-      slots[(size_t)r * max_ctx + p0 + q] = sl[psrc[r] * kSlotChunk + q];
+      slots[(size_t)r * max_ctx + p0 + q] = dyn[psrc[r] * kSlotChunk + q];
     }
     __syncthreads();
   }
-  // next step's suppression mask per beam
-  for (int e = tid; e < B * mw; e += 256) mask2[e] = 0u;
+  // 6. next step's suppression mask per beam, built in LDS: suppress list, 3- and 4-gram repeats of
+  //    the new history (a match of the last n-1 tokens at i blocks the token after it), timestamp
+  //    rules (not the first step)
+  uint32_t* msk = reinterpret_cast<uint32_t*>(dyn);
+  for (int e = tid; e < B * mw; e += 256) msk[e] = 0u;
   __syncthreads();
+  auto set = [&](int j, int t) {
+    if (t >= 0 && t < V) atomicOr(msk + (size_t)j * mw + (t >> 5), 1u << (t & 31));
+  };
   for (int j = 0; j < B; ++j) {
-    uint32_t* row = mask2 + (size_t)j * mw;
-    const int* g = bd->toks[nxt][j];
-    const int cnt = bd->len[cur][psrc[j]] + 1;
-    for (int q = tid; q < nsup; q += 256) mask_set(row, V, sup[q]);
-    // n-gram repeats (n = 3, 4): a match of the last n-1 tokens at i blocks the token after it
-    for (int nn = 3; nn <= 4; ++nn) {
+    const int b = psrc[j], cnt = slen[b] + 1;
+    auto g = [&](int q) { return q < cnt - 1 ? stoks[b][q] : ptok[j]; };
+    for (int q = tid; q < nsup; q += 256) set(j, sup[q]);
+    for (int nn = 3; nn <= 4; ++nn)
       for (int i = tid; i <= cnt - nn; i += 256) {
         bool match = true;
-        for (int q = 0; q < nn - 1; ++q) match &= g[i + q] == g[cnt - (nn - 1) + q];
-        if (match) mask_set(row, V, g[i + nn - 1]);
+        for (int q = 0; q < nn - 1; ++q) match &= g(i + q) == g(cnt - (nn - 1) + q);
+        if (match) set(j, g(i + nn - 1));
       }
-    }
-    if (tsb > 0) {  // timestamp rules (not the first step)
-      if (tid == 0) mask_set(row, V, tsb - 1);
-      const bool last_ts = g[cnt - 1] >= tsb;
-      const bool pen_ts = cnt < 2 || g[cnt - 2] >= tsb;
+    if (tsb > 0) {
+      if (tid == 0) set(j, tsb - 1);
+      const bool last_ts = g(cnt - 1) >= tsb;
+      const bool pen_ts = cnt < 2 || g(cnt - 2) >= tsb;
       int lastTs = -1;
       for (int q = cnt - 1; q >= 0; --q)
-        if (g[q] >= tsb) {
-          lastTs = g[q];
+        if (g(q) >= tsb) {
+          lastTs = g(q);
           break;
         }
       int lo1 = 0, hi1 = 0, lo2 = 0, hi2 = 0;
@@ -891,15 +922,13 @@ __global__ __launch_bounds__(256) void k_w_beam(WideCtl* __restrict__ ctl, BeamD
         lo2 = tsb;
         hi2 = (last_ts && !pen_ts) ? lastTs + 1 : lastTs;
       }
-      for (int t = lo1 + tid; t < hi1; t += 256) mask_set(row, V, t);
-      for (int t = lo2 + tid; t < hi2; t += 256) mask_set(row, V, t);
+      for (int t = lo1 + tid; t < hi1; t += 256) set(j, t);
+      for (int t = lo2 + tid; t < hi2; t += 256) set(j, t);
     }
   }
   __syncthreads();
-  if (tid == 0) {
-    bd->nfin = s_nf;
-    bd->cur = nxt;
-  }
+  for (int e = tid; e < B * mw; e += 256) mask2[e] = msk[e];
+  if (tid == 0) bd->cur = nxt;
 }
 
 // Control block of a run (one thread).
@@ -1017,6 +1046,8 @@ static hipError_t prepare_mt() {
 }
 
 hipError_t wide_prepare(int Rp, int wq8) {
+  WCHK(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w_beam), hipFuncAttributeMaxDynamicSharedMemorySize,
+                           (int)beam_lds_bytes(kBeamMax, 4096)));
   if (Rp == 16) return wq8 ? prepare_mt<1, 1>() : prepare_mt<1, 0>();
   return wq8 ? prepare_mt<2, 1>() : prepare_mt<2, 0>();
 }
@@ -1067,7 +1098,8 @@ static hipError_t enqueue_step(const WideParams& p, hipStream_t st) {
   hipLaunchKernelGGL(k_w_selmerge, dim3(p.S), dim3(64), 0, st, p.ctl, p.selp, p.S, p.nsel, p.out, p.next_tok);
   WCHK(hipGetLastError());
   if (p.beam_dev) {
-    hipLaunchKernelGGL(k_w_beam, dim3(1), dim3(256), 0, st, p.ctl, p.beam_dev, p.out, p.S, p.beam_eot, p.beam_tsb, p.beam_sup,
+    hipLaunchKernelGGL(k_w_beam, dim3(1), dim3(256), beam_lds_bytes(p.S, p.mw), st, p.ctl, p.beam_dev, p.out, p.S, p.beam_eot,
+                       p.beam_tsb, p.beam_sup,
                        p.beam_nsup, p.V, p.mw, const_cast<uint32_t*>(p.mask2), const_cast<int32_t*>(p.slots), p.max_ctx, p.next_tok);
     WCHK(hipGetLastError());
   }
