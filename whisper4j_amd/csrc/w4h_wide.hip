@@ -53,7 +53,7 @@ struct GemmArgs {
   const float* act;      // [Rp][lda] fp32 rows (rows >= S read as zero)
   int lda, S;
   float* part;           // [slices][Rp][N] partial sums (rows < S written)
-  const WideCtl* ctl;    // a stopped run (ended beam search) returns at once
+  const WideCtl* ctl;    // a stopped run (ended beam search) stores nothing
 };
 
 // Sum of the ks slices of a GEMM output at p[j * ss + idx]: kSliceBatch loads in flight, added in
@@ -83,7 +83,8 @@ DEV float slice_sum(const float* p, int ks, size_t ss, size_t idx) {
 template <int MT, int WQ8, int KB, int NW>
 __global__ __launch_bounds__(256) void k_w_gemm(GemmArgs a) {
   extern __shared__ __align__(16) uint16_t lds_h[];
-  if (a.ctl->stop) return;
+  // an ended beam search: nothing is stored (the flag is read with the other loads, used at the end)
+  const int stopped = a.ctl->stop;
   constexpr int KW = 4 / NW;
   constexpr int Rp = MT * 16;
   constexpr int CB = 16 * NW;                // columns per workgroup
@@ -205,6 +206,7 @@ __global__ __launch_bounds__(256) void k_w_gemm(GemmArgs a) {
   }
 
   // 5. partial sums of this slice: lane holds rows 4(i/16) + [0, 4) of each 16-row tile, column n
+  if (stopped) return;
   if (kw == 0 && n < N) {
     float* o = a.part + (size_t)blockIdx.y * Rp * N + n;
 #pragma unroll
@@ -231,7 +233,7 @@ __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl
                                                  const float* __restrict__ g, const float* __restrict__ b, float* __restrict__ act,
                                                  int lda) {
   __shared__ float red[8];
-  if (ctl->stop) return;
+  const int stopped = ctl->stop;  // ended beam search: read with the other loads, checked before storing
   const int s = blockIdx.x, tid = threadIdx.x;
   float v[kWideVec];
   if (EMB) {
@@ -250,7 +252,6 @@ __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl
         if (!WQ8) e = h2f(static_cast<const uint16_t*>(emb)[(size_t)tk * d + j]);
         else e = (float)static_cast<const int8_t*>(emb)[(size_t)tk * d + j] * h2f(emb_s[(size_t)tk * (d >> 5) + (j >> 5)]);
         v[i] = e + pos[(size_t)pe * d + j];
-        x[(size_t)s * d + j] = v[i];
       }
     }
   } else {
@@ -276,12 +277,13 @@ __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl
     for (int i = 0; i < kWideVec; ++i) {
       const int j = tid + 256 * i;
       v[i] = 0.f;
-      if (j < d) {
-        v[i] = x[(size_t)s * d + j] + (bias[j] + acc[i]);
-        x[(size_t)s * d + j] = v[i];
-      }
+      if (j < d) v[i] = x[(size_t)s * d + j] + (bias[j] + acc[i]);
     }
   }
+  if (stopped) return;
+#pragma unroll
+  for (int i = 0; i < kWideVec; ++i)
+    if (tid + 256 * i < d) x[(size_t)s * d + tid + 256 * i] = v[i];
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < kWideVec; ++i) sum += v[i];
@@ -307,11 +309,12 @@ __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl
 // act[r][k] = GELU(bias[k] + the slices of the MLP1 GEMM), r < S, k < n.
 __global__ __launch_bounds__(256) void k_w_gelu(const WideCtl* __restrict__ ctl, const float* __restrict__ P, int ks, size_t ss,
                                                 const float* __restrict__ bias, int S, int n, float* __restrict__ act, int lda) {
-  if (ctl->stop) return;
+  const int stopped = ctl->stop;
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= S * n) return;
   const int r = i / n, k = i - r * n;
-  act[(size_t)r * lda + k] = gelu_f16(bias[k] + slice_sum(P, ks, ss, (size_t)r * n + k));
+  const float v = gelu_f16(bias[k] + slice_sum(P, ks, ss, (size_t)r * n + k));
+  if (!stopped) act[(size_t)r * lda + k] = v;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -494,7 +497,7 @@ __global__ __launch_bounds__(256) void k_w_cross(const WideCtl* __restrict__ ctl
                                                  float* __restrict__ act, int lda) {
   extern __shared__ float scs[];  // [RG][chlen]
   __shared__ float q[RG * 64], red[4 * RG * 64], rm[RG], rl[RG];
-  if (ctl->stop) return;
+  const int stopped = ctl->stop;  // checked before the stores
   const int e = blockIdx.x, h = blockIdx.y, c = blockIdx.z % nch, rg = blockIdx.z / nch;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   int r0, nr;
@@ -621,6 +624,7 @@ __global__ __launch_bounds__(256) void k_w_cross(const WideCtl* __restrict__ ctl
     }
   }
   __syncthreads();
+  if (stopped) return;
   for (int i = tid; i < nr * 64; i += 256) {
     const int r = i >> 6, k = i & 63;
     const float v = red[(0 * RG + r) * 64 + k] + red[(1 * RG + r) * 64 + k] + red[(2 * RG + r) * 64 + k] +
@@ -643,7 +647,7 @@ __global__ __launch_bounds__(256) void k_w_cross(const WideCtl* __restrict__ ctl
 // with eight loads in flight.
 __global__ __launch_bounds__(64) void k_w_cmerge(const WideCtl* __restrict__ ctl, const float* __restrict__ cpart, int H, int nch,
                                                   float* __restrict__ act, int lda) {
-  if (ctl->stop) return;
+  const int stopped = ctl->stop;  // checked before the store
   const int s = blockIdx.x, h = blockIdx.y, k = threadIdx.x;
   const float* p = cpart + ((size_t)s * H + h) * nch * kPartWords;
   const float mc = k < nch ? p[k * kPartWords] : -INFINITY;
@@ -659,7 +663,7 @@ __global__ __launch_bounds__(64) void k_w_cmerge(const WideCtl* __restrict__ ctl
 #pragma unroll
     for (int u = 0; u < 8; ++u) o = fmaf(__shfl(f, c0 + u), t[u], o);
   }
-  act[(size_t)s * lda + h * kHeadDim + k] = o / Lsum;
+  if (!stopped) act[(size_t)s * lda + h * kHeadDim + k] = o / Lsum;
 }
 
 // ------------------------------------------------------------------------------------------------
