@@ -176,8 +176,9 @@ def measure_forced(w4h, synth, name, wtype, n_steps, repeats, n_rows=1, n_encode
 
 
 def measure_beam(w4h, synth, name, n_steps, beam):
-    """Beam search through the library's beam driver (device step + host candidate bookkeeping and KV
-    reorder per step); EOT is suppressed so every hypothesis runs all steps."""
+    """Beam search through the library's beam driver (w4h_decode_beam: the prompt prefill, then for a
+    batched session candidate scoring, sorting, finished list, masks and KV reorder on the device in
+    32-step launches); EOT is suppressed so every hypothesis runs all steps."""
     from whisper4j_amd.decoder import WhisperDecoder
 
     dims = synth.SHAPES[name]
@@ -204,7 +205,7 @@ def other_configs(w4h, synth):
     out["tiny.en greedy b=1, 224 forced steps"] = {"tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
                                                    "roofline_frac": round(frac, 4)}
     sps, hps, us, steps = measure_beam(w4h, synth, "small", 224, 5)
-    out["small beam 5, 224 steps (library beam driver: device step + host candidate sort + KV reorder; EOT suppressed)"] = {
+    out["small beam 5, 224 steps (library beam driver w4h_decode_beam: prompt prefill, then the search on the device; EOT suppressed)"] = {
         "steps_per_s": round(sps, 1), "hypothesis_tokens_per_s": round(hps, 1), "us_per_step": round(us, 2),
         "steps": steps}
     tps, us, frac = measure_forced(w4h, synth, "small", "f16", 224, 2, n_rows=5, n_encoders=1)
