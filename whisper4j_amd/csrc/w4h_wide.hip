@@ -224,7 +224,9 @@ __global__ __launch_bounds__(256) void k_w_gemm(GemmArgs a) {
 
 constexpr int kWideVec = 8;  // d <= 8 * 256
 
-template <int WQ8, int EMB>
+// NV = ceil(d / 256) elements per thread (template, so no dead element slots).  The residual row
+// is loaded first, then every slice of every element at once with clamped (branch-free) addresses.
+template <int WQ8, int EMB, int NV>
 __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl, const int32_t* __restrict__ tokens0,
                                                  const int32_t* __restrict__ forced, const int32_t* __restrict__ next_tok, int S, int C,
                                                  const void* __restrict__ emb, const uint16_t* __restrict__ emb_s,
@@ -235,7 +237,7 @@ __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl
   __shared__ float red[8];
   const int stopped = ctl->stop;  // ended beam search: read with the other loads, checked before storing
   const int s = blockIdx.x, tid = threadIdx.x;
-  float v[kWideVec];
+  float v[NV];
   if (EMB) {
     // token of this step: the run's first tokens, the forced row, or the last step's argmax;
     // positional row clamped as the reference
@@ -244,63 +246,63 @@ __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl
     const int tk = (i0 == 0 && !ctl->tok_dev) ? tokens0[s]
                                               : (ctl->forced_on ? forced[(size_t)(i0 - 1) * S + s] : next_tok[s]);
 #pragma unroll
-    for (int i = 0; i < kWideVec; ++i) {
-      const int j = tid + 256 * i;
-      v[i] = 0.f;
-      if (j < d) {
-        float e;
-        if (!WQ8) e = h2f(static_cast<const uint16_t*>(emb)[(size_t)tk * d + j]);
-        else e = (float)static_cast<const int8_t*>(emb)[(size_t)tk * d + j] * h2f(emb_s[(size_t)tk * (d >> 5) + (j >> 5)]);
-        v[i] = e + pos[(size_t)pe * d + j];
-      }
+    for (int i = 0; i < NV; ++i) {
+      const int j = min(tid + 256 * i, d - 1);
+      float e;
+      if (!WQ8) e = h2f(static_cast<const uint16_t*>(emb)[(size_t)tk * d + j]);
+      else e = (float)static_cast<const int8_t*>(emb)[(size_t)tk * d + j] * h2f(emb_s[(size_t)tk * (d >> 5) + (j >> 5)]);
+      v[i] = tid + 256 * i < d ? e + pos[(size_t)pe * d + j] : 0.f;
     }
   } else {
-    // slices added in slice order; every slice (kWideMaxSlices) of every element in flight at once
-    float acc[kWideVec];
+    float xr[NV], bs[NV];
 #pragma unroll
-    for (int i = 0; i < kWideVec; ++i) acc[i] = 0.f;
+    for (int i = 0; i < NV; ++i) {
+      const int j = min(tid + 256 * i, d - 1);
+      xr[i] = x[(size_t)s * d + j];
+      bs[i] = bias[j];
+    }
+    // slices added in slice order; kWideMaxSlices of every element in flight at once
+    float acc[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) acc[i] = 0.f;
     for (int z = 0; z < ks; z += kWideMaxSlices) {
-      float t[kWideVec][kWideMaxSlices];
+      float t[NV][kWideMaxSlices];
 #pragma unroll
-      for (int i = 0; i < kWideVec; ++i)
+      for (int i = 0; i < NV; ++i)
 #pragma unroll
         for (int u = 0; u < kWideMaxSlices; ++u) {
-          const int j = tid + 256 * i;
-          t[i][u] = (j < d && z + u < ks) ? P[(size_t)(z + u) * ss + (size_t)s * d + j] : 0.f;
+          const int j = min(tid + 256 * i, d - 1), zz = min(z + u, ks - 1);
+          t[i][u] = P[(size_t)zz * ss + (size_t)s * d + j];
         }
 #pragma unroll
-      for (int i = 0; i < kWideVec; ++i)
+      for (int i = 0; i < NV; ++i)
 #pragma unroll
-        for (int u = 0; u < kWideMaxSlices; ++u) acc[i] += t[i][u];
+        for (int u = 0; u < kWideMaxSlices; ++u) acc[i] += z + u < ks ? t[i][u] : 0.f;
     }
 #pragma unroll
-    for (int i = 0; i < kWideVec; ++i) {
-      const int j = tid + 256 * i;
-      v[i] = 0.f;
-      if (j < d) v[i] = x[(size_t)s * d + j] + (bias[j] + acc[i]);
-    }
+    for (int i = 0; i < NV; ++i) v[i] = tid + 256 * i < d ? xr[i] + (bs[i] + acc[i]) : 0.f;
   }
   if (stopped) return;
 #pragma unroll
-  for (int i = 0; i < kWideVec; ++i)
+  for (int i = 0; i < NV; ++i)
     if (tid + 256 * i < d) x[(size_t)s * d + tid + 256 * i] = v[i];
   float sum = 0.f;
 #pragma unroll
-  for (int i = 0; i < kWideVec; ++i) sum += v[i];
+  for (int i = 0; i < NV; ++i) sum += v[i];
   sum = wave_sum(sum);
   if ((tid & 63) == 0) red[tid >> 6] = sum;
   __syncthreads();
   const float mean = (red[0] + red[1] + red[2] + red[3]) / (float)d;
   float q = 0.f;
 #pragma unroll
-  for (int i = 0; i < kWideVec; ++i)
+  for (int i = 0; i < NV; ++i)
     if (tid + 256 * i < d) q = fmaf(v[i] - mean, v[i] - mean, q);
   q = wave_sum(q);
   if ((tid & 63) == 0) red[4 + (tid >> 6)] = q;
   __syncthreads();
   const float inv = 1.0f / sqrtf((red[4] + red[5] + red[6] + red[7]) / (float)d + 1e-5f);
 #pragma unroll
-  for (int i = 0; i < kWideVec; ++i) {
+  for (int i = 0; i < NV; ++i) {
     const int j = tid + 256 * i;
     if (j < d) act[(size_t)s * lda + j] = (v[i] - mean) * inv * g[j] + b[j];
   }
@@ -1010,29 +1012,39 @@ static hipError_t gemm(const WideParams& p, const WideGemm& g, const void* w, co
 
 static size_t sstride(const WideParams& p, const WideGemm& g) { return (size_t)p.Rp * g.N; }
 
+template <int WQ8, int NV>
+static hipError_t resid_nv(const WideParams& p, bool emb, int ks, size_t ss, const float* bias, const float* lg, const float* lb,
+                           hipStream_t st) {
+  const int lda = 4 * p.d;
+  const dim3 grid(p.S), blk(256);
+  if (emb)
+    hipLaunchKernelGGL((k_w_resid<WQ8, 1, NV>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos,
+                       p.part, ks, ss, bias, p.x, p.d, lg, lb, p.act, lda);
+  else
+    hipLaunchKernelGGL((k_w_resid<WQ8, 0, NV>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos,
+                       p.part, ks, ss, bias, p.x, p.d, lg, lb, p.act, lda);
+  return hipGetLastError();
+}
+
+template <int WQ8>
+static hipError_t resid_wq(const WideParams& p, bool emb, int ks, size_t ss, const float* bias, const float* lg, const float* lb,
+                           hipStream_t st) {
+  switch ((p.d + 255) / 256) {
+    case 1:
+    case 2: return resid_nv<WQ8, 2>(p, emb, ks, ss, bias, lg, lb, st);
+    case 3: return resid_nv<WQ8, 3>(p, emb, ks, ss, bias, lg, lb, st);
+    case 4: return resid_nv<WQ8, 4>(p, emb, ks, ss, bias, lg, lb, st);
+    case 5: return resid_nv<WQ8, 5>(p, emb, ks, ss, bias, lg, lb, st);
+    default: return resid_nv<WQ8, kWideVec>(p, emb, ks, ss, bias, lg, lb, st);
+  }
+}
+
 // Residual update (or layer-0 embedding when g_prev is null) + LayerNorm (lg, lb) -> act.
 static hipError_t resid(const WideParams& p, const WideGemm* g_prev, const float* bias, const float* lg, const float* lb,
                         hipStream_t st) {
-  const int lda = 4 * p.d;
-  const dim3 grid(p.S), blk(256);
   const int ks = g_prev ? g_prev->ks : 0;
   const size_t ss = g_prev ? sstride(p, *g_prev) : 0;
-  if (p.wq8) {
-    if (!g_prev)
-      hipLaunchKernelGGL((k_w_resid<1, 1>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos,
-                         p.part, ks, ss, bias, p.x, p.d, lg, lb, p.act, lda);
-    else
-      hipLaunchKernelGGL((k_w_resid<1, 0>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos,
-                         p.part, ks, ss, bias, p.x, p.d, lg, lb, p.act, lda);
-  } else {
-    if (!g_prev)
-      hipLaunchKernelGGL((k_w_resid<0, 1>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos,
-                         p.part, ks, ss, bias, p.x, p.d, lg, lb, p.act, lda);
-    else
-      hipLaunchKernelGGL((k_w_resid<0, 0>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos,
-                         p.part, ks, ss, bias, p.x, p.d, lg, lb, p.act, lda);
-  }
-  return hipGetLastError();
+  return p.wq8 ? resid_wq<1>(p, !g_prev, ks, ss, bias, lg, lb, st) : resid_wq<0>(p, !g_prev, ks, ss, bias, lg, lb, st);
 }
 
 #define WCHK(x)                          \
