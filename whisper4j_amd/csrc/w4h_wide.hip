@@ -27,7 +27,6 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPadH = 8;  // halves of padding per LDS activation row (16 bytes: spreads banks)
-constexpr int kSliceBatch = 4;  // slices whose partials a reducing thread loads at once
 
 DEV half8 as_half8(uint4 u) {
   half8 h;
@@ -56,16 +55,17 @@ struct GemmArgs {
   const WideCtl* ctl;    // a stopped run (ended beam search) stores nothing
 };
 
-// Sum of the ks slices of a GEMM output at p[j * ss + idx]: kSliceBatch loads in flight, added in
-// slice order.
+// Sum of the ks slices of a GEMM output at p[j * ss + idx], added in slice order: four slices' loads
+// in flight at a time, with clamped (branch-free) addresses.
+constexpr int kSliceBatch = 4;
 DEV float slice_sum(const float* p, int ks, size_t ss, size_t idx) {
   float v = 0.f;
   for (int j = 0; j < ks; j += kSliceBatch) {
     float t[kSliceBatch];
 #pragma unroll
-    for (int u = 0; u < kSliceBatch; ++u) t[u] = j + u < ks ? p[(size_t)(j + u) * ss + idx] : 0.f;
+    for (int u = 0; u < kSliceBatch; ++u) t[u] = p[(size_t)min(j + u, ks - 1) * ss + idx];
 #pragma unroll
-    for (int u = 0; u < kSliceBatch; ++u) v += t[u];
+    for (int u = 0; u < kSliceBatch; ++u) v += j + u < ks ? t[u] : 0.f;
   }
   return v;
 }
