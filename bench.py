@@ -7,7 +7,8 @@ encoder output, prompt [50257, 50258, 50359, 50363], then 444 teacher-forced sin
 
 A bench "step" is one such 444-token decode sweep over device-resident weights, cross-attention
 K/V and a self-KV cache holding the prefilled 4-token prompt; each sweep rewinds the KV to the
-prompt.  Prefill and the cross-K/V projection are outside the timed region.  Every token step is
+prompt.  Prefill and the cross-K/V projection are outside the timed region and reported under
+"setup" (wall clock, encoder output already in device memory).  Every token step is
 a real single-token decoder step (the next token could be the previous argmax; the teacher-forced
 id is read from device memory instead).  The whole sweep is one launch of the persistent step
 kernel, timed with HIP events on the session stream.
@@ -136,23 +137,65 @@ def traffic_from(fetch_csv, write_csv, copy_mib, out_path):
     print(open(out_path).read())
 
 
+def measure_setup(sess, dims, xas, n_rows, prompt, repeats=3):
+    """Per-utterance set-up outside the timed decode steps, with the encoder outputs already in device
+    memory: the cross-attention K/V projection of every layer for every encoder (MFMA GEMMs through
+    w4h_session_set_encoder_device, one call and synchronisation per encoder), then the 4-token prompt
+    prefill (one run call).  Wall clock, median of `repeats` after an untimed first call; leaves the
+    session holding the prefilled prompt."""
+    from whisper4j_amd.device import DeviceArray
+
+    dev = [DeviceArray(np.asarray(x, dtype=np.float32)) for x in xas]
+
+    def project():
+        for e, x in enumerate(dev):
+            sess.set_encoder_device(x.address, enc=e)
+
+    project()
+    proj = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        project()
+        proj.append(time.perf_counter() - t0)
+    first = [prompt[0]] * n_rows
+    rest = [[t] * n_rows for t in prompt[1:]]
+    pre = []
+    for _ in range(repeats + 1):
+        sess.reset(0)
+        t0 = time.perf_counter()
+        sess.run(first, forced=rest, n_steps=len(prompt))
+        pre.append(time.perf_counter() - t0)
+    for x in dev:
+        x.close()
+    L, d, A = dims.n_text_layer, dims.n_text_state, dims.n_audio_ctx
+    flop = 2 * 2 * L * A * d * d * len(xas)
+    p = float(np.median(proj))
+    return {"cross_kv_ms": round(p * 1e3, 4), "cross_kv_gflop": round(flop / 1e9, 2),
+            "cross_kv_tflop_s": round(flop / p / 1e12, 1), "prefill_ms": round(float(np.median(pre[1:])) * 1e3, 4)}
+
+
 def measure_forced(w4h, synth, name, wtype, n_steps, repeats, n_rows=1, n_encoders=1, n_sessions=1):
     """Teacher-forced decode of one config: 4-token prefix prefilled untimed, then `n_steps` steps in
     one launch per session and repeat; returns (tokens/s over all rows and sessions, us per step,
-    roofline fraction of the mean step)."""
+    roofline fraction of the mean step, set-up costs of the first session)."""
     dims = synth.SHAPES[name]
     T = synth.make_decoder(dims, seed=0, wtype=wtype)
     model = w4h.Model.from_tensors(dims, T)
     prompt = list(synth.BENCH_PREFIX)
     forced = synth.forced_tokens(n_steps, 0)
     sessions = []
+    setup = None
     for q in range(n_sessions):
         sess = model.session(n_rows=n_rows, n_encoders=n_encoders, max_ctx=dims.n_text_ctx)
-        for e in range(n_encoders):
-            sess.set_encoder(synth.encoder_output(dims, 0, stream=q * n_encoders + e), enc=e)
-        first = [prompt[0]] * n_rows
-        rest = [[t] * n_rows for t in prompt[1:]]
-        sess.run(first, forced=rest, n_steps=len(prompt))
+        xas = [synth.encoder_output(dims, 0, stream=q * n_encoders + e) for e in range(n_encoders)]
+        if q == 0:
+            setup = measure_setup(sess, dims, xas, n_rows, prompt)
+        else:
+            for e in range(n_encoders):
+                sess.set_encoder(xas[e], enc=e)
+            first = [prompt[0]] * n_rows
+            rest = [[t] * n_rows for t in prompt[1:]]
+            sess.run(first, forced=rest, n_steps=len(prompt))
         sessions.append(sess)
     kv0 = sessions[0].kv_len
     tok0 = [int(forced[0])] * n_rows
@@ -172,7 +215,7 @@ def measure_forced(w4h, synth, name, wtype, n_steps, repeats, n_rows=1, n_encode
     encs = n_encoders * n_sessions
     byts = sum(algorithmic_bytes_per_step(dims, kv0 + i, rows=rows, encoders=encs, w_b=w_b) for i in range(n_steps))
     frac = byts / (total_ms * 1e-3) / 1e9 / HBM_PEAK_GBS
-    return rows * n_steps / (total_ms * 1e-3), step_us, frac
+    return rows * n_steps / (total_ms * 1e-3), step_us, frac, setup
 
 
 def measure_beam(w4h, synth, name, n_steps, beam):
@@ -201,23 +244,23 @@ def measure_beam(w4h, synth, name, n_steps, beam):
 def other_configs(w4h, synth):
     """Absolute decode rates of the four other workload shapes (one bounded run each)."""
     out = {}
-    tps, us, frac = measure_forced(w4h, synth, "tiny.en", "f16", 224, 5)
+    tps, us, frac, setup = measure_forced(w4h, synth, "tiny.en", "f16", 224, 5)
     out["tiny.en greedy b=1, 224 forced steps"] = {"tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
-                                                   "roofline_frac": round(frac, 4)}
+                                                   "roofline_frac": round(frac, 4), "setup": setup}
     sps, hps, us, steps = measure_beam(w4h, synth, "small", 224, 5)
     out["small beam 5, 224 steps (library beam driver w4h_decode_beam: prompt prefill, then the search on the device; EOT suppressed)"] = {
         "steps_per_s": round(sps, 1), "hypothesis_tokens_per_s": round(hps, 1), "us_per_step": round(us, 2),
         "steps": steps}
-    tps, us, frac = measure_forced(w4h, synth, "small", "f16", 224, 2, n_rows=5, n_encoders=1)
+    tps, us, frac, setup = measure_forced(w4h, synth, "small", "f16", 224, 2, n_rows=5, n_encoders=1)
     out["small 5 beam rows on one encoder, 224 forced steps in one run (device step only)"] = {
         "steps_per_s": round(1e6 / us, 1), "hypothesis_tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
-        "roofline_frac": round(frac, 4)}
-    tps, us, frac = measure_forced(w4h, synth, "large-v3-turbo", "f16", 224, 2, n_rows=32, n_encoders=32)
+        "roofline_frac": round(frac, 4), "setup": setup}
+    tps, us, frac, setup = measure_forced(w4h, synth, "large-v3-turbo", "f16", 224, 2, n_rows=32, n_encoders=32)
     out["large-v3-turbo 32 streams (own encoder each) in lockstep, 224 forced steps (batched MFMA engine)"] = {
-        "tokens_per_s": round(tps, 1), "us_per_step": round(us, 2), "roofline_frac": round(frac, 4)}
-    tps, us, frac = measure_forced(w4h, synth, "medium", "q8_0", 444, 2)
+        "tokens_per_s": round(tps, 1), "us_per_step": round(us, 2), "roofline_frac": round(frac, 4), "setup": setup}
+    tps, us, frac, setup = measure_forced(w4h, synth, "medium", "q8_0", 444, 2)
     out["medium q8_0 greedy b=1, 444 forced steps"] = {"tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
-                                                      "roofline_frac": round(frac, 4)}
+                                                      "roofline_frac": round(frac, 4), "setup": setup}
     return out
 
 
@@ -252,15 +295,15 @@ def main():
     if args.only:
         n = args.only_steps
         if args.only == "turbo":
-            tps, us, frac = measure_forced(w4h, synth, "large-v3-turbo", "f16", n, 2, n_rows=32, n_encoders=32)
+            tps, us, frac, setup = measure_forced(w4h, synth, "large-v3-turbo", "f16", n, 2, n_rows=32, n_encoders=32)
             work = f"large-v3-turbo 32 streams (own encoder each) in lockstep, {n} forced steps"
         else:
-            tps, us, frac = measure_forced(w4h, synth, "small", "f16", n, 2, n_rows=5, n_encoders=1)
+            tps, us, frac, setup = measure_forced(w4h, synth, "small", "f16", n, 2, n_rows=5, n_encoders=1)
             work = f"small 5 beam rows on one encoder, {n} forced steps"
         if args.copy_mib:
             copy_calibration(args.copy_mib)
         print(json.dumps({"workload": work, "tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
-                          "roofline_frac": round(frac, 4)}))
+                          "roofline_frac": round(frac, 4), "setup": setup}))
         return
 
     dims = synth.SHAPES["base.en"]
@@ -271,8 +314,7 @@ def main():
 
     model = w4h.Model.from_tensors(dims, T)
     sess = model.session(n_rows=1, max_ctx=dims.n_text_ctx)
-    sess.set_encoder(xa)
-    sess.run([prompt[0]], forced=prompt[1:], n_steps=len(prompt))  # prefill (untimed)
+    setup = measure_setup(sess, dims, [xa], 1, prompt)  # cross K/V + prefill, outside the timed sweeps
     kv0 = sess.kv_len
     # sweep: forced[i] at position 4 + i for i < 444 (kv_len 4 -> 448)
     tok0 = [int(forced[0])]
@@ -326,6 +368,7 @@ def main():
                      "kernel": "w4h::k_step<1,0> (persistent decoder step, whole sweep per launch)",
                      "algorithmic_bytes_per_launch": int(bytes_launch)},
         "cpu_baseline": cpu,
+        "setup": setup,
         "other_configs": configs,
     }
     print(json.dumps(line))

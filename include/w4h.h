@@ -120,6 +120,11 @@ int w4h_session_destroy(w4h_session* s);
  * cross-attention K/V of every layer on the device (MultiHeadAttention.forward, cross branch,
  * main/nn/MultiHeadAttention.java:65-75). */
 int w4h_session_set_encoder(w4h_session* s, int32_t enc, const float* xa);
+/* The same with xa [n_audio_ctx][n_text_state] fp32 already in memory of the session's device (an
+ * encoder that ran on the GPU): no host copy.  The projection is ordered only after earlier work on
+ * the session's own stream, so the producer of xa must have finished writing it.  Returns when the
+ * K/V are ready; xa may then be reused.  Replaces the same call site as w4h_session_set_encoder. */
+int w4h_session_set_encoder_device(w4h_session* s, int32_t enc, const float* xa_device);
 /* Rewind the self-KV of every row to kv_len positions (0 = empty, as a fresh decode call). */
 int w4h_session_reset(w4h_session* s, int32_t kv_len);
 int w4h_session_kv_len(const w4h_session* s, int32_t* kv_len);

@@ -239,3 +239,45 @@ def test_session_errors(gpu):
     assert rc == _lib.W4H_ERR_CLOSED
     assert s2.step([3])[0].argmax >= 0
     s2.close()
+
+
+@pytest.mark.parametrize("wtype,frames", [("f16", 300), ("q8_0", 300), ("f16", 129)])
+def test_cross_kv_projection_frame_tiles(gpu, orc, wtype, frames):
+    """The cross-attention K/V projection (MFMA GEMM, 128 encoder frames per workgroup) over several
+    frame tiles with a partial last one: forced-decode logits within 1e-2 of the oracle; the
+    device-memory entry point gives logits bit-identical to the host-memory one and refuses a host
+    pointer."""
+    from whisper4j_amd.device import DeviceArray
+
+    dims = synth.Dims(n_vocab=800, n_text_ctx=32, n_text_state=256, n_text_head=4, n_text_layer=2,
+                      n_audio_ctx=frames)
+    say(f"cross K/V projection: {frames} frames, {wtype}")
+    T = make(dims, 51, wtype=wtype)
+    xa = synth.encoder_output(dims, 51)
+    prompt, forced = [1, 2, 3], synth.forced_tokens(8, 51, high=dims.n_vocab - 1)
+    ref = orc.Model(dims, T).forced(xa, prompt, forced, want_logits=True)
+    m = gpu.Model.from_tensors(dims, T)
+    out = {}
+    for how in ("host", "device"):
+        s = m.session()
+        if how == "host":
+            s.set_encoder(xa)
+        else:
+            xd = DeviceArray(np.asarray(xa, dtype=np.float32))
+            s.set_encoder_device(xd.address)
+            xd.close()
+            with pytest.raises(gpu.W4HError) as e:
+                s.set_encoder_device(xa.ctypes.data)
+            assert e.value.code == -1
+        lgs = []
+        for i, tok in enumerate(prompt + list(forced)):
+            _, lg = s.step([tok], want_logits=True)
+            if i >= len(prompt) - 1:
+                lgs.append(lg[0].copy())
+        out[how] = np.array(lgs)
+        s.close()
+    m.close()
+    worst = float(np.abs(out["host"] - ref["logits"][:len(out["host"])]).max())
+    say("max-abs", worst)
+    assert worst <= TOL
+    np.testing.assert_array_equal(out["host"], out["device"])

@@ -30,7 +30,7 @@ TYPE_F32, TYPE_F16, TYPE_Q8_0 = 0, 1, 8
 EXPORTS = (
     "w4h_last_error", "w4h_device_count", "w4h_model_create", "w4h_model_load_ggml", "w4h_model_dims",
     "w4h_model_destroy", "w4h_ggml_inspect", "w4h_ggml_read_tensor", "w4h_session_create", "w4h_session_destroy",
-    "w4h_session_set_encoder", "w4h_session_reset", "w4h_session_kv_len", "w4h_session_set_suppress",
+    "w4h_session_set_encoder", "w4h_session_set_encoder_device", "w4h_session_reset", "w4h_session_kv_len", "w4h_session_set_suppress",
     "w4h_session_set_probe", "w4h_session_step", "w4h_session_run", "w4h_session_reorder", "w4h_session_time_run",
     "w4h_session_trace_run",
     "w4h_decode", "w4h_decode_beam", "w4h_decode_with_fallback", "w4h_compression_ratio", "w4h_op_linear",
@@ -103,6 +103,7 @@ def lib():
         "w4h_session_create": (i32, [vp, ctypes.POINTER(SessionDesc), ctypes.POINTER(vp)]),
         "w4h_session_destroy": (i32, [vp]),
         "w4h_session_set_encoder": (i32, [vp, i32, f32p]),
+        "w4h_session_set_encoder_device": (i32, [vp, i32, vp]),
         "w4h_session_reset": (i32, [vp, i32]),
         "w4h_session_kv_len": (i32, [vp, i32p]),
         "w4h_session_set_suppress": (i32, [vp, i32p, i32]),

@@ -888,6 +888,15 @@ int w4h_session_destroy(w4h_session* s) {
   return W4H_OK;
 }
 
+static int project_encoder(w4h_session* s, int32_t enc, const float* xa_dev) {
+  const w4h_dims& D = s->m->dims;
+  const size_t off = (size_t)enc * D.n_text_layer * D.n_text_head * D.n_audio_ctx * kHeadDim;
+  HIPCHK(launch_cross_kv(s->m->layers_dev.as<LayerDev>(), D.n_text_layer, D.n_text_state, D.n_text_head, D.n_audio_ctx,
+                         s->m->wq8, xa_dev, s->xk.as<uint16_t>() + off, s->xv.as<uint16_t>() + off, s->stream));
+  HIPCHK(hipStreamSynchronize(s->stream));
+  return W4H_OK;
+}
+
 int w4h_session_set_encoder(w4h_session* s, int32_t enc, const float* xa) {
   if (!s || !xa) return fail(W4H_ERR_INVALID, "null argument");
   if (enc < 0 || enc >= s->X) return fail(W4H_ERR_INVALID, "encoder %d outside [0, %d)", enc, s->X);
@@ -897,11 +906,21 @@ int w4h_session_set_encoder(w4h_session* s, int32_t enc, const float* xa) {
   int rc = ensure(s->xa_tmp, n * sizeof(float));
   if (rc) return rc;
   HIPCHK(hipMemcpyAsync(s->xa_tmp.p, xa, n * sizeof(float), hipMemcpyHostToDevice, s->stream));
-  const size_t off = (size_t)enc * D.n_text_layer * D.n_text_head * D.n_audio_ctx * kHeadDim;
-  HIPCHK(launch_cross_kv(s->m->layers_dev.as<LayerDev>(), D.n_text_layer, D.n_text_state, D.n_text_head, D.n_audio_ctx,
-                         s->m->wq8, s->xa_tmp.as<float>(), s->xk.as<uint16_t>() + off, s->xv.as<uint16_t>() + off, s->stream));
-  HIPCHK(hipStreamSynchronize(s->stream));
-  return W4H_OK;
+  return project_encoder(s, enc, s->xa_tmp.as<float>());
+}
+
+int w4h_session_set_encoder_device(w4h_session* s, int32_t enc, const float* xa_device) {
+  if (!s || !xa_device) return fail(W4H_ERR_INVALID, "null argument");
+  if (enc < 0 || enc >= s->X) return fail(W4H_ERR_INVALID, "encoder %d outside [0, %d)", enc, s->X);
+  HIPCHK(hipSetDevice(s->m->device));
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, xa_device) != hipSuccess || attr.type != hipMemoryTypeDevice ||
+      attr.device != s->m->device) {
+    (void)hipGetLastError();
+    return fail(W4H_ERR_INVALID, "xa_device is not device memory of device %d", s->m->device);
+  }
+  if (reinterpret_cast<uintptr_t>(xa_device) % 16 != 0) return fail(W4H_ERR_INVALID, "xa_device is not 16-byte aligned");
+  return project_encoder(s, enc, xa_device);
 }
 
 int w4h_session_reset(w4h_session* s, int32_t kv_len) {

@@ -1,70 +1,9 @@
-// Device code of whisper4j_amd for gfx950 outside the step kernel: the cross-attention K/V
-// projection, the op kernels behind the kernel-level entry points, and the launchers.
+// Device code of whisper4j_amd for gfx950 outside the step kernels: the op kernels behind the
+// kernel-level entry points and their launchers.
 
 #include "w4h_kernels.h"
 
 namespace w4h {
-
-// ------------------------------------------------------------------------------------------------
-// Cross-attention K/V projection: out[h][t][e] = f16(sum_k xa[t][k] * W[h*64+e][k] (+ b)), per layer.
-// 64x64 output tiles, k-tiles of 32, 4x4 outputs per thread (fp32 FMA).
-
-template <int WQ8>
-__global__ void __launch_bounds__(kThreads) k_cross_kv(const LayerDev* layers, int d, int H, int A, const float* xa,
-                                                      uint16_t* xk, uint16_t* xv) {
-  __shared__ float As[32][64 + 4];  // [k][t]
-  __shared__ float Bs[32][64 + 4];  // [k][n]
-  const int t0 = blockIdx.x * 64, n0 = blockIdx.y * 64;
-  const int l = blockIdx.z >> 1, isv = blockIdx.z & 1;
-  const LayerDev& lw = layers[l];
-  const void* W = isv ? lw.w_cv : lw.w_ck;
-  const uint16_t* Ws = isv ? lw.s_cv : lw.s_ck;
-  const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
-  float acc[4][4] = {};
-  for (int k0 = 0; k0 < d; k0 += 32) {
-    for (int i = tid; i < 64 * 32; i += kThreads) {
-      const int r = i >> 5, kk = i & 31;
-      const int t = t0 + r;
-      As[kk][r] = t < A ? xa[(size_t)t * d + k0 + kk] : 0.f;
-      const int n = n0 + r;
-      float wv;
-      if (!WQ8) {
-        wv = h2f(static_cast<const uint16_t*>(W)[(size_t)n * d + k0 + kk]);
-      } else {
-        wv = (float)static_cast<const int8_t*>(W)[(size_t)n * d + k0 + kk] * h2f(Ws[(size_t)n * (d >> 5) + ((k0 + kk) >> 5)]);
-      }
-      Bs[kk][r] = wv;
-    }
-    lds_barrier();
-#pragma unroll 8
-    for (int kk = 0; kk < 32; ++kk) {
-      float a[4], b[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[i] = As[kk][ty * 4 + i];
-        b[i] = Bs[kk][tx * 4 + i];
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
-    }
-    lds_barrier();
-  }
-  uint16_t* out = (isv ? xv : xk) + (size_t)l * H * A * kHeadDim;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = t0 + ty * 4 + i;
-    if (t >= A) continue;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + tx * 4 + j;
-      float v = acc[i][j];
-      if (isv && lw.b_cv) v += lw.b_cv[n];
-      out[((size_t)(n >> 6) * A + t) * kHeadDim + (n & 63)] = f2h(v);
-    }
-  }
-}
 
 __global__ void k_fill_u64(u64* p, size_t n) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -237,16 +176,6 @@ hipError_t launch_step(const StepParams& p, int grid, size_t lds, hipStream_t st
   }
   if (p.wq8) return launch_step_8_q8_r2(p, grid, lds, st);
   return dr == 2 ? launch_step_8_f16_r2(p, grid, lds, st) : launch_step_8_f16_r3(p, grid, lds, st);
-}
-
-hipError_t launch_cross_kv(const LayerDev* layers_dev, int L, int d, int H, int A, int wq8, const float* xa,
-                           uint16_t* xk, uint16_t* xv, hipStream_t st) {
-  dim3 grid((A + 63) / 64, d / 64, 2 * L);
-  if (wq8)
-    hipLaunchKernelGGL(k_cross_kv<1>, grid, dim3(kThreads), 0, st, layers_dev, d, H, A, xa, xk, xv);
-  else
-    hipLaunchKernelGGL(k_cross_kv<0>, grid, dim3(kThreads), 0, st, layers_dev, d, H, A, xa, xk, xv);
-  return hipGetLastError();
 }
 
 hipError_t launch_fill_u64(u64* p, size_t n, hipStream_t st) {

@@ -19,31 +19,9 @@
 // adds the slices in slice order together with the bias (and residual, GELU), so a GEMM ends with
 // its stores and no workgroup waits for another.
 
-#include "w4h_kernels.h"
+#include "w4h_mfma.h"
 
 namespace w4h {
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-constexpr int kPadH = 8;  // halves of padding per LDS activation row (16 bytes: spreads banks)
-
-DEV half8 as_half8(uint4 u) {
-  half8 h;
-  __builtin_memcpy(&h, &u, 16);
-  return h;
-}
-
-// 8 int8 values (two dwords) to 8 exact f16 values.
-DEV half8 i8x8_to_h8(uint2 u) {
-  half8 h;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    h[j] = (_Float16)(float)(int8_t)((u.x >> (8 * j)) & 0xff);
-    h[4 + j] = (_Float16)(float)(int8_t)((u.y >> (8 * j)) & 0xff);
-  }
-  return h;
-}
 
 struct GemmArgs {
   const void* w;         // [N][K] f16, or int8 with f16 scales [N][K/32] in ws

@@ -137,6 +137,12 @@ class Session:
         xa = np.ascontiguousarray(xa, dtype=np.float32)
         check(lib().w4h_session_set_encoder(self._h, enc, _ptr(xa, _f32p)))
 
+    def set_encoder_device(self, xa_ptr: int, enc: int = 0) -> None:
+        """Encoder output already on the session's device: xa_ptr is the address of a contiguous
+        fp32 [n_audio_ctx][n_text_state] buffer (e.g. a torch tensor's data_ptr()) whose producer
+        has finished writing it."""
+        check(lib().w4h_session_set_encoder_device(self._h, enc, ctypes.c_void_p(int(xa_ptr))))
+
     def reset(self, kv_len: int = 0) -> None:
         check(lib().w4h_session_reset(self._h, kv_len))
 
