@@ -241,12 +241,49 @@ def measure_beam(w4h, synth, name, n_steps, beam):
     return steps / dt, beam * steps / dt, dt * 1e6 / steps, steps
 
 
+def measure_greedy_driver(w4h, synth, name, n_tokens):
+    """The library's greedy decode driver (w4h_decode: prompt prefill, then the decode with the
+    suppress, n-gram and timestamp rules; EOT suppressed so every token runs), with the rules on the
+    device (one launch that ends at the end token) and, for comparison, driven from the host (one
+    step call and host round trip per token).  Returns {mode: (tokens/s, us per token)}."""
+    from whisper4j_amd.decoder import WhisperDecoder
+
+    dims = synth.SHAPES[name]
+    T = synth.make_decoder(dims, seed=0, wtype="f16")
+    model = w4h.Model.from_tensors(dims, T)
+    xa = synth.encoder_output(dims, 0)
+    eot, tsb = 50256, 50363
+    prompt = list(synth.BENCH_PREFIX)
+    out = {}
+    old = os.environ.get("W4H_DEVICE_RULES")
+    for mode, env in (("device_rules", "1"), ("host_loop", "0")):
+        os.environ["W4H_DEVICE_RULES"] = env
+        dec = WhisperDecoder(model, beam_size=1, max_ctx=dims.n_text_ctx)
+        dec.decode(xa, prompt, eot, 16, suppress_tokens=[eot], timestamp_begin=tsb)  # warm-up
+        t0 = time.perf_counter()
+        r = dec.decode(xa, prompt, eot, n_tokens, suppress_tokens=[eot], timestamp_begin=tsb)
+        dt = time.perf_counter() - t0
+        dec.close()
+        out[mode] = (len(r.tokens) / dt, dt * 1e6 / len(r.tokens))
+    if old is None:
+        os.environ.pop("W4H_DEVICE_RULES", None)
+    else:
+        os.environ["W4H_DEVICE_RULES"] = old
+    model.close()
+    return out
+
+
 def other_configs(w4h, synth):
     """Absolute decode rates of the four other workload shapes (one bounded run each)."""
     out = {}
     tps, us, frac, setup = measure_forced(w4h, synth, "tiny.en", "f16", 224, 5)
     out["tiny.en greedy b=1, 224 forced steps"] = {"tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
                                                    "roofline_frac": round(frac, 4), "setup": setup}
+    drv = measure_greedy_driver(w4h, synth, "base.en", 224)
+    out["base.en greedy decode driver w4h_decode, 224 tokens (prompt prefill, then suppress + n-gram + timestamp rules; EOT suppressed)"] = {
+        "tokens_per_s": round(drv["device_rules"][0], 1), "us_per_token": round(drv["device_rules"][1], 2),
+        "rules": "on the device, one launch",
+        "host_loop_tokens_per_s": round(drv["host_loop"][0], 1), "host_loop_us_per_token": round(drv["host_loop"][1], 2)}
     sps, hps, us, steps = measure_beam(w4h, synth, "small", 224, 5)
     out["small beam 5, 224 steps (library beam driver w4h_decode_beam: prompt prefill, then the search on the device; EOT suppressed)"] = {
         "steps_per_s": round(sps, 1), "hypothesis_tokens_per_s": round(hps, 1), "us_per_step": round(us, 2),
@@ -273,7 +310,7 @@ def main():
     ap.add_argument("--cpu-max-sweeps", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the tiny/small/turbo/medium lines")
-    ap.add_argument("--only", choices=["turbo", "small-beam-rows"],
+    ap.add_argument("--only", choices=["turbo", "small-beam-rows", "greedy-driver"],
                     help="run only this other workload (one JSON line; for profiling the batched engine)")
     ap.add_argument("--only-steps", type=int, default=224, help="forced steps of the --only workload")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -294,6 +331,11 @@ def main():
 
     if args.only:
         n = args.only_steps
+        if args.only == "greedy-driver":
+            drv = measure_greedy_driver(w4h, synth, "base.en", n)
+            print(json.dumps({"workload": f"base.en greedy decode driver, {n} tokens",
+                              **{k: {"tokens_per_s": round(v[0], 1), "us_per_token": round(v[1], 2)} for k, v in drv.items()}}))
+            return
         if args.only == "turbo":
             tps, us, frac, setup = measure_forced(w4h, synth, "large-v3-turbo", "f16", n, 2, n_rows=32, n_encoders=32)
             work = f"large-v3-turbo 32 streams (own encoder each) in lockstep, {n} forced steps"

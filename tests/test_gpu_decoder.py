@@ -281,3 +281,53 @@ def test_cross_kv_projection_frame_tiles(gpu, orc, wtype, frames):
     say("max-abs", worst)
     assert worst <= TOL
     np.testing.assert_array_equal(out["host"], out["device"])
+
+
+def _ngram_blocks(tokens):
+    """Steps of a greedy decode at which the 3/4-gram rule masks at least one token."""
+    n = 0
+    for j in range(1, len(tokens) + 1):
+        h = tokens[:j]
+        hit = any(h[i:i + 2] == h[-2:] for i in range(len(h) - 2)) or any(h[i:i + 3] == h[-3:] for i in range(len(h) - 3))
+        n += int(len(h) >= 3 and hit)
+    return n
+
+
+@pytest.mark.parametrize("ts_begin,eot,max_tokens,max_ctx", [(-1, 399, 80, 96), (301, 300, 60, 96), (-1, 399, 80, 40)])
+def test_greedy_decode_rules_on_device(gpu, orc, monkeypatch, ts_begin, eot, max_tokens, max_ctx):
+    """Greedy decode of a one-row session with the n-gram and timestamp rules applied by the step
+    kernel (one launch that ends at the end token): tokens and avg log-prob bit-identical to the
+    host-driven loop (one step call per token, rules on the host), and tokens equal to the oracle's
+    decode.  With a self-KV of 40 positions the device run stops at the capacity and the host loop
+    reports the capacity error exactly as it does alone."""
+    dims = synth.Dims(n_vocab=400, n_text_ctx=96, n_text_state=128, n_text_head=2, n_text_layer=2, n_audio_ctx=50)
+    T = make(dims, 61)
+    xa = synth.encoder_output(dims, 61)
+    sup = [1, 2, 3, 220 % dims.n_vocab]
+    prompt = [10, 11, 12]
+    m = gpu.Model.from_tensors(dims, T)
+    res = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("W4H_DEVICE_RULES", mode)
+        dec = gpu.WhisperDecoder(m, beam_size=1, max_ctx=max_ctx)
+        try:
+            res[mode] = dec.decode(xa, prompt, eot, max_tokens, sup, timestamp_begin=ts_begin)
+        except gpu.W4HError as e:
+            res[mode] = e.code
+        dec.close()
+    m.close()
+    if max_ctx < len(prompt) + max_tokens:
+        assert res["1"] == res["0"] == -8  # W4H_ERR_CAPACITY
+        return
+    dev, host = res["1"], res["0"]
+    assert dev.tokens == host.tokens
+    assert dev.avg_logprob == host.avg_logprob
+    og = orc.Model(dims, T).decode(xa, prompt, eot=eot, max_tokens=max_tokens, suppress=sup, ts_begin=ts_begin)
+    blocks = _ngram_blocks(list(og["tokens"]))
+    say(f"greedy rules ts={ts_begin}: {len(dev.tokens)} tokens, n-gram rule active at {blocks} steps")
+    assert dev.tokens == og["tokens"]
+    assert dev.avg_logprob == pytest.approx(og["avg_logprob"], abs=1e-3)
+    if ts_begin < 0:
+        assert blocks > 0
+    else:
+        assert any(t >= ts_begin for t in dev.tokens)

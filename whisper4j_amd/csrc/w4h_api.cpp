@@ -426,6 +426,7 @@ struct w4h_session {
   int S = 1, X = 1, max_ctx = 0, grid = 0, ngroups = 2, ncs_max = 0, ncc = 0, chc = 0, rpw = 0, mw = 0;
   size_t rep_stride = 0, res_off = 0;
   int nres = 0;
+  size_t item_bytes = 0;  // LDS bytes of one resident vocabulary item
   size_t lds = 0;
   hipStream_t stream = nullptr;
   DevBuf kvk, kvv, xk, xv, ll, out, forced, mask, logits, xa_tmp, trace;
@@ -582,9 +583,28 @@ static int copy_back(w4h_session* s, int n_steps, w4h_step_out* out, float* logi
   return W4H_OK;
 }
 
-// Launch n_steps steps; tokens/forced are host arrays.  Results (if out) are copied back.
+// LDS layout of a launch with the decode rules: the rules region takes the start of the resident
+// vocabulary region, which gives up as many items as that needs.  Returns the launch's LDS bytes,
+// or 0 when the rules region does not fit.
+static size_t rules_layout(const w4h_session* s, int hist_cap, StepParams& p) {
+  const size_t rb = rules_lds_bytes(hist_cap, s->rpw);
+  p.rules_off = s->res_off;
+  p.res_off = s->res_off + rb;
+  const int drop = s->nres > 0 ? (int)std::min<size_t>((size_t)s->nres, (rb + s->item_bytes - 1) / s->item_bytes) : 0;
+  p.nres = s->nres - drop;
+  const size_t lds = std::max(s->lds, p.res_off + (size_t)p.nres * s->item_bytes);
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, s->m->device) != hipSuccess || lds > (size_t)prop.sharedMemPerBlock) return 0;
+  return lds;
+}
+
+// Launch n_steps steps; tokens/forced are host arrays.  Results (if out) are copied back.  With
+// `rules` (one-row persistent sessions, greedy feedback, out required) the decode rules run on the
+// device and the run ends after the step that selects rules->eot; *steps_done receives the number
+// of steps run and the self-KV advances by that many.
 int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int n_steps, const uint32_t* extra_mask,
-              int topk, w4h_step_out* out, float* logits, float* ms, uint64_t* trace = nullptr) {
+              int topk, w4h_step_out* out, float* logits, float* ms, uint64_t* trace = nullptr,
+              const RulesRun* rules = nullptr, int* steps_done = nullptr) {
   if (s->closed) return fail(W4H_ERR_CLOSED, "session destroyed");
   if (!tokens || n_steps <= 0) return fail(W4H_ERR_INVALID, "tokens and n_steps > 0 required");
   if (topk < 0 || topk > W4H_TOPK_MAX) return fail(W4H_ERR_INVALID, "topk %d outside [0, %d]", topk, W4H_TOPK_MAX);
@@ -608,6 +628,15 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
   const size_t in_len = s->slots_dirty ? s->in_bytes : (extra_mask ? s->o_slots : s->o_mask2);
   HIPCHK(hipMemcpyAsync(s->in.p, hp, in_len, hipMemcpyHostToDevice, s->stream));
   s->slots_dirty = false;
+  if (rules && (s->wide || s->S != 1 || forced || !out || trace || !steps_done || rules->nhist < 0 ||
+                (rules->nhist > 0 && !rules->hist)))
+    return fail(W4H_ERR_INVALID, "device decode rules need a one-row persistent session, greedy feedback and outputs");
+  if (rules && rules->nhist > 0) {  // the history travels in the forced-token buffers (unused here)
+    const size_t b_hist = sizeof(int32_t) * (size_t)rules->nhist;
+    if ((rc = ensure(s->forced, b_hist)) || (rc = s->h_forced.ensure(b_hist))) return rc;
+    memcpy(s->h_forced.p, rules->hist, b_hist);
+    HIPCHK(hipMemcpyAsync(s->forced.p, s->h_forced.p, b_hist, hipMemcpyHostToDevice, s->stream));
+  }
   if (forced && n_steps > 1) {
     const size_t b_forced = sizeof(int32_t) * (size_t)(n_steps - 1) * s->S;
     if ((rc = ensure(s->forced, b_forced)) || (rc = s->h_forced.ensure(b_forced))) return rc;
@@ -658,13 +687,23 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
   p.out = out ? s->out.as<w4h_step_out>() : nullptr;
   p.logits_out = logits ? s->logits.as<float>() : nullptr;
   p.trace = trace ? s->trace.as<unsigned long long>() : nullptr;
+  size_t lds = s->lds;
+  if (rules) {
+    p.rules = 1;
+    p.eot = rules->eot;
+    p.tsb = rules->tsb;
+    p.hist0 = rules->nhist > 0 ? s->forced.as<int32_t>() : nullptr;
+    p.nhist0 = rules->nhist;
+    p.hist_cap = rules->nhist + n_steps;
+    if (!(lds = rules_layout(s, p.hist_cap, p))) return fail(W4H_ERR_INVALID, "no LDS left for the device decode rules");
+  }
   hipEvent_t e0 = nullptr, e1 = nullptr;
   if (ms) {
     HIPCHK(hipEventCreate(&e0));
     HIPCHK(hipEventCreate(&e1));
     HIPCHK(hipEventRecord(e0, s->stream));
   }
-  hipError_t le = launch_step(p, s->grid, s->lds, s->stream);
+  hipError_t le = launch_step(p, s->grid, lds, s->stream);
   if (le != hipSuccess) return fail(W4H_ERR_DEVICE, "decoder step launch failed: %s", hipGetErrorString(le));
   s->next_tag += (uint32_t)n_steps;
   if (ms) HIPCHK(hipEventRecord(e1, s->stream));
@@ -677,7 +716,15 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
     (void)hipEventDestroy(e1);
   }
   if (herr) return fail(W4H_ERR_TIMEOUT, "a device-side wait expired during the step (code %u); step aborted", herr);
-  s->kv_len += n_steps;
+  int done = n_steps;
+  if (rules)
+    for (int i = 0; i < n_steps; i++)
+      if (out[i].argmax == rules->eot) {
+        done = i + 1;
+        break;
+      }
+  if (steps_done) *steps_done = done;
+  s->kv_len += done;
   return W4H_OK;
 }
 
@@ -824,6 +871,7 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   if (s->S == 1) {
     const int dr = step_rounds(d, m->wq8);
     const size_t item_bytes = (size_t)dr * kThreads * 16 + (m->wq8 ? (size_t)dr * kThreads * 2 : 0);
+    s->item_bytes = item_bytes;
     const size_t limit = (size_t)prop.sharedMemPerBlock;
     const size_t avail = limit > s->res_off + 1024 ? limit - s->res_off - 1024 : 0;
     const int nmine = ((V + 7) / 8 + s->grid - 1) / s->grid;
@@ -1117,6 +1165,24 @@ int w4h_op_select(const float* logits, int32_t rows, int32_t n, const uint32_t* 
 namespace w4h {
 int session_rows(const w4h_session* s) { return s->S; }
 bool session_device_beam(const w4h_session* s) { return s->wide && s->S <= kBeamMax; }
+
+bool session_device_rules(const w4h_session* s) {
+  if (s->wide || s->S != 1) return false;
+  if (const char* e = getenv("W4H_DEVICE_RULES"))
+    if (!strcmp(e, "0")) return false;
+  StepParams p{};  // room for the longest history a decode can reach
+  return rules_layout(s, kMaxDecodeTokens + s->max_ctx, p) != 0;
+}
+
+int session_max_ctx(const w4h_session* s) { return s->max_ctx; }
+
+int device_greedy_run(w4h_session* s, const RulesRun& r, int n_steps, const uint32_t* mask2, w4h_step_out* out,
+                      int* steps_done) {
+  if (!session_device_rules(s)) return fail(W4H_ERR_INVALID, "device decode rules need a one-row persistent session");
+  if (r.nhist < 1 || !r.hist) return fail(W4H_ERR_INVALID, "device decode rules need the generated tokens");
+  const int32_t tok = r.hist[r.nhist - 1];
+  return run_steps(s, &tok, nullptr, n_steps, mask2, 1, out, nullptr, nullptr, nullptr, &r, steps_done);
+}
 
 int device_beam_search(w4h_session* s, const BeamSearchIn& in, BeamSearchOut* out) {
   if (!s->wide || in.beam != s->S || in.beam > kBeamMax) return fail(W4H_ERR_INVALID, "device beam search needs a batched session");

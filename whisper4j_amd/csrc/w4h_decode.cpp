@@ -142,7 +142,8 @@ int check_opts(w4h_session* s, const w4h_decode_opts* o, w4h_decode_result* r) {
   if (!s || !o || !r) return w4h::fail(W4H_ERR_INVALID, "null argument");
   const w4h_dims D = w4h::session_dims(s);
   if (!o->prompt || o->n_prompt < 1) return w4h::fail(W4H_ERR_INVALID, "empty prompt");
-  if (o->max_tokens < 1 || o->max_tokens > 1024) return w4h::fail(W4H_ERR_INVALID, "max_tokens outside [1, 1024]");
+  if (o->max_tokens < 1 || o->max_tokens > w4h::kMaxDecodeTokens)
+    return w4h::fail(W4H_ERR_INVALID, "max_tokens outside [1, %d]", w4h::kMaxDecodeTokens);
   if (o->eot < 0 || o->eot >= D.n_vocab) return w4h::fail(W4H_ERR_INVALID, "eot out of range");
   return W4H_OK;
 }
@@ -207,7 +208,34 @@ int w4h_decode(w4h_session* s, const w4h_decode_opts* o, w4h_decode_result* r) {
   std::vector<int32_t> tok(S);
   w4h_step_out out0{};
   std::vector<w4h_step_out> outs(S);
+  // After the first step a one-row greedy decode runs on the device: the same rules, applied by the
+  // step kernel from the generated tokens, for as many steps as the self-KV holds (the host loop
+  // below takes over if the decode has not ended by then).
+  const bool on_device = greedy && w4h::session_device_rules(s);
   for (int step = 0; step < o->max_tokens; step++) {
+    if (on_device && step == 1) {
+      int32_t kv = 0;
+      if ((rc = w4h_session_kv_len(s, &kv))) return rc;
+      const int n = std::min(o->max_tokens - 1, (int)(w4h::session_max_ctx(s) - kv));
+      if (n > 0) {
+        Mask sup(V, 1);
+        apply_suppress(sup, 0, o->suppress, o->n_suppress);
+        std::vector<w4h_step_out> dev(n);
+        int done = 0;
+        const w4h::RulesRun rr{gen.data(), (int)gen.size(), o->eot, o->timestamp_begin > 0 ? o->timestamp_begin : 0};
+        if ((rc = w4h::device_greedy_run(s, rr, n, sup.bits.data(), dev.data(), &done))) return rc;
+        bool ended = false;
+        for (int i = 0; i < done && !ended; i++) {
+          sumLogprob += (double)dev[i].max_logit - (double)dev[i].logsumexp;
+          if (dev[i].argmax == o->eot)
+            ended = true;
+          else
+            gen.push_back(dev[i].argmax);
+        }
+        step = 1 + done;
+        if (ended || step >= o->max_tokens) break;
+      }
+    }
     mask.clear();
     if (step == 0) suppress_blank(mask, 0, o->eot);
     apply_suppress(mask, 0, o->suppress, o->n_suppress);

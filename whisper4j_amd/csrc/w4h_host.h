@@ -31,4 +31,17 @@ struct BeamSearchOut {
   std::vector<double> fin_lp, lps;
 };
 int device_beam_search(w4h_session* s, const BeamSearchIn& in, BeamSearchOut* out);
+
+// Greedy steps with the decode rules (n-gram repeats, timestamp rules) applied on the device from
+// the generated tokens, for one-row sessions on the persistent step kernel.  The run starts with
+// the last generated token, feeds back each argmax and ends after the step that selects eot.
+struct RulesRun {
+  const int32_t* hist;  // tokens generated so far (the last one is the run's first input)
+  int nhist, eot, tsb;
+};
+constexpr int kMaxDecodeTokens = 1024;  // w4h_decode_opts.max_tokens at most
+bool session_device_rules(const w4h_session* s);
+int session_max_ctx(const w4h_session* s);
+int device_greedy_run(w4h_session* s, const RulesRun& r, int n_steps, const uint32_t* mask2, w4h_step_out* out,
+                      int* steps_done);
 }  // namespace w4h

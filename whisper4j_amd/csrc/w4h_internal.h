@@ -63,7 +63,22 @@ struct StepParams {
   int nres;                     // vocabulary items (8 rows) a workgroup keeps resident in LDS (S = 1)
   size_t res_off;               // byte offset of the resident vocabulary rows in dynamic LDS
   unsigned long long* trace;    // [nsteps][6L+2][grid] phase-end timestamps (wall clock) or null
+  // Decode rules on the device (one-row greedy runs): every workgroup keeps the generated tokens in
+  // LDS, masks the n-gram repeats and timestamp rules of the greedy driver on its own vocabulary
+  // rows, and the run ends after the step that selects the end token.
+  int rules;                    // 1: on (needs S = 1 and greedy feedback)
+  int eot, tsb;                 // end token; first timestamp token (<= 0: no timestamp rules)
+  const int32_t* hist0;         // [nhist0] tokens generated before the run
+  int nhist0, hist_cap;         // history length before the run; LDS history capacity (>= nhist0 + nsteps)
+  size_t rules_off;             // byte offset of the rules region in dynamic LDS
 };
+
+// Ints of the rules region in LDS: history, then a bitmap over the workgroup's logits rows, then
+// the timestamp ranges (count + 4 [lo, hi) pairs); rounded to 16 bytes.
+inline size_t rules_lds_bytes(int hist_cap, int rows_per_wg) {
+  const size_t ints = (size_t)hist_cap + (size_t)(rows_per_wg + 31) / 32 + 9;
+  return (ints * 4 + 15) & ~(size_t)15;
+}
 
 // 16-byte weight chunks per lane and weight row kept in registers by the step kernel's GEMVs over
 // d (32 lanes cover a row, so a row of d halves needs d / 256 rounds, of d int8 values d / 512):

@@ -1251,6 +1251,9 @@ struct Lds {
   float* big;   // phase scratch
   uint4* ew;    // [nres][DR][kThreads] resident vocabulary rows (S = 1), GEMV register image
   uint16_t* es; // [nres][DR][kThreads] their q8_0 scales
+  int* hist;        // decode rules: [hist_cap] generated tokens
+  uint32_t* rbits;  // decode rules: [(rows_per_wg + 31) / 32] rows of this workgroup masked this step
+  int* rrng;        // decode rules: range count, then [lo, hi) token ranges masked this step
 };
 
 // LayerNorm of S rows of d (LDS in, LDS out) with gamma/beta in registers; two passes, eps 1e-5.
@@ -1833,9 +1836,12 @@ DEV bool phase_reduce(const StepParams& p, const Lds& m, const StepCtx& c) {
   // Only the workgroups of the first two phases of the next step (layer 0 self-attention and
   // out-projection, which embed the next token) need the token; the output writer needs the
   // records.  Everyone else goes straight to its next phase, whose inputs depend on these.
+  // The output writer is the grid's last workgroup: the first phases of the next step give their
+  // items to the first workgroups of their groups, so the merge stays off the next step's path.
   const Grp g0 = phase_group(0, G, ng), g1 = phase_group(1, G, ng);
-  const int writer = phase_group(2, G, ng).base;
-  const bool need_tok = !last_step && ((g >= g0.base && g < g0.base + g0.size) || (g >= g1.base && g < g1.base + g1.size));
+  const int writer = G - 1;
+  // With decode rules every workgroup keeps the token history, so every workgroup needs the token.
+  const bool need_tok = !last_step && (p.rules || (g >= g0.base && g < g0.base + g0.size) || (g >= g1.base && g < g1.base + g1.size));
   const bool is_writer = g == writer && p.out != nullptr;
   if (!need_tok && !is_writer) return true;
   float* pairs = m.big;  // [G][S][2]
@@ -1850,6 +1856,7 @@ DEV bool phase_reduce(const StepParams& p, const Lds& m, const StepCtx& c) {
       if ((tid & 63) == 0) m.toks[s] = p.forced ? p.forced[(size_t)c.st * S + s] : (am == 0x7fffffff ? 0 : am);
     }
     lds_barrier();
+    if (p.rules && tid == 0) m.hist[p.nhist0 + c.st] = m.toks[0];
   }
   if (is_writer) {
     const int nblk = (G + kRedBlock - 1) / kRedBlock;
@@ -2192,6 +2199,69 @@ DEV bool phase_mlp2_1(const StepParams& p, const Lds& m, const StepCtx& c, int l
 }
 
 // Final LN + tied-embedding logits + masks + the workgroup's selection partial (one row).
+// Decode rules of one greedy step from the n generated tokens in m.hist (WhisperDecoder
+// applyRepetitionPenalty / applyNgramBlock, main/nn/WhisperDecoder.java:472-476, 543-564, and
+// applyTimestampRules for every step after the first, :484-541): a token that would complete a
+// 3-gram or 4-gram already in the history is masked, marked in m.rbits when it is one of this
+// workgroup's logits rows (item (row / 8) = g + i * G is local row i * 8 + row % 8); the
+// timestamp rules become at most four [lo, hi) ranges in m.rrng.  Runs before the logits poll.
+DEV void rules_prepare(const StepParams& p, const Lds& m, int n, int rpw) {
+  const int tid = threadIdx.x, G = gridDim.x, g = blockIdx.x, V = p.V, tsb = p.tsb;
+  const int* h = m.hist;
+  for (int i = tid; i < (rpw + 31) / 32; i += kThreads) m.rbits[i] = 0u;
+  lds_barrier();
+  const int l1 = n >= 1 ? h[n - 1] : -1, l2 = n >= 2 ? h[n - 2] : -1, l3 = n >= 3 ? h[n - 3] : -1;
+  auto mark = [&](int t) {
+    if (t < 0 || t >= V) return;
+    const int item = t >> 3;
+    if (item < g || (item - g) % G != 0) return;
+    const int li = ((item - g) / G) * 8 + (t & 7);
+    atomicOr(&m.rbits[li >> 5], 1u << (li & 31));
+  };
+  int last_ts = -1;  // index of the last timestamp token
+  for (int i = tid; i < n; i += kThreads) {
+    if (tsb > 0 && h[i] >= tsb) last_ts = i;
+    if (i <= n - 3 && h[i] == l2 && h[i + 1] == l1) mark(h[i + 2]);
+    if (i <= n - 4 && h[i] == l3 && h[i + 1] == l2 && h[i + 2] == l1) mark(h[i + 3]);
+  }
+  last_ts = -wave_min_i(-last_ts);
+  int* red = m.rrng + 5;  // the pair slots double as the four waves' maxima before they are written
+  lds_barrier();
+  if ((tid & 63) == 0) red[tid >> 6] = last_ts;
+  lds_barrier();
+  if (tid == 0) {
+    const int lt = max(max(red[0], red[1]), max(red[2], red[3]));
+    int r[8], nr = 0;
+    if (tsb > 0) {
+      r[nr++] = tsb - 1;
+      r[nr++] = tsb;
+      if (n > 0) {
+        const bool last_was = h[n - 1] >= tsb, pen_was = n < 2 || h[n - 2] >= tsb;
+        if (last_was) {
+          r[nr++] = pen_was ? tsb : 0;
+          r[nr++] = pen_was ? V : p.eot;
+        }
+        if (lt >= 0) {
+          r[nr++] = tsb;
+          r[nr++] = (last_was && !pen_was) ? h[lt] + 1 : h[lt];
+        }
+      }
+    }
+    m.rrng[0] = nr / 2;
+    for (int k = 0; k < nr; ++k) m.rrng[1 + k] = r[k];
+  }
+  lds_barrier();
+}
+
+DEV bool rule_masked(const StepParams& p, const Lds& m, int row, int li) {
+  if (!p.rules) return false;
+  if ((m.rbits[li >> 5] >> (li & 31)) & 1u) return true;
+  const int nr = m.rrng[0];
+  for (int k = 0; k < nr; ++k)
+    if (row >= m.rrng[1 + 2 * k] && row < m.rrng[2 + 2 * k]) return true;
+  return false;
+}
+
 template <int WQ8, int DR>
 DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
   constexpr int R = DR;
@@ -2230,7 +2300,7 @@ DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
       if (row < V) {
         const float v = gemv_out(rb, i, rr);
         rw[li] = v;
-        lg[li] = (masked(p.mask, p.mw, 0, row) || masked(p.mask2, p.mw, 0, row)) ? -INFINITY : v;
+        lg[li] = (masked(p.mask, p.mw, 0, row) || masked(p.mask2, p.mw, 0, row) || rule_masked(p, m, row, li)) ? -INFINITY : v;
         lidx[li] = row;
         if (p.logits_out) p.logits_out[(size_t)c.st * V + row] = v;
       } else {
@@ -2290,7 +2360,12 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
   m.big = m.xn + S * d;
   m.ew = reinterpret_cast<uint4*>(reinterpret_cast<char*>(lds_raw) + p.res_off);
   m.es = reinterpret_cast<uint16_t*>(m.ew + (size_t)p.nres * DR * kThreads);
+  m.hist = reinterpret_cast<int*>(reinterpret_cast<char*>(lds_raw) + p.rules_off);
+  m.rbits = reinterpret_cast<uint32_t*>(m.hist + p.hist_cap);
+  m.rrng = reinterpret_cast<int*>(m.rbits + (p.rows_per_wg + 31) / 32);
   if (tid < S) m.toks[tid] = p.tokens0[tid];
+  if (p.rules)
+    for (int i = tid; i < p.nhist0; i += kThreads) m.hist[i] = p.hist0[i];
   if constexpr (SM == 1) {
     if (p.nres > 0) {
       const int nitems = (p.V + 7) / 8, G = gridDim.x;
@@ -2315,9 +2390,15 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
         if (!phase_self1<WQ8, DR>(p, m, c, l, phase_group(q, G, ng))) return;
         STAMP(3);
         ++c.ph;
+        // Decode rules for this step's logits, prepared where the workgroup waits anyway: the
+        // group of layer 0's out-projection waits there for the self-attention, the other group
+        // waits for the out-projection before its cross-attention.
+        const bool in_g1 = grp_first(phase_group(1, G, ng)) != 0x7fffffff;
+        if (l == 0 && p.rules && in_g1) rules_prepare(p, m, p.nhist0 + st, p.rows_per_wg);
         if (!phase_out1<WQ8, DR>(p, m, c, l, phase_group(q + 1, G, ng), false)) return;
         STAMP(3);
         ++c.ph;
+        if (l == 0 && p.rules && !in_g1) rules_prepare(p, m, p.nhist0 + st, p.rows_per_wg);
         if (!phase_cross1<WQ8, DR>(p, m, c, l, phase_group(q + 2, G, ng))) return;
         STAMP(3);
         ++c.ph;
@@ -2361,6 +2442,8 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
     if (!phase_reduce(p, m, c)) return;
     STAMP(3);
     ++c.ph;
+    // every workgroup saw the same token (all reduce the same pairs): the run ends together
+    if (p.rules && st + 1 < p.nsteps && m.toks[0] == p.eot) break;
   }
   kv_drain();
 }
