@@ -202,3 +202,4 @@ def test_device_beam_search_matches_oracle(gpu, orc, monkeypatch, beam, max_toke
         assert b.avg_logprob == pytest.approx(ob["avg_logprob"], abs=1e-3)
     dec.close()
     m.close()
+

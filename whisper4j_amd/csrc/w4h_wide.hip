@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void k_w_gemm(GemmArgs a) {
   const int stopped = a.ctl->stop;
   constexpr int KW = 4 / NW;
   constexpr int Rp = MT * 16;
-  constexpr int CB = 16 * NW;                // columns per workgroup
+  constexpr int CB = 16 * NW;                // columns per column block
   constexpr int kpart = KB * kWideKBlock;    // k per wave
   constexpr int kslice = KW * kpart;         // k per workgroup
   constexpr int rs = kslice + kPadH;         // halves per LDS row
@@ -74,60 +74,61 @@ __global__ __launch_bounds__(256) void k_w_gemm(GemmArgs a) {
   const int N = a.N, K = a.K;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g4 = lane >> 4, c16 = lane & 15;
   const int cg = wv % NW, kw = wv / NW;
-  const int n = blockIdx.x * CB + cg * 16 + c16;
   const int k0 = blockIdx.y * kslice;        // workgroup's first k
   const int kp0 = k0 + kw * kpart;           // wave's first k
   const int nkb = max(0, min(kpart, K - kp0)) / kWideKBlock;
+  const int n = blockIdx.x * CB + cg * 16 + c16;
   const int nr = min(n, N - 1);
 
   // 1. activation slice into registers first (L2 hits), so that waiting for it does not wait for
   //    the weight loads issued after it; 8 consecutive k per task
   constexpr int tasks_per_row = kslice / 8;
   constexpr int TPT = Rp * tasks_per_row / 256;  // tasks per thread
+  //    Every load is unconditional (rows and k clamped, out-of-range values zeroed when staged), so
+  //    the compiler can count the loads in flight and wait only for the ones it consumes.
   float4 av[TPT][2];
 #pragma unroll
   for (int q = 0; q < TPT; ++q) {
     const int t = tid + 256 * q;
     const int r = t / tasks_per_row, c8 = t - r * tasks_per_row;
-    const int k = k0 + c8 * 8;
-    if (r < a.S && k < K) {
-      av[q][0] = *reinterpret_cast<const float4*>(a.act + (size_t)r * a.lda + k);
-      av[q][1] = *reinterpret_cast<const float4*>(a.act + (size_t)r * a.lda + k + 4);
-    } else {
-      av[q][0] = make_float4(0.f, 0.f, 0.f, 0.f);
-      av[q][1] = av[q][0];
-    }
+    const int rc = min(r, a.S - 1), kc = min(k0 + c8 * 8, K - 8);
+    av[q][0] = *reinterpret_cast<const float4*>(a.act + (size_t)rc * a.lda + kc);
+    av[q][1] = *reinterpret_cast<const float4*>(a.act + (size_t)rc * a.lda + kc + 4);
   }
 
-  // 2. weight fragments of the wave's k part
+  // 2. weight fragments of the wave's k part; blocks past K (the last slice) load the row's last 16
+  //    bytes again and are skipped by the MFMA loop.  The activation loads are issued first and the
+  //    weights after them, so that staging the activations waits for its own loads only.
   half8 bf[KB][4];
   uint2 bq[KB][4];
   float sc[KB][4];
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      const int k = kp0 + kb * kWideKBlock + 32 * b + 8 * g4;
-      if (kb < nkb) {
-        if (!WQ8) {
-          bf[kb][b] = as_half8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.w) + (size_t)nr * K + k));
-        } else {
-          bq[kb][b] = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(a.w) + (size_t)nr * K + k);
-          sc[kb][b] = h2f(a.ws[(size_t)nr * (K >> 5) + (k >> 5)]);
-        }
+      const int k = min(kp0 + kb * kWideKBlock + 32 * b + 8 * g4, K - 8);
+      if (!WQ8) {
+        bf[kb][b] = as_half8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.w) + (size_t)nr * K + k));
+      } else {
+        bq[kb][b] = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(a.w) + (size_t)nr * K + k);
+        sc[kb][b] = h2f(a.ws[(size_t)nr * (K >> 5) + (k >> 5)]);
       }
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
 
   // activation slice -> LDS as (hi, lo) f16 parts
 #pragma unroll
   for (int q = 0; q < TPT; ++q) {
     const int t = tid + 256 * q;
     const int r = t / tasks_per_row, c8 = t - r * tasks_per_row;
-    const float v[8] = {av[q][0].x, av[q][0].y, av[q][0].z, av[q][0].w, av[q][1].x, av[q][1].y, av[q][1].z, av[q][1].w};
+    const bool in = r < a.S && k0 + c8 * 8 < K;
+    float v[8] = {av[q][0].x, av[q][0].y, av[q][0].z, av[q][0].w, av[q][1].x, av[q][1].y, av[q][1].z, av[q][1].w};
     half8 h, l;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
+      v[j] = in ? v[j] : 0.f;
       h[j] = (_Float16)v[j];
       l[j] = (_Float16)(v[j] - (float)h[j]);
     }
@@ -137,61 +138,60 @@ __global__ __launch_bounds__(256) void k_w_gemm(GemmArgs a) {
   lds_barrier();
 
   // 3. MFMA over the wave's k part
-  floatx4 acc[MT];
+  {
+    floatx4 acc[MT];
 #pragma unroll
-  for (int m = 0; m < MT; ++m) acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < MT; ++m) acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
-    if (kb < nkb) {
+    for (int kb = 0; kb < KB; ++kb) {
+      if (kb < nkb) {
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int kk = kw * kpart + kb * kWideKBlock + 32 * b + 8 * g4;
-        const half8 B = WQ8 ? i8x8_to_h8(bq[kb][b]) : bf[kb][b];
+        for (int b = 0; b < 4; ++b) {
+          const int kk = kw * kpart + kb * kWideKBlock + 32 * b + 8 * g4;
+          const half8 B = WQ8 ? i8x8_to_h8(bq[kb][b]) : bf[kb][b];
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          const half8 ah = *reinterpret_cast<const half8*>(hi + (m * 16 + c16) * rs + kk);
-          const half8 al = *reinterpret_cast<const half8*>(lo + (m * 16 + c16) * rs + kk);
-          if (!WQ8) {
-            acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, B, acc[m], 0, 0, 0);
-            acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, B, acc[m], 0, 0, 0);
-          } else {
-            floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, B, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, B, t, 0, 0, 0);
-            acc[m] += t * sc[kb][b];
+          for (int m = 0; m < MT; ++m) {
+            const half8 ah = *reinterpret_cast<const half8*>(hi + (m * 16 + c16) * rs + kk);
+            const half8 al = *reinterpret_cast<const half8*>(lo + (m * 16 + c16) * rs + kk);
+            if (!WQ8) {
+              acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, B, acc[m], 0, 0, 0);
+              acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, B, acc[m], 0, 0, 0);
+            } else {
+              floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, B, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+              t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, B, t, 0, 0, 0);
+              acc[m] += t * sc[kb][b];
+            }
           }
         }
       }
     }
-  }
-
-  // 4. k parts of a column group added in k order through LDS (reusing the staging area)
-  if constexpr (KW > 1) {
-    float* red = reinterpret_cast<float*>(lds_h);  // [KW-1][NW][MT*4][64]
-    lds_barrier();
-    if (kw > 0)
-#pragma unroll
-      for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) red[(((kw - 1) * NW + cg) * MT * 4 + m * 4 + j) * 64 + lane] = acc[m][j];
-    lds_barrier();
-    if (kw == 0)
-#pragma unroll
-      for (int q = 1; q < KW; ++q)
+    // 4. k parts of a column group added in k order through LDS (after the staged slice)
+    if constexpr (KW > 1) {
+      float* red = reinterpret_cast<float*>(lds_h + 2 * Rp * rs);  // [KW-1][NW][MT*4][64]
+      lds_barrier();
+      if (kw > 0)
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[m][j] += red[(((q - 1) * NW + cg) * MT * 4 + m * 4 + j) * 64 + lane];
-  }
-
-  // 5. partial sums of this slice: lane holds rows 4(i/16) + [0, 4) of each 16-row tile, column n
-  if (stopped) return;
-  if (kw == 0 && n < N) {
-    float* o = a.part + (size_t)blockIdx.y * Rp * N + n;
+          for (int j = 0; j < 4; ++j) red[(((kw - 1) * NW + cg) * MT * 4 + m * 4 + j) * 64 + lane] = acc[m][j];
+      lds_barrier();
+      if (kw == 0)
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
+        for (int q = 1; q < KW; ++q)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (m * 16 + 4 * g4 + j < a.S) o[(size_t)(m * 16 + 4 * g4 + j) * N] = acc[m][j];
+          for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[m][j] += red[(((q - 1) * NW + cg) * MT * 4 + m * 4 + j) * 64 + lane];
+    }
+    // 5. partial sums of this slice: lane holds rows 4(i/16) + [0, 4) of each 16-row tile, column n
+    if (!stopped && kw == 0 && n < N) {
+      float* o = a.part + (size_t)blockIdx.y * Rp * N + n;
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (m * 16 + 4 * g4 + j < a.S) o[(size_t)(m * 16 + 4 * g4 + j) * N] = acc[m][j];
+    }
   }
 }
 
@@ -945,7 +945,8 @@ WideGemm wide_plan(const void* w, const uint16_t* ws, int N, int K, int n_cu) {
 
 template <int MT, int KB, int NW>
 constexpr size_t gemm_lds() {
-  return (size_t)2 * MT * 16 * ((4 / NW) * KB * kWideKBlock + kPadH) * sizeof(uint16_t);
+  return (size_t)2 * MT * 16 * ((4 / NW) * KB * kWideKBlock + kPadH) * sizeof(uint16_t) +
+         (size_t)(4 / NW - 1) * NW * MT * 4 * 64 * sizeof(float);
 }
 
 template <int MT, int WQ8, int KB, int NW>
