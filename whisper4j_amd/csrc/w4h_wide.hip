@@ -33,17 +33,19 @@ struct GemmArgs {
   const WideCtl* ctl;    // a stopped run (ended beam search) stores nothing
 };
 
-// Sum of the ks slices of a GEMM output at p[j * ss + idx], added in slice order: four slices' loads
-// in flight at a time, with clamped (branch-free) addresses.
-constexpr int kSliceBatch = 4;
+// Sum of the ks slices of a GEMM output at p[j * ss + idx], added in slice order: B slices' loads in
+// flight at a time, with clamped (branch-free) addresses.  Kernels with one output value per thread
+// take every slice in one round trip (B = kWideMaxSlices); the selection, which loops over many
+// values per lane, takes four at a time.
+template <int B>
 DEV float slice_sum(const float* p, int ks, size_t ss, size_t idx) {
   float v = 0.f;
-  for (int j = 0; j < ks; j += kSliceBatch) {
-    float t[kSliceBatch];
+  for (int j = 0; j < ks; j += B) {
+    float t[B];
 #pragma unroll
-    for (int u = 0; u < kSliceBatch; ++u) t[u] = p[(size_t)min(j + u, ks - 1) * ss + idx];
+    for (int u = 0; u < B; ++u) t[u] = p[(size_t)min(j + u, ks - 1) * ss + idx];
 #pragma unroll
-    for (int u = 0; u < kSliceBatch; ++u) v += j + u < ks ? t[u] : 0.f;
+    for (int u = 0; u < B; ++u) v += j + u < ks ? t[u] : 0.f;
   }
   return v;
 }
@@ -293,7 +295,7 @@ __global__ __launch_bounds__(256) void k_w_gelu(const WideCtl* __restrict__ ctl,
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= S * n) return;
   const int r = i / n, k = i - r * n;
-  const float v = gelu_f16(bias[k] + slice_sum(P, ks, ss, (size_t)r * n + k));
+  const float v = gelu_f16(bias[k] + slice_sum<kWideMaxSlices>(P, ks, ss, (size_t)r * n + k));
   if (!stopped) act[(size_t)r * lda + k] = v;
 }
 
@@ -363,7 +365,7 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
   if (tid < 192) {
     const int part = tid >> 6, e = tid & 63;
     const int col = part * d + h * kHeadDim + e;
-    const float v = bqkv[col] + slice_sum(P, ks, ss, (size_t)s * 3 * d + col);
+    const float v = bqkv[col] + slice_sum<kWideMaxSlices>(P, ks, ss, (size_t)s * 3 * d + col);
     if (part == 0) q[e] = v;
     else if (part == 1) kc[e] = v;
     else vc[e] = v;
@@ -503,7 +505,7 @@ __global__ __launch_bounds__(256) void k_w_cross(const WideCtl* __restrict__ ctl
   for (int i = tid; i < nr * 64; i += 256) {
     const int r = i >> 6, k = i & 63;
     const int col = h * kHeadDim + k;
-    q[i] = (bcq[col] + slice_sum(P, ks, ss, (size_t)(r0 + r) * d + col)) * 0.125f;
+    q[i] = (bcq[col] + slice_sum<kWideMaxSlices>(P, ks, ss, (size_t)(r0 + r) * d + col)) * 0.125f;
   }
   __syncthreads();
   for (int jj = 0; jj < n; jj += 32 * kKeysInFlight) {
@@ -669,7 +671,7 @@ __global__ __launch_bounds__(256) void k_w_select(const WideCtl* __restrict__ ct
   const int nl = max(0, min(kWideSelChunk, V - v0));
   for (int j = lane; j < nl; j += 64) {
     const int v = v0 + j;
-    const float x = slice_sum(P, ks, ss, (size_t)s * V + v);
+    const float x = slice_sum<4>(P, ks, ss, (size_t)s * V + v);
     rw[wv][j] = x;
     lg[wv][j] = (masked(mask, mw, s, v) || masked(mask2, mw, s, v)) ? -INFINITY : x;
     idx[wv][j] = v;
