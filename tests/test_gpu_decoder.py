@@ -331,3 +331,29 @@ def test_greedy_decode_rules_on_device(gpu, orc, monkeypatch, ts_begin, eot, max
         assert blocks > 0
     else:
         assert any(t >= ts_begin for t in dev.tokens)
+
+
+@pytest.mark.parametrize("d,heads,wtype", [(768, 12, "f16"), (512, 8, "q8_0"), (1024, 16, "q8_0")])
+def test_greedy_decode_rules_on_device_variants(gpu, orc, monkeypatch, d, heads, wtype):
+    """The device decode rules in the other one-row step kernels (three register rounds for
+    d = 768, q8_0 weights, streamed rows for d = 1024): timestamp rules on, tokens and average
+    log-probability bit-identical to the host-driven loop, tokens equal to the oracle's decode."""
+    dims = synth.Dims(n_vocab=500, n_text_ctx=64, n_text_state=d, n_text_head=heads, n_text_layer=2, n_audio_ctx=40)
+    T = make(dims, 62, wtype=wtype)
+    xa = synth.encoder_output(dims, 62)
+    sup = [1, 2, 3]
+    prompt, eot, tsb = [10, 11, 12], 400, 401
+    m = gpu.Model.from_tensors(dims, T)
+    res = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("W4H_DEVICE_RULES", mode)
+        dec = gpu.WhisperDecoder(m, beam_size=1, max_ctx=dims.n_text_ctx)
+        res[mode] = dec.decode(xa, prompt, eot, 40, sup, timestamp_begin=tsb)
+        dec.close()
+    m.close()
+    assert res["1"].tokens == res["0"].tokens
+    assert res["1"].avg_logprob == res["0"].avg_logprob
+    og = orc.Model(dims, T).decode(xa, prompt, eot=eot, max_tokens=40, suppress=sup, ts_begin=tsb)
+    say(f"greedy rules d={d} {wtype}: {len(res['1'].tokens)} tokens")
+    assert res["1"].tokens == og["tokens"]
+    assert res["1"].avg_logprob == pytest.approx(og["avg_logprob"], abs=1e-3)
