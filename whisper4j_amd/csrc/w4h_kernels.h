@@ -816,23 +816,28 @@ DEV float gemv_out(const float* red, int i, int rr) {
 }
 
 // gemv_rx for items whose weight chunks sit in LDS in register-image order
-// (wl[(i * R + r) * kThreads + thread], scales alike); items i >= nit are skipped.
+// (wl[(i * R + r) * kThreads + thread], scales alike).  Items i >= nit (nit >= 1) recompute item
+// nit - 1 and their sums are not used: without a branch per item every LDS read of the batch is
+// issued at once and the items' FMA chains interleave.
 template <int R, int NB, int WQ8>
 DEV void gemv_lds(const uint4* wl, const uint16_t* sl, int nit, const XR<R, WQ8>& X, float* red) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, row = lane >> 3;
+  uint4 wv[NB][R];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int r = 0; r < R; ++r) wv[i][r] = wl[(min(i, nit - 1) * R + r) * kThreads + tid];
   float acc[NB];
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
+    const int ic = min(i, nit - 1);
     float a = 0.f;
-    if (i < nit) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const uint4 wv = wl[(i * R + r) * kThreads + tid];
-        if (!WQ8)
-          a += dot8_fx(wv, X.v[r]);
-        else
-          a = fmaf(h2f(sl[(i * R + r) * kThreads + tid]), dot16_qx(wv, X.v[r]), a);
-      }
+    for (int r = 0; r < R; ++r) {
+      if (!WQ8)
+        a += dot8_fx(wv[i][r], X.v[r]);
+      else
+        a = fmaf(h2f(sl[(ic * R + r) * kThreads + tid]), dot16_qx(wv[i][r], X.v[r]), a);
     }
     acc[i] = sum8(a);
   }
