@@ -971,10 +971,15 @@ template <int NI>
 DEV void ln_row(const float* x, float* y, int d, const VecRegs& g, const VecRegs& b) {
   float mean, inv;
   ln_stats<NI>(x, d, mean, inv);
+  // every element read first (clamped index, no branch per element), so the LDS reads overlap;
+  // NI * 256 >= d, so NI elements per thread cover the row
+  float xv[NI];
 #pragma unroll
-  for (int i = 0; i < kVecRegs; ++i) {
+  for (int i = 0; i < NI; ++i) xv[i] = x[min((int)threadIdx.x + kThreads * i, d - 1)];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
     const int j = threadIdx.x + kThreads * i;
-    if (j < d) y[j] = (x[j] - mean) * inv * g.v[i] + b.v[i];
+    if (j < d) y[j] = (xv[i] - mean) * inv * g.v[i] + b.v[i];
   }
   lds_barrier();
 }
