@@ -676,6 +676,35 @@ DEV void attn_compute(const KVRegs<KPT>& r, int n, int ns, const float* q, const
 
 // Merge attention partials: part[(c * nrow + row) * kPartWords + w] for c < nc -> o[row*64 + e].
 DEV void attn_merge(const float* part, int nc, int nrow, float* o) {
+  constexpr int CM = 8;  // chunks merged from registers: every partial read before the sums
+  if (nc <= CM) {
+    for (int i = threadIdx.x; i < nrow * kHeadDim; i += kThreads) {
+      const int row = i >> 6, e = i & 63;
+      float mv[CM], lv[CM], av[CM];
+#pragma unroll
+      for (int c = 0; c < CM; ++c) {
+        const float* pp = part + (min(c, nc - 1) * nrow + row) * kPartWords;  // clamped: no branch
+        mv[c] = pp[0];
+        lv[c] = pp[1];
+        av[c] = pp[2 + e];
+      }
+      float M = -INFINITY;
+#pragma unroll
+      for (int c = 0; c < CM; ++c) M = fmaxf(M, mv[c]);  // repeats of the last chunk leave it alone
+      float Lsum = 0.f, acc = 0.f;
+#pragma unroll
+      for (int c = 0; c < CM; ++c) {
+        if (c < nc) {  // same chunks, same order as below
+          const float f = __expf(mv[c] - M);
+          Lsum = fmaf(lv[c], f, Lsum);
+          acc = fmaf(av[c], f, acc);
+        }
+      }
+      o[i] = acc / Lsum;
+    }
+    lds_barrier();
+    return;
+  }
   for (int i = threadIdx.x; i < nrow * kHeadDim; i += kThreads) {
     const int row = i >> 6, e = i & 63;
     float M = -INFINITY;
