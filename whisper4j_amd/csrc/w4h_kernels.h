@@ -843,6 +843,16 @@ DEV float gemv_out(const float* red, int i, int rr) {
   const float* p = red + i * 32 + rr;
   return (p[0] + p[8]) + (p[16] + p[24]);
 }
+// All 8 outputs of item i (o[rr] = gemv_out(red, i, rr), same sums): the item's 32 partials are
+// contiguous and read as eight 16-byte words at once.
+DEV void gemv_out8(const float* red, int i, float (&o)[8]) {
+  float4 q[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) q[k] = reinterpret_cast<const float4*>(red + i * 32)[k];
+  const float* p = reinterpret_cast<const float*>(q);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (p[e] + p[8 + e]) + (p[16 + e] + p[24 + e]);
+}
 
 // gemv_rx for items whose weight chunks sit in LDS in register-image order
 // (wl[(i * R + r) * kThreads + thread], scales alike).  Items i >= nit (nit >= 1) recompute item
@@ -1986,8 +1996,12 @@ DEV bool phase_self1(const StepParams& p, const Lds& m, const StepCtx& c, int l,
       gemv_rx<R, kNB, WQ8>(wa, X, lw.w_qkv, lw.s_qkv, d3, d, rowA >> 3, 1, m.xn, red);
       lds_barrier();
       float Q[8];
+      {
+        float qv[8];
+        gemv_out8(red, sub, qv);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) Q[e] = gemv_out(red, sub, e) + bq[e];
+        for (int e = 0; e < 8; ++e) Q[e] = qv[e] + bq[e];
+      }
       float M, Ls, A;
       attn_rx<KPT_SELF>(kr, n, Q, 0.125f, wpart, M, Ls, A);
       STAMP(2);
@@ -2072,8 +2086,12 @@ DEV bool phase_cross1(const StepParams& p, const Lds& m, const StepCtx& c, int l
     gemv_rx<R, kNB, WQ8>(wq, X, lw.w_cq, lw.s_cq, d, d, (h * kHeadDim) >> 3, 1, m.xn, red);
     lds_barrier();
     float Q[8];
+    {
+      float qv[8];
+      gemv_out8(red, sub, qv);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) Q[e] = gemv_out(red, sub, e) + bq[e];
+      for (int e = 0; e < 8; ++e) Q[e] = qv[e] + bq[e];
+    }
     float M, Ls, A;
     attn_rx<KPT_CROSS>(kr, n, Q, 0.125f, wpart, M, Ls, A);
     STAMP(2);
