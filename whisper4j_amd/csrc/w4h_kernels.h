@@ -1789,12 +1789,15 @@ DEV bool phase_mlp2(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
 // in flight before the poll.
 template <int SM, int WQ8, int DR>
 DEV bool phase_logits(const StepParams& p, const Lds& m, const StepCtx& c) {
-  constexpr int R = DR, NBL = SM == 1 ? kNB : 4;
+  // several rows: every item streamed (one-row sessions run phase_logits1, which keeps part of the
+  // vocabulary resident in LDS)
+  static_assert(SM > 1, "one-row sessions use phase_logits1");
+  constexpr int R = DR, NBL = 4;
   const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x, S = p.S, d = p.d, V = p.V;
   const int nitems = (V + 7) / 8;
   const int nmine = g < nitems ? (nitems - g + G - 1) / G : 0;
-  const int nr = SM == 1 ? min(p.nres, nmine) : 0;  // items resident in LDS
-  const int nst = nmine - nr;                       // items streamed from memory
+  const int nr = 0;
+  const int nst = nmine - nr;
   const int nb = (nst + NBL - 1) / NBL;
   const int rpw = p.rows_per_wg;
   float* lg = m.big;                                  // [S][rpw] masked
@@ -1829,17 +1832,6 @@ DEV bool phase_logits(const StepParams& p, const Lds& m, const StepCtx& c) {
       }
     }
   };
-  if constexpr (SM == 1) {
-    XR<R, WQ8> X;
-    xr_load<R, WQ8>(m.xn, d, X);
-    for (int b = 0; b < nr; b += kNB, ++nbat) {
-      const int nit = min(kNB, nr - b);
-      float* rb = red + (nbat & 1) * NBL * 32 * SM;
-      gemv_lds<R, kNB, WQ8>(m.ew + (size_t)b * R * kThreads, m.es + (size_t)b * R * kThreads, nit, X, rb);
-      lds_barrier();
-      emit(rb, b, nit);
-    }
-  }
   auto batch = [&](const WBatch<R, NBL>& w, int b) {
     const int nit = min(NBL, nst - b * NBL);
     float* rb = red + (nbat & 1) * NBL * 32 * SM;
