@@ -225,13 +225,15 @@ __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl
     const int pe = t < C - 1 ? t : C - 1;
     const int tk = (i0 == 0 && !ctl->tok_dev) ? tokens0[s]
                                               : (ctl->forced_on ? forced[(size_t)(i0 - 1) * S + s] : next_tok[s]);
+    // every load unconditional (clamped j), so they are all in flight together
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int j = min(tid + 256 * i, d - 1);
       float e;
       if (!WQ8) e = h2f(static_cast<const uint16_t*>(emb)[(size_t)tk * d + j]);
       else e = (float)static_cast<const int8_t*>(emb)[(size_t)tk * d + j] * h2f(emb_s[(size_t)tk * (d >> 5) + (j >> 5)]);
-      v[i] = tid + 256 * i < d ? e + pos[(size_t)pe * d + j] : 0.f;
+      const float pv = pos[(size_t)pe * d + j];
+      v[i] = tid + 256 * i < d ? e + pv : 0.f;
     }
   } else {
     float xr[NV], bs[NV];
@@ -787,6 +789,7 @@ __global__ __launch_bounds__(256) void k_w_beam(WideCtl* __restrict__ ctl, BeamD
   __syncthreads();
   if (tid < nc && clive[tid]) {
     int rank = 0;
+#pragma unroll 8
     for (int c = 0; c < nc; ++c)
       if (clive[c] && (csc[c] > csc[tid] || (csc[c] == csc[tid] && c < tid))) ++rank;
     order[rank] = tid;
@@ -874,6 +877,18 @@ __global__ __launch_bounds__(256) void k_w_beam(WideCtl* __restrict__ ctl, BeamD
   auto set = [&](int j, int t) {
     if (t >= 0 && t < V) atomicOr(msk + (size_t)j * mw + (t >> 5), 1u << (t & 31));
   };
+  // tokens [lo, hi) of row j, one word per thread and step (bits of [lo, hi) within each word)
+  auto set_range = [&](int j, int lo, int hi) {
+    lo = max(lo, 0);
+    hi = min(hi, V);
+    if (lo >= hi) return;
+    for (int w = (lo >> 5) + tid; w <= ((hi - 1) >> 5); w += 256) {
+      const int a = max(lo - 32 * w, 0), e = min(hi - 32 * w, 32);  // bits [a, e) of word w
+      const uint32_t bits = (e >= 32 ? 0xffffffffu : ((1u << e) - 1u)) & ~((1u << a) - 1u);
+      atomicOr(msk + (size_t)j * mw + w, bits);
+    }
+  };
+  __shared__ int s_lastq;
   for (int j = 0; j < B; ++j) {
     const int b = psrc[j], cnt = slen[b] + 1;
     auto g = [&](int q) { return q < cnt - 1 ? stoks[b][q] : ptok[j]; };
@@ -888,12 +903,16 @@ __global__ __launch_bounds__(256) void k_w_beam(WideCtl* __restrict__ ctl, BeamD
       if (tid == 0) set(j, tsb - 1);
       const bool last_ts = g(cnt - 1) >= tsb;
       const bool pen_ts = cnt < 2 || g(cnt - 2) >= tsb;
-      int lastTs = -1;
-      for (int q = cnt - 1; q >= 0; --q)
-        if (g(q) >= tsb) {
-          lastTs = g(q);
-          break;
-        }
+      // the last timestamp of the history: the largest position holding one, found in parallel
+      if (tid == 0) s_lastq = -1;
+      __syncthreads();
+      int qmax = -1;
+      for (int q = tid; q < cnt; q += 256)
+        if (g(q) >= tsb) qmax = q;
+      if (qmax >= 0) atomicMax(&s_lastq, qmax);
+      __syncthreads();
+      const int lastTs = s_lastq >= 0 ? g(s_lastq) : -1;
+      __syncthreads();  // s_lastq is reset for the next beam only after every thread has read it
       int lo1 = 0, hi1 = 0, lo2 = 0, hi2 = 0;
       if (last_ts) {
         if (pen_ts) {
@@ -908,8 +927,8 @@ __global__ __launch_bounds__(256) void k_w_beam(WideCtl* __restrict__ ctl, BeamD
         lo2 = tsb;
         hi2 = (last_ts && !pen_ts) ? lastTs + 1 : lastTs;
       }
-      for (int t = lo1 + tid; t < hi1; t += 256) set(j, t);
-      for (int t = lo2 + tid; t < hi2; t += 256) set(j, t);
+      set_range(j, lo1, hi1);
+      set_range(j, lo2, hi2);
     }
   }
   __syncthreads();
