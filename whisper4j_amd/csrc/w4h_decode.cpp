@@ -26,8 +26,18 @@ struct Mask {
   void set(int r, int t) {
     if (t >= 0 && t < V) bits[(size_t)r * mw + (t >> 5)] |= 1u << (t & 31);
   }
-  void range(int r, int lo, int hi) {  // [lo, hi)
-    for (int t = std::max(lo, 0); t < std::min(hi, V); t++) set(r, t);
+  void range(int r, int lo, int hi) {  // [lo, hi), whole words where the range covers them
+    lo = std::max(lo, 0);
+    hi = std::min(hi, V);
+    for (int t = lo; t < hi;) {
+      if ((t & 31) == 0 && t + 32 <= hi) {
+        bits[(size_t)r * mw + (t >> 5)] = 0xffffffffu;
+        t += 32;
+      } else {
+        set(r, t);
+        ++t;
+      }
+    }
   }
   bool get(int r, int t) const { return (bits[(size_t)r * mw + (t >> 5)] >> (t & 31)) & 1u; }
 };
