@@ -861,6 +861,7 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   probe_p.S = s->S;
   probe_p.d = d;
   probe_p.H = H;
+  probe_p.wq8 = m->wq8;  // the one-row layout depends on the weight type
   probe_p.ncs_max = s->ncs_max;
   probe_p.ncc = s->ncc;
   probe_p.rows_per_wg = s->rpw;

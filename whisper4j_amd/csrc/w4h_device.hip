@@ -78,7 +78,7 @@ __global__ void __launch_bounds__(kThreads) k_op_attention(const float* q, const
       part[c * kPartWords + i] = i == 0 ? pmv[0] : (i == 1 ? plv[0] : acc[i - 2]);
     lds_barrier();
   }
-  attn_merge(part, nc, 1, acc);
+  attn_merge<false>(part, nc, 1, acc);
   for (int i = threadIdx.x; i < kHeadDim; i += kThreads) out[h * kHeadDim + i] = acc[i];
 }
 
@@ -139,7 +139,8 @@ size_t step_lds_bytes(const StepParams& p, int grid) {
   if ((size_t)grid * S * 2 > reduce) reduce = (size_t)grid * S * 2;
   // out phases: one row keeps partials + reductions in big; several rows put partials, merged
   // output and reductions at the start of the region
-  const size_t out_one = S == 1 ? mp + 512 : 0;  // phase_out1: partials + two 256-float reductions
+  // phase_out1: partials (room for merge_chunks_1 chunks) + two 256-float reductions
+  const size_t out_one = S == 1 ? (size_t)merge_chunks_1(p) * p.H * kPartWords + 512 : 0;
   const size_t out_rows = S == 1 ? 0 : mp + (size_t)S * d + 2 * 32 * SM;
   size_t big = self_attn;
   big = big > cross_attn ? big : cross_attn;
@@ -148,7 +149,15 @@ size_t step_lds_bytes(const StepParams& p, int grid) {
   big = big > logits ? big : logits;
   big = big > reduce ? big : reduce;
   big = big > out_one ? big : out_one;
-  const size_t region = fixed + big > out_rows ? fixed + big : out_rows;
+  size_t region = fixed + big > out_rows ? fixed + big : out_rows;
+  if (S == 1 && p.wq8) {
+    // One-row q8_0 GEMV activation loads (xr_load) read a fixed span from xin (4d inputs of the
+    // second MLP matrix: 4 * DR rounds) and from xn (d inputs: DR rounds), past K when K is shorter.
+    const size_t ce = 16, dr = (size_t)step_rounds(d, p.wq8);
+    const size_t span_xin = 32 * 4 * dr * ce, span_xn = (size_t)4 * d + 32 * dr * ce;
+    if (region < span_xin) region = span_xin;
+    if (region < span_xn) region = span_xn;
+  }
   return (persistent + region) * sizeof(float);
 }
 

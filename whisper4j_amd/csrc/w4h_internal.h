@@ -17,6 +17,7 @@ constexpr int kMaxChunk = 256;   // longest key chunk an attention work item may
 constexpr int kResItems = 4;     // d-row items (8 rows each) one workgroup may own in a phase
 constexpr int kRep = 1;          // replicas of every exchange buffer (consumers poll blockIdx % kRep)
 constexpr int kPartWords = 2 + kHeadDim;            // (m, l, acc[64]) per attention partial
+constexpr int kMergeChunks = 8;                     // attention partials merged from registers
 constexpr int kSelWords = 6 + 2 * W4H_TOPK_MAX;     // per-workgroup selection partial
 
 // Device pointers of one decoder layer.  Matrices are [out][in] row-major; f16 matrices hold
@@ -72,6 +73,14 @@ struct StepParams {
   int nhist0, hist_cap;         // history length before the run; LDS history capacity (>= nhist0 + nsteps)
   size_t rules_off;             // byte offset of the rules region in dynamic LDS
 };
+
+// Attention partial chunks the one-row out phases keep room for in LDS: every chunk either
+// attention phase produces, and with q8_0 weights at least kMergeChunks (their attn_merge reads that
+// many slots; the f16 kernels re-read the last chunk instead and keep the LDS for resident rows).
+__host__ __device__ inline int merge_chunks_1(const StepParams& p) {
+  const int nc = p.ncs_max > p.ncc ? p.ncs_max : p.ncc;
+  return p.wq8 && nc < kMergeChunks ? kMergeChunks : nc;
+}
 
 // Ints of the rules region in LDS: history, then a bitmap over the workgroup's logits rows, then
 // the timestamp ranges (count + 4 [lo, hi) pairs); rounded to 16 bytes.

@@ -675,22 +675,29 @@ DEV void attn_compute(const KVRegs<KPT>& r, int n, int ns, const float* q, const
 }
 
 // Merge attention partials: part[(c * nrow + row) * kPartWords + w] for c < nc -> o[row*64 + e].
+// With nc <= kMergeChunks, PAD = true reads every chunk slot below kMergeChunks, in range or not (the
+// caller's partial area holds kMergeChunks chunks), so the reads need no per-chunk address select;
+// PAD = false re-reads the last chunk for the slots past it.  Slots at or past nc are left out of
+// the sums either way.
+template <bool PAD>
 DEV void attn_merge(const float* part, int nc, int nrow, float* o) {
-  constexpr int CM = 8;  // chunks merged from registers: every partial read before the sums
+  constexpr int CM = kMergeChunks;  // chunks merged from registers: every partial read before the sums
   if (nc <= CM) {
+    const int cs = nrow * kPartWords;
     for (int i = threadIdx.x; i < nrow * kHeadDim; i += kThreads) {
       const int row = i >> 6, e = i & 63;
+      const float* pp = part + row * kPartWords;
       float mv[CM], lv[CM], av[CM];
 #pragma unroll
       for (int c = 0; c < CM; ++c) {
-        const float* pp = part + (min(c, nc - 1) * nrow + row) * kPartWords;  // clamped: no branch
-        mv[c] = pp[0];
-        lv[c] = pp[1];
-        av[c] = pp[2 + e];
+        const float* pc = PAD ? pp + c * cs : part + (min(c, nc - 1) * nrow + row) * kPartWords;
+        mv[c] = pc[0];
+        lv[c] = pc[1];
+        av[c] = pc[2 + e];
       }
       float M = -INFINITY;
 #pragma unroll
-      for (int c = 0; c < CM; ++c) M = fmaxf(M, mv[c]);  // repeats of the last chunk leave it alone
+      for (int c = 0; c < CM; ++c) M = fmaxf(M, PAD && c >= nc ? -INFINITY : mv[c]);  // re-reads leave M alone
       float Lsum = 0.f, acc = 0.f;
 #pragma unroll
       for (int c = 0; c < CM; ++c) {
@@ -753,15 +760,20 @@ struct XR {
   float v[R][WQ8 ? 16 : 8];
 };
 
+// Chunks at or past K are zeroed.  With q8_0 weights every round reads x + (slot + 32 r) * CE, in
+// range or not, so that the R addresses are one base plus constant offsets: the q8_0 kernel is at
+// its register limit and otherwise spills the per-round addresses.  Those reads span 32 * R * CE
+// floats from x, which the step kernel's LDS sizing keeps inside the allocation (step_lds_bytes).
+// The f16 kernels read chunk 0 for the rounds past K.
 template <int R, int WQ8>
 DEV void xr_load(const float* x, int K, XR<R, WQ8>& X) {
   constexpr int CE = WQ8 ? 16 : 8;
   const int slot = ((threadIdx.x >> 6) << 3) | (threadIdx.x & 7);
+  const float* base = x + slot * CE;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int c = slot + 32 * r;
-    const bool ok = (c + 1) * CE <= K;
-    const float4* src = reinterpret_cast<const float4*>(x + (ok ? c * CE : 0));
+    const bool ok = (slot + 32 * r + 1) * CE <= K;
+    const float4* src = reinterpret_cast<const float4*>(WQ8 ? base + 32 * CE * r : x + (ok ? (slot + 32 * r) * CE : 0));
 #pragma unroll
     for (int q = 0; q < CE / 4; ++q) {
       const float4 t = src[q];
@@ -1601,7 +1613,7 @@ DEV bool phase_out(const StepParams& p, const Lds& m, const StepCtx& c, int l, G
   const u64* psrc = cross ? p.cp + (size_t)l * p.ncc * S * H * kPartWords : p.sp + (size_t)l * p.ncs_max * S * H * kPartWords;
   if (!ll_poll1<16>(rep(p, psrc), nc * S * H * kPartWords, part, c.tag, p.err)) return false;
   STAMP(1);
-  attn_merge(part, nc, S * H, o);
+  attn_merge<false>(part, nc, S * H, o);
   u64* xout = (cross ? p.x2 : p.x1) + (size_t)l * S * d;
   for (int b = 0; b < nmine; ++b) {
     if (b > 0) {
@@ -2123,13 +2135,13 @@ DEV bool phase_out1(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
     bv = bias[row_of(0)];
     if (emb_res) pv = p.pos[(size_t)c.pe * d + row_of(0)];
   }
-  float* part = m.big;
-  float* red = part + (size_t)(p.ncs_max > p.ncc ? p.ncs_max : p.ncc) * H * kPartWords;  // [2][256]
+  float* part = m.big;  // [merge_chunks_1(p)][H][kPartWords]
+  float* red = part + (size_t)merge_chunks_1(p) * H * kPartWords;  // [2][256]
   const int nc = cross ? p.ncc : (c.kv + kSelfChunk - 1) / kSelfChunk + 1;
   const u64* psrc = cross ? p.cp + (size_t)l * p.ncc * H * kPartWords : p.sp + (size_t)l * p.ncs_max * H * kPartWords;
   if (!ll_poll1<16>(rep(p, psrc), nc * H * kPartWords, part, c.tag, p.err)) return false;
   STAMP(1);
-  attn_merge(part, nc, H, m.xn);
+  attn_merge<WQ8 != 0>(part, nc, H, m.xn);  // q8_0: the padded reads keep the kernel from spilling
   XR<R, WQ8> X;
   xr_load<R, WQ8>(m.xn, d, X);
   u64* xout = (cross ? p.x2 : p.x1) + (size_t)l * d;
