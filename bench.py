@@ -310,8 +310,8 @@ def main():
     ap.add_argument("--cpu-max-sweeps", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the tiny/small/turbo/medium lines")
-    ap.add_argument("--only", choices=["turbo", "small-beam-rows", "greedy-driver"],
-                    help="run only this other workload (one JSON line; for profiling the batched engine)")
+    ap.add_argument("--only", choices=["turbo", "small-beam-rows", "greedy-driver", "medium", "tiny"],
+                    help="run only this other workload (one JSON line; for profiling it alone)")
     ap.add_argument("--only-steps", type=int, default=224, help="forced steps of the --only workload")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run a plain copy of this many MiB (counter calibration for rocprofv3 --pmc)")
@@ -339,6 +339,12 @@ def main():
         if args.only == "turbo":
             tps, us, frac, setup = measure_forced(w4h, synth, "large-v3-turbo", "f16", n, 2, n_rows=32, n_encoders=32)
             work = f"large-v3-turbo 32 streams (own encoder each) in lockstep, {n} forced steps"
+        elif args.only == "medium":
+            tps, us, frac, setup = measure_forced(w4h, synth, "medium", "q8_0", n, 2)
+            work = f"medium q8_0 greedy b=1, {n} forced steps"
+        elif args.only == "tiny":
+            tps, us, frac, setup = measure_forced(w4h, synth, "tiny.en", "f16", n, 5)
+            work = f"tiny.en greedy b=1, {n} forced steps"
         else:
             tps, us, frac, setup = measure_forced(w4h, synth, "small", "f16", n, 2, n_rows=5, n_encoders=1)
             work = f"small 5 beam rows on one encoder, {n} forced steps"
