@@ -764,13 +764,15 @@ int create_wide(std::unique_ptr<w4h_session>& s, const hipDeviceProp_t& prop, w4
   size_t pmax = 0;
   for (const WideGemm* g : {&s->g_qkv, &s->g_o, &s->g_1, &s->g_2, &s->g_v})
     pmax = std::max(pmax, (size_t)g->ks * s->Rp * g->N);
-  // cross-attention chunks: enough (encoder, head, chunk) workgroups for two per compute unit,
-  // chunks of at least 64 keys
+  // cross-attention chunks: enough (encoder, head, chunk) workgroups for two per compute unit, but
+  // no more than ceil(A / kWideKeysPerPass), the fewest that keep every chunk within one pass of the
+  // kernel's key loop: more, shorter chunks only add partials to merge (small, 5 rows: 751 us per
+  // step with 23 chunks of 66 keys, 731 with 12 of 125)
   const int ngroups = s->X == s->S ? 1 : (s->S + 7) / 8;
   int per_cu = 2;  // W4H_XWG overrides the cross-attention workgroups per compute unit (tuning)
   if (const char* e = getenv("W4H_XWG")) per_cu = std::max(1, std::min(16, atoi(e)));
   int nch = (per_cu * ncu + s->X * H * ngroups - 1) / (s->X * H * ngroups);
-  nch = std::max(1, std::min(nch, A / 64));
+  nch = std::max(1, std::min(std::min(nch, (A + kWideKeysPerPass - 1) / kWideKeysPerPass), 64));  // k_w_cmerge: <= 64
   s->chlen = (A + nch - 1) / nch;
   s->nch = (A + s->chlen - 1) / s->chlen;
   s->nsel = (V + kWideSelChunk - 1) / kWideSelChunk;

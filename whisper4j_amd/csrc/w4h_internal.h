@@ -99,6 +99,7 @@ inline int step_rounds(int d, int wq8) { return wq8 ? 2 : (d <= 512 ? 2 : 3); }
 // kWideMaxRows) run as a sequence of ordinary kernels per token step, with every projection an MFMA
 // GEMM over all rows.  Row counts are padded to Rp = 16 or 32 (one or two 16-row MFMA tiles).
 constexpr int kWideMaxRows = 32;
+constexpr int kWideKeysPerPass = 128;  // keys one pass of the batched cross-attention key loop covers
 constexpr int kWideCols = 64;        // output columns per GEMM workgroup (16 per wave)
 constexpr int kWideKBlock = 128;     // k per block: four 16x16x32 MFMA steps
 constexpr int kWideSelChunk = 512;   // vocabulary entries per selection partial (one wave)

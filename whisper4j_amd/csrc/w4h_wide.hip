@@ -309,6 +309,7 @@ __global__ __launch_bounds__(256) void k_w_gelu(const WideCtl* __restrict__ ctl,
 // formed (they do not depend on it), so one memory round trip covers them; longer contexts loop.
 
 constexpr int kKeysInFlight = 4;   // keys per lane group in flight (cross-attention loops)
+static_assert(32 * kKeysInFlight == kWideKeysPerPass, "one key-loop pass: 32 lane groups x kKeysInFlight");
 constexpr int kSelfKF = 16;        // keys per lane group loaded up front (self-attention)
 constexpr int kSelfBlock = 32 * kSelfKF;
 
