@@ -130,6 +130,11 @@ int w4h_session_reset(w4h_session* s, int32_t kv_len);
 int w4h_session_kv_len(const w4h_session* s, int32_t* kv_len);
 /* Tokens set to -inf before selection on every following step (static suppress list). */
 int w4h_session_set_suppress(w4h_session* s, const int32_t* ids, int32_t n);
+/* A fixed bias [n_vocab] added to every row's raw logits before any mask or selection, on every
+ * following step (NULL switches it off).  The reference has no counterpart: it serves the beam-search
+ * workload whose selection is made deterministic by a seeded logit bias.  step_out, logits and the
+ * decode drivers all see the biased logits. */
+int w4h_session_set_logit_bias(w4h_session* s, const float* bias);
 /* Token whose raw logit is reported in w4h_step_out.probe_logit (e.g. <|nospeech|>), -1 for none. */
 int w4h_session_set_probe(w4h_session* s, int32_t token);
 
@@ -216,6 +221,7 @@ int w4h_op_attention(const float* q, const uint16_t* k, const uint16_t* v, int32
 /* Selection over rows of logits [rows][n]: mask (nullable bitmask [rows][ceil(n/32)]) -> argmax,
  * logsumexp and top-k (k <= W4H_TOPK_MAX). */
 int w4h_op_select(const float* logits, int32_t rows, int32_t n, const uint32_t* mask, int32_t k, w4h_step_out* out);
+
 
 #ifdef __cplusplus
 }

@@ -40,6 +40,15 @@ class OrcResult(ctypes.Structure):
                 "temperature": self.temperature}
 
 
+_PREFILL = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, _f32p, _f32p)
+_STEP = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int32, _f32p)
+_REARRANGE = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, _i32p, ctypes.c_int, ctypes.c_int)
+
+
+class OrcOps(ctypes.Structure):
+    _fields_ = [("ctx", ctypes.c_void_p), ("prefill", _PREFILL), ("step", _STEP), ("rearrange", _REARRANGE)]
+
+
 def build() -> None:
     subprocess.run(["make", "-s", "-C", _HERE], check=True)
 
@@ -82,6 +91,28 @@ def lib():
                                                ctypes.c_int, ctypes.c_uint64, ctypes.POINTER(OrcResult)]
         L.orc_forced.argtypes = [ctypes.c_void_p, _f32p, _i32p, ctypes.c_int, _i32p, ctypes.c_int, _i32p, _f32p,
                                  _f32p, _f32p, _f32p]
+        L.orc_model_set_logit_bias.argtypes = [ctypes.c_void_p, _f32p]
+        L.orc_suppress_blank.argtypes = [_f32p, ctypes.c_int, ctypes.c_int]
+        L.orc_apply_suppress.argtypes = [_f32p, _i32p, ctypes.c_int, ctypes.c_int]
+        L.orc_ngram_block.argtypes = [_f32p, _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.orc_timestamp_rules.argtypes = [_f32p, _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int]
+        L.orc_needs_fallback.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_float]
+        L.orc_sample_u.argtypes = [_f32p, ctypes.c_int, ctypes.c_float, ctypes.c_double]
+        L.orc_splitmix64_next.restype = ctypes.c_uint64
+        L.orc_splitmix64_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        L.orc_rng_uniform.restype = ctypes.c_double
+        L.orc_rng_uniform.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        L.orc_fallback_pick.argtypes = [ctypes.POINTER(OrcResult), ctypes.POINTER(ctypes.c_int)]
+        L.orc_greedy_drive.argtypes = [ctypes.POINTER(OrcOps), ctypes.c_int, ctypes.c_int, ctypes.c_int, _i32p,
+                                       ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_uint64,
+                                       ctypes.POINTER(OrcResult)]
+        L.orc_beam_drive.argtypes = [ctypes.POINTER(OrcOps), ctypes.c_int, ctypes.c_int, ctypes.c_int, _i32p,
+                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(OrcResult),
+                                     ctypes.POINTER(ctypes.c_double)]
+        L.orc_decode_beam_gaps.argtypes = [ctypes.c_void_p, _f32p, _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                           _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                           ctypes.POINTER(OrcResult), ctypes.POINTER(ctypes.c_double)]
         _lib = L
     return _lib
 
@@ -192,6 +223,124 @@ def f32_to_f16(f: float) -> int:
     return int(lib().orc_f32_to_f16(ctypes.c_float(f)))
 
 
+# ---- logit rules (each returns a copy of the row with the rule applied) ----------------------
+
+def suppress_blank(row, eot):
+    r = f32(row).copy()
+    lib().orc_suppress_blank(_p(r), r.size, eot)
+    return r
+
+
+def apply_suppress(row, ids):
+    r, i = f32(row).copy(), i32(list(ids))
+    lib().orc_apply_suppress(_p(r), _p(i, _i32p), i.size, r.size)
+    return r
+
+
+def ngram_block(row, generated, n):
+    r, g = f32(row).copy(), i32(list(generated) or [0])
+    lib().orc_ngram_block(_p(r), _p(g, _i32p), len(generated), n, r.size)
+    return r
+
+
+def timestamp_rules(row, generated, ts_begin, eot, first_step=False):
+    r, g = f32(row).copy(), i32(list(generated) or [0])
+    lib().orc_timestamp_rules(_p(r), _p(g, _i32p), len(generated), ts_begin, eot, r.size, int(first_step))
+    return r
+
+
+def needs_fallback(compression_ratio, avg_logprob, no_speech_prob) -> bool:
+    return bool(lib().orc_needs_fallback(compression_ratio, avg_logprob, no_speech_prob))
+
+
+def sample_u(row, temperature, u):
+    """(chosen index, the row after the call: the reference overwrites it with exp weights)"""
+    r = f32(row).copy()
+    k = lib().orc_sample_u(_p(r), r.size, ctypes.c_float(temperature), ctypes.c_double(u))
+    return int(k), r
+
+
+def splitmix64(seed, n):
+    st = ctypes.c_uint64(seed)
+    return [int(lib().orc_splitmix64_next(ctypes.byref(st))) for _ in range(n)]
+
+
+def rng_uniform(seed, n):
+    st = ctypes.c_uint64(seed)
+    return [float(lib().orc_rng_uniform(ctypes.byref(st))) for _ in range(n)]
+
+
+def fallback_pick(results):
+    """results: six dicts (compression_ratio, avg_logprob, no_speech_prob) decoded at 0, 0.2 .. 1.0.
+    Returns (index decodeWithFallback returns, number of decodes it runs)."""
+    arr = (OrcResult * 6)()
+    for i, r in enumerate(results):
+        arr[i].n_tokens = 1
+        arr[i].tokens[0] = i
+        arr[i].compression_ratio = r["compression_ratio"]
+        arr[i].avg_logprob = r["avg_logprob"]
+        arr[i].no_speech_prob = r["no_speech_prob"]
+        arr[i].temperature = 0.2 * i
+    used = ctypes.c_int(0)
+    k = lib().orc_fallback_pick(arr, ctypes.byref(used))
+    return int(k), int(used.value)
+
+
+class TableSource:
+    """Logits source for the decode drivers from a function of each hypothesis's generated tokens:
+    rows(tuple_of_generated_tokens) -> logits row; first_row is the prompt's first-position row."""
+
+    def __init__(self, n_vocab, rows, first_row=None):
+        self.V, self.rows = n_vocab, rows
+        self.first = f32(first_row if first_row is not None else np.zeros(n_vocab))
+        self.hist = [()]
+        self.calls = []
+
+        def prefill(ctx, first, last):
+            self.hist = [()]
+            ctypes.memmove(first, self.first.ctypes.data, 4 * self.V)
+            r = f32(self.rows(()))
+            ctypes.memmove(last, r.ctypes.data, 4 * self.V)
+            return 0
+
+        def step(ctx, b, tok, out):
+            self.hist[b] = self.hist[b] + (int(tok),)
+            self.calls.append((b, self.hist[b]))
+            r = f32(self.rows(self.hist[b]))
+            ctypes.memmove(out, r.ctypes.data, 4 * self.V)
+            return 0
+
+        def rearrange(ctx, src, saved, beam):
+            old = list(self.hist) + [()] * (beam - len(self.hist))
+            new = [old[src[b]] for b in range(saved)]
+            new += [new[0]] * (beam - saved)
+            self.hist = new
+            return 0
+
+        self._cb = (_PREFILL(prefill), _STEP(step), _REARRANGE(rearrange))
+        self.ops = OrcOps(None, *self._cb)
+
+
+def greedy_drive(src, eot, max_tokens, suppress=(), no_speech=-1, temperature=0.0, ts_begin=-1, seed=0):
+    s = i32(list(suppress) or [0])
+    r = OrcResult()
+    rc = lib().orc_greedy_drive(ctypes.byref(src.ops), src.V, eot, max_tokens, _p(s, _i32p), len(suppress), no_speech,
+                                ctypes.c_float(temperature), ts_begin, ctypes.c_uint64(seed), ctypes.byref(r))
+    if rc:
+        raise ValueError(f"orc_greedy_drive failed ({rc})")
+    return r.as_dict()
+
+
+def beam_drive(src, eot, max_tokens, beam, suppress=(), no_speech=-1, ts_begin=-1):
+    s = i32(list(suppress) or [0])
+    r = OrcResult()
+    rc = lib().orc_beam_drive(ctypes.byref(src.ops), src.V, eot, max_tokens, _p(s, _i32p), len(suppress), no_speech,
+                              ts_begin, beam, ctypes.byref(r), None)
+    if rc:
+        raise ValueError(f"orc_beam_drive failed ({rc})")
+    return r.as_dict()
+
+
 # ---- model ---------------------------------------------------------------------------------
 
 class Model:
@@ -229,6 +378,11 @@ class Model:
             self.close()
         except Exception:
             pass
+
+    def set_logit_bias(self, bias):
+        """Fixed bias [n_vocab] added to every logits row (None: off)."""
+        self._bias = None if bias is None else f32(bias)
+        lib().orc_model_set_logit_bias(self.h, _p(self._bias))
 
     def new_cache(self):
         return Cache(self)
@@ -271,6 +425,19 @@ class Model:
         if rc:
             raise ValueError(f"orc_decode_beam failed ({rc})")
         return r.as_dict()
+
+    def decode_beam_gaps(self, xa, prompt, eot, max_tokens, suppress=(), no_speech=-1, ts_begin=-1, beam=5):
+        """decode_beam plus its decision gaps: gaps[i] (search step i) = score of the last hypothesis kept
+        minus the first non-end candidate left out, gaps[0] = the final pick's margin."""
+        p, s, xa = i32(prompt), i32(list(suppress)), f32(xa)
+        r = OrcResult()
+        g = np.empty(max_tokens, np.float64)
+        rc = lib().orc_decode_beam_gaps(self.h, _p(xa), _p(p, _i32p), p.size, eot, max_tokens, _p(s, _i32p), s.size,
+                                        no_speech, ts_begin, beam, ctypes.byref(r),
+                                        g.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+        if rc:
+            raise ValueError(f"orc_decode_beam_gaps failed ({rc})")
+        return r.as_dict(), g
 
     def decode_with_fallback(self, xa, prompt, eot, max_tokens, suppress=(), no_speech=-1, ts_begin=-1, beam=1,
                              seed=0):

@@ -290,6 +290,7 @@ struct orc_model {
   float* pos_emb; /* [ctx][d] */
   float *ln_g, *ln_b;
   orc_block* blocks;
+  float* logit_bias; /* [V] added to every logits row, or NULL */
 };
 
 static const orc_tensor* find_tensor(const orc_tensor* t, int n, const char* name) {
@@ -362,6 +363,7 @@ void orc_model_destroy(orc_model* m) {
   free(m->pos_emb);
   free(m->ln_g);
   free(m->ln_b);
+  free(m->logit_bias);
   if (m->blocks) {
     for (int i = 0; i < m->d.n_text_layer; i++) {
       orc_block* b = &m->blocks[i];
@@ -429,6 +431,17 @@ orc_model* orc_model_create(const orc_dims* dims, const orc_tensor* tab, int nta
 fail:
   orc_model_destroy(m);
   return NULL;
+}
+
+/* A fixed logit bias (the beam workload's seeded bias; not part of the reference): added to the
+ * raw logits of every row after the tied projection, before any rule or selection. */
+void orc_model_set_logit_bias(orc_model* m, const float* bias) {
+  free(m->logit_bias);
+  m->logit_bias = NULL;
+  if (bias) {
+    m->logit_bias = (float*)malloc(sizeof(float) * (size_t)m->d.n_vocab);
+    memcpy(m->logit_bias, bias, sizeof(float) * (size_t)m->d.n_vocab);
+  }
 }
 
 /* ------------------------------------------------------------------------------------------ */
@@ -674,6 +687,9 @@ int orc_forward(const orc_model* m, const int32_t* tokens, int n, const float* x
   for (int t = 0; t < n; t++)
     for (int v = 0; v < V; v++)
       logits[(size_t)t * V + v] = orc_dot(h + (size_t)t * d, m->tok_emb + (size_t)v * d, d) * 1.0f;
+  if (m->logit_bias)
+    for (int t = 0; t < n; t++)
+      for (int v = 0; v < V; v++) logits[(size_t)t * V + v] = logits[(size_t)t * V + v] + m->logit_bias[v];
   if (tmp) orc_cache_destroy(tmp);
   free(x); free(h); free(a); free(f);
   return 0;
@@ -700,18 +716,21 @@ static double log_softmax_at(const float* l, int n, int index) { /* :614-626 */
   return (double)(l[index] - max) - log(logSum);
 }
 
-static void suppress_blank(float* l, int n, int eot) { /* :450-455 */
+/* suppressBlank :450-455 */
+void orc_suppress_blank(float* l, int n, int eot) {
   l[eot] = -INFINITY;
   if (220 < n) l[220] = -INFINITY;
 }
 
-static void apply_suppress(float* l, const int32_t* s, int ns, int n) { /* :457-466 */
+/* applySuppress :457-466 */
+void orc_apply_suppress(float* l, const int32_t* s, int ns, int n) {
   if (!s) return;
   for (int i = 0; i < ns; i++)
     if (s[i] >= 0 && s[i] < n) l[s[i]] = -INFINITY;
 }
 
-static void ngram_block(float* l, const int32_t* g, int cnt, int nn, int nvocab) { /* :543-564 */
+/* applyNgramBlock :543-564 */
+void orc_ngram_block(float* l, const int32_t* g, int cnt, int nn, int nvocab) {
   if (cnt < nn - 1) return;
   for (int i = 0; i <= cnt - nn; i++) {
     int match = 1;
@@ -724,13 +743,14 @@ static void ngram_block(float* l, const int32_t* g, int cnt, int nn, int nvocab)
   }
 }
 
-static void repetition_penalty(float* l, const int32_t* g, int cnt, int nvocab) { /* :472-476 */
-  ngram_block(l, g, cnt, 3, nvocab);
-  ngram_block(l, g, cnt, 4, nvocab);
+/* applyRepetitionPenalty :472-476 */
+static void repetition_penalty(float* l, const int32_t* g, int cnt, int nvocab) {
+  orc_ngram_block(l, g, cnt, 3, nvocab);
+  orc_ngram_block(l, g, cnt, 4, nvocab);
 }
 
-static void timestamp_rules(float* l, const int32_t* g, int cnt, int tsb, int eot, int nvocab, int first) {
-  /* :484-541 */
+/* applyTimestampRules :484-541 */
+void orc_timestamp_rules(float* l, const int32_t* g, int cnt, int tsb, int eot, int nvocab, int first) {
   if (tsb > 0 && tsb - 1 >= 0 && tsb - 1 < nvocab) l[tsb - 1] = -INFINITY;
   if (first) {
     for (int i = 0; i < tsb && i < nvocab; i++) l[i] = -INFINITY;
@@ -757,17 +777,21 @@ static void timestamp_rules(float* l, const int32_t* g, int cnt, int tsb, int eo
   }
 }
 
-/* Math.random() replaced by a seeded SplitMix64 -> [0,1) so runs repeat (the reference's draw is
- * unseeded). */
-static double rng_uniform(uint64_t* s) {
+/* Math.random() replaced by a seeded SplitMix64 (Steele, Lea and Flood, "Fast splittable
+ * pseudorandom number generators", OOPSLA 2014; the constants of Vigna's splitmix64.c) so runs
+ * repeat; the reference's draw is unseeded.  The top 53 bits make a double in [0, 1). */
+uint64_t orc_splitmix64_next(uint64_t* s) {
   uint64_t z = (*s += 0x9e3779b97f4a7c15ull);
   z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
   z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
-  z ^= z >> 31;
-  return (double)(z >> 11) * (1.0 / 9007199254740992.0);
+  return z ^ (z >> 31);
 }
 
-static int sample_tok(float* l, int n, float temperature, uint64_t* rng) { /* :576-598 (mutates l) */
+double orc_rng_uniform(uint64_t* s) { return (double)(orc_splitmix64_next(s) >> 11) * (1.0 / 9007199254740992.0); }
+
+/* sample :576-598 with the uniform draw u given (mutates l: the reference overwrites the logits
+ * with the unnormalised probabilities). */
+int orc_sample_u(float* l, int n, float temperature, double u) {
   float max = -INFINITY;
   for (int i = 0; i < n; i++)
     if (l[i] > max) max = l[i];
@@ -777,7 +801,7 @@ static int sample_tok(float* l, int n, float temperature, uint64_t* rng) { /* :5
     l[i] = (float)p;
     sum += p;
   }
-  double r = rng_uniform(rng) * sum;
+  double r = u * sum;
   double cum = 0;
   for (int i = 0; i < n; i++) {
     cum += l[i];
@@ -786,46 +810,47 @@ static int sample_tok(float* l, int n, float temperature, uint64_t* rng) { /* :5
   return n - 1;
 }
 
+/* needsFallback :435-440 */
+int orc_needs_fallback(float compression_ratio, float avg_logprob, float no_speech_prob) {
+  if (compression_ratio > 2.4f) return !(no_speech_prob > 0.6f && avg_logprob < -1.0f);
+  return avg_logprob < -1.0f && !(no_speech_prob > 0.6f);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Decode drivers over a logits source.  The model-backed source below runs orc_forward with one
+ * KV cache per hypothesis; tests drive the same drivers from hand-built logit tables.           */
+
 /* WhisperDecoder.decode: main/nn/WhisperDecoder.java:161-204 */
-int orc_decode(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, int eot, int max_tokens,
-               const int32_t* suppress, int n_suppress, int no_speech, float temperature, int ts_begin,
-               uint64_t seed, orc_result* out) {
-  int V = m->d.n_vocab;
-  if (max_tokens > 1024) return -3;
-  orc_cache* cache = orc_cache_create(m);
+int orc_greedy_drive(const orc_ops* ops, int V, int eot, int max_tokens, const int32_t* suppress, int n_suppress,
+                     int no_speech, float temperature, int ts_begin, uint64_t seed, orc_result* out) {
+  if (max_tokens > 1024 || max_tokens < 0) return -3;
   int32_t generated[1024];
   int genCount = 0;
   double sumLogprob = 0;
   float noSpeechProb = 0;
   uint64_t rng = seed;
-  const int32_t* cur = prompt;
-  int ncur = n_prompt;
-  int32_t one;
-  float* logits = (float*)malloc(sizeof(float) * (size_t)(n_prompt > 1 ? n_prompt : 1) * V);
+  float* first = (float*)malloc(sizeof(float) * (size_t)V);
+  float* last = (float*)malloc(sizeof(float) * (size_t)V);
+  int rc = 0;
   for (int step = 0; step < max_tokens; step++) {
-    if (orc_forward(m, cur, ncur, xa, cache, logits)) {
-      free(logits);
-      orc_cache_destroy(cache);
-      return -1;
-    }
-    float* last = logits + (size_t)(ncur - 1) * V;
+    rc = step == 0 ? ops->prefill(ops->ctx, first, last) : ops->step(ops->ctx, 0, generated[genCount - 1], last);
+    if (rc) break;
     if (step == 0) {
-      noSpeechProb = (no_speech < 0 || no_speech >= V) ? 0.0f : softmax_at(logits, V, no_speech);
-      suppress_blank(last, V, eot);
+      /* collectNoSpeechProb reads logits row 0 (:442-448) */
+      noSpeechProb = (no_speech < 0 || no_speech >= V) ? 0.0f : softmax_at(first, V, no_speech);
+      orc_suppress_blank(last, V, eot);
     }
-    apply_suppress(last, suppress, n_suppress, V);
+    orc_apply_suppress(last, suppress, n_suppress, V);
     repetition_penalty(last, generated, genCount, V);
-    if (ts_begin > 0) timestamp_rules(last, generated, genCount, ts_begin, eot, V, step == 0);
-    int best = temperature == 0.0f ? orc_argmax(last, V) : sample_tok(last, V, temperature, &rng);
+    if (ts_begin > 0) orc_timestamp_rules(last, generated, genCount, ts_begin, eot, V, step == 0);
+    int best = temperature == 0.0f ? orc_argmax(last, V) : orc_sample_u(last, V, temperature, orc_rng_uniform(&rng));
     sumLogprob += log_softmax_at(last, V, best);
     if (best == eot) break;
     generated[genCount++] = best;
-    one = best;
-    cur = &one;
-    ncur = 1;
   }
-  free(logits);
-  orc_cache_destroy(cache);
+  free(first);
+  free(last);
+  if (rc) return rc;
   out->n_tokens = genCount;
   memcpy(out->tokens, generated, sizeof(int32_t) * (size_t)genCount);
   out->avg_logprob = genCount > 0 ? (float)(sumLogprob / genCount) : 0.0f;
@@ -841,47 +866,51 @@ typedef struct {
 } cand_t;
 
 /* WhisperDecoder.decodeBeam: main/nn/WhisperDecoder.java:214-394 */
-int orc_decode_beam(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, int eot,
-                    int max_tokens, const int32_t* suppress, int n_suppress, int no_speech, int ts_begin, int beam,
-                    orc_result* out) {
-  int V = m->d.n_vocab;
-  if (max_tokens > 1024 || beam < 1 || beam > 16) return -3;
-  orc_cache** caches = (orc_cache**)calloc((size_t)beam, sizeof(orc_cache*));
+int orc_beam_drive(const orc_ops* ops, int V, int eot, int max_tokens, const int32_t* suppress, int n_suppress,
+                   int no_speech, int ts_begin, int beam, orc_result* out, double* gaps) {
+  if (max_tokens > 1024 || max_tokens < 1 || beam < 1 || beam > 16) return -3;
   int32_t(*toks)[1024] = calloc((size_t)beam, sizeof(*toks));
   int* lens = (int*)calloc((size_t)beam, sizeof(int));
   double* lps = (double*)calloc((size_t)beam, sizeof(double));
-  int maxfin = beam + beam * (beam + 1) + 1;
+  int maxfin = beam + 1;
   int32_t(*fin_t)[1024] = calloc((size_t)maxfin, sizeof(*fin_t));
   int* fin_len = (int*)calloc((size_t)maxfin, sizeof(int));
   double* fin_lp = (double*)calloc((size_t)maxfin, sizeof(double));
   int nfin = 0;
-  float* logits = (float*)malloc(sizeof(float) * (size_t)(n_prompt > 1 ? n_prompt : 1) * V);
+  float* first = (float*)malloc(sizeof(float) * (size_t)V);
+  float* logits = (float*)malloc(sizeof(float) * (size_t)V);
   float* lp = (float*)malloc(sizeof(float) * (size_t)V);
   int32_t* top = (int32_t*)malloc(sizeof(int32_t) * (size_t)(beam + 1));
   cand_t* cands = (cand_t*)malloc(sizeof(cand_t) * (size_t)beam * (beam + 1));
-  caches[0] = orc_cache_create(m);
-  orc_forward(m, prompt, n_prompt, xa, caches[0], logits);
-  float noSpeechProb = (no_speech < 0 || no_speech >= V) ? 0.0f : softmax_at(logits, V, no_speech);
-  float* last0 = logits + (size_t)(n_prompt - 1) * V;
-  suppress_blank(last0, V, eot);
-  apply_suppress(last0, suppress, n_suppress, V);
-  orc_log_softmax(last0, V, lp);
+  int32_t(*ntoks)[1024] = calloc((size_t)beam, sizeof(*ntoks));
+  int* nlens = (int*)calloc((size_t)beam, sizeof(int));
+  double* nlps = (double*)calloc((size_t)beam, sizeof(double));
+  int32_t* src = (int32_t*)calloc((size_t)beam, sizeof(int32_t));
+  float noSpeechProb = 0.0f;
+  if (gaps)
+    for (int i = 0; i < max_tokens; i++) gaps[i] = INFINITY;
+  int rc = ops->prefill(ops->ctx, first, logits);
+  if (rc) goto done;
+  noSpeechProb = (no_speech < 0 || no_speech >= V) ? 0.0f : softmax_at(first, V, no_speech);
+  orc_suppress_blank(logits, V, eot);
+  orc_apply_suppress(logits, suppress, n_suppress, V);
+  orc_log_softmax(logits, V, lp);
   orc_topk(lp, V, beam, top);
   for (int b = 0; b < beam; b++) {
     toks[b][0] = top[b];
     lens[b] = 1;
     lps[b] = (double)lp[top[b]];
-    if (b > 0) caches[b] = cache_copy(caches[0]); /* cross + self entries shared by reference */
+    src[b] = 0; /* every beam starts from the prompt's cache (:260-266) */
   }
+  if ((rc = ops->rearrange(ops->ctx, src, beam, beam))) goto done;
   for (int step = 1; step < max_tokens; step++) {
     int nc = 0;
     for (int b = 0; b < beam; b++) {
       if (toks[b][lens[b] - 1] == eot) continue;
-      int32_t lt = toks[b][lens[b] - 1];
-      orc_forward(m, &lt, 1, xa, caches[b], logits);
-      apply_suppress(logits, suppress, n_suppress, V);
+      if ((rc = ops->step(ops->ctx, b, toks[b][lens[b] - 1], logits))) goto done;
+      orc_apply_suppress(logits, suppress, n_suppress, V);
       repetition_penalty(logits, toks[b], lens[b], V);
-      if (ts_begin > 0) timestamp_rules(logits, toks[b], lens[b], ts_begin, eot, V, 0);
+      if (ts_begin > 0) orc_timestamp_rules(logits, toks[b], lens[b], ts_begin, eot, V, 0);
       orc_log_softmax(logits, V, lp);
       orc_topk(lp, V, beam + 1, top);
       for (int k = 0; k < beam + 1; k++) {
@@ -902,14 +931,13 @@ int orc_decode_beam(const orc_model* m, const float* xa, const int32_t* prompt, 
       }
       cands[j + 1] = c;
     }
-    int32_t(*ntoks)[1024] = calloc((size_t)beam, sizeof(*ntoks));
-    int* nlens = (int*)calloc((size_t)beam, sizeof(int));
-    double* nlps = (double*)calloc((size_t)beam, sizeof(double));
-    int* src = (int*)calloc((size_t)beam, sizeof(int));
     int saved = 0;
     for (int ci = 0; ci < nc; ci++) {
       int sb = cands[ci].beam, tok = cands[ci].tok;
       double score = cands[ci].score;
+      /* decision margin of this step: the last hypothesis kept against the first non-end candidate
+       * left out (test instrumentation, not part of the reference's algorithm) */
+      if (gaps && tok != eot && saved == beam && gaps[step] == INFINITY) gaps[step] = nlps[beam - 1] - score;
       if (tok == eot) {
         memcpy(fin_t[nfin], toks[sb], sizeof(int32_t) * (size_t)lens[sb]);
         fin_len[nfin] = lens[sb];
@@ -926,98 +954,219 @@ int orc_decode_beam(const orc_model* m, const float* xa, const int32_t* prompt, 
       src[saved] = sb;
       saved++;
     }
-    int stop = (saved == 0 || nfin >= beam);
-    if (!stop) {
-      orc_cache** nc2 = (orc_cache**)calloc((size_t)beam, sizeof(orc_cache*));
-      for (int b = 0; b < saved; b++) {
-        if (src[b] == b) {
-          nc2[b] = caches[b];
-          caches[b]->refs++;
-        } else {
-          nc2[b] = cache_copy(caches[src[b]]);
-        }
+    if (saved == 0 || nfin >= beam) break;
+    for (int b = saved; b < beam; b++) { /* leftover beams continue new beam 0 (:356-361) */
+      memcpy(ntoks[b], ntoks[0], sizeof(int32_t) * (size_t)nlens[0]);
+      nlens[b] = nlens[0];
+      nlps[b] = nlps[0];
+      src[b] = -1;
+    }
+    if ((rc = ops->rearrange(ops->ctx, src, saved, beam))) goto done;
+    memcpy(toks, ntoks, sizeof(*toks) * (size_t)beam);
+    memcpy(lens, nlens, sizeof(int) * (size_t)beam);
+    memcpy(lps, nlps, sizeof(double) * (size_t)beam);
+  }
+  for (int b = 0; b < beam && nfin < beam; b++) { /* unfinished beams fill the list (:370-377) */
+    memcpy(fin_t[nfin], toks[b], sizeof(int32_t) * (size_t)lens[b]);
+    fin_len[nfin] = lens[b];
+    fin_lp[nfin] = lps[b];
+    nfin++;
+  }
+  {
+    int bestIdx = 0;
+    double bestScore = -INFINITY, second = -INFINITY;
+    for (int i = 0; i < nfin; i++) { /* MaximumLikelihoodRanker (:379-388) */
+      double score = fin_lp[i] / (double)(fin_len[i] > 1 ? fin_len[i] : 1);
+      if (score > bestScore) {
+        second = bestScore;
+        bestScore = score;
+        bestIdx = i;
+      } else if (score > second) {
+        second = score;
       }
-      for (int b = saved; b < beam; b++) { /* leftover beams alias beam 0's map (:356-361) */
-        nc2[b] = nc2[0];
-        nc2[0]->refs++;
-        memcpy(ntoks[b], ntoks[0], sizeof(int32_t) * (size_t)nlens[0]);
-        nlens[b] = nlens[0];
-        nlps[b] = nlps[0];
-      }
-      for (int b = 0; b < beam; b++) orc_cache_destroy(caches[b]);
-      free(caches);
-      caches = nc2;
-      memcpy(toks, ntoks, sizeof(*toks) * (size_t)beam);
-      memcpy(lens, nlens, sizeof(int) * (size_t)beam);
-      memcpy(lps, nlps, sizeof(double) * (size_t)beam);
     }
-    free(ntoks); free(nlens); free(nlps); free(src);
-    if (stop) break;
+    if (gaps) gaps[0] = bestScore - second; /* margin of the final pick */
+    out->n_tokens = fin_len[bestIdx];
+    memcpy(out->tokens, fin_t[bestIdx], sizeof(int32_t) * (size_t)fin_len[bestIdx]);
+    out->avg_logprob = fin_len[bestIdx] > 0 ? (float)(fin_lp[bestIdx] / fin_len[bestIdx]) : 0.0f;
+    out->compression_ratio = orc_compression_ratio(out->tokens, out->n_tokens);
+    out->no_speech_prob = noSpeechProb;
+    out->temperature = 0.0f;
   }
-  if (nfin < beam) {
-    for (int b = 0; b < beam && nfin < beam; b++) {
-      memcpy(fin_t[nfin], toks[b], sizeof(int32_t) * (size_t)lens[b]);
-      fin_len[nfin] = lens[b];
-      fin_lp[nfin] = lps[b];
-      nfin++;
-    }
+done:
+  free(toks); free(lens); free(lps); free(fin_t); free(fin_len); free(fin_lp);
+  free(first); free(logits); free(lp); free(top); free(cands);
+  free(ntoks); free(nlens); free(nlps); free(src);
+  return rc;
+}
+
+/* decodeWithFallback's loop (main/nn/WhisperDecoder.java:119-149) as a state machine: feed the
+ * result decoded at temps[i]; returns 1 when the loop ends (result in *best), 0 to continue with
+ * temps[i + 1]. */
+static const float kTemps[6] = {0.0f, 0.2f, 0.4f, 0.6f, 0.8f, 1.0f};
+static int fallback_feed(const orc_result* cur, float t, orc_result* best, int* have) {
+  if (!orc_needs_fallback(cur->compression_ratio, cur->avg_logprob, cur->no_speech_prob)) {
+    *best = *cur;
+    return 1;
   }
-  int bestIdx = 0;
-  double bestScore = -INFINITY;
-  for (int i = 0; i < nfin; i++) {
-    double score = fin_lp[i] / (double)(fin_len[i] > 1 ? fin_len[i] : 1);
-    if (score > bestScore) {
-      bestScore = score;
-      bestIdx = i;
-    }
+  if (!*have || cur->avg_logprob > best->avg_logprob) {
+    *best = *cur;
+    *have = 1;
   }
-  out->n_tokens = fin_len[bestIdx];
-  memcpy(out->tokens, fin_t[bestIdx], sizeof(int32_t) * (size_t)fin_len[bestIdx]);
-  out->avg_logprob = fin_len[bestIdx] > 0 ? (float)(fin_lp[bestIdx] / fin_len[bestIdx]) : 0.0f;
-  out->compression_ratio = orc_compression_ratio(out->tokens, out->n_tokens);
-  out->no_speech_prob = noSpeechProb;
-  out->temperature = 0.0f;
-  for (int b = 0; b < beam; b++) orc_cache_destroy(caches[b]);
-  free(caches); free(toks); free(lens); free(lps); free(fin_t); free(fin_len); free(fin_lp);
-  free(logits); free(lp); free(top); free(cands);
+  if (t == 0.0f && cur->compression_ratio <= 2.4f) return 1;
+  if (t > 0.0f && cur->avg_logprob < best->avg_logprob - 1.0f) return 1;
   return 0;
 }
 
-static int needs_fallback(const orc_result* r) { /* :435-440 */
-  if (r->compression_ratio > 2.4f) return !(r->no_speech_prob > 0.6f && r->avg_logprob < -1.0f);
-  return r->avg_logprob < -1.0f && !(r->no_speech_prob > 0.6f);
+/* The fallback choice over results already decoded at 0, 0.2, .., 1.0: index of the result
+ * decodeWithFallback returns, and in *n_used how many decodes it would have run. */
+int orc_fallback_pick(const orc_result* per_temp, int* n_used) {
+  orc_result best;
+  int have = 0, i = 0, pick = -1;
+  for (; i < 6; i++) {
+    if (fallback_feed(&per_temp[i], kTemps[i], &best, &have)) {
+      i++;
+      break;
+    }
+  }
+  for (int j = 0; j < 6; j++)
+    if (memcmp(&per_temp[j], &best, sizeof best) == 0) { pick = j; break; }
+  if (n_used) *n_used = i;
+  return pick;
 }
 
-/* WhisperDecoder.decodeWithFallback: main/nn/WhisperDecoder.java:119-149 */
+/* ---- the model-backed logits source ---- */
+typedef struct {
+  const orc_model* m;
+  const float* xa;
+  const int32_t* prompt;
+  int n_prompt, n;
+  orc_cache** caches; /* [n] */
+  float* rows;        /* [n_prompt][V] */
+} model_src;
+
+static int ms_prefill(void* ctx, float* first, float* last) {
+  model_src* s = (model_src*)ctx;
+  int V = s->m->d.n_vocab;
+  int rc = orc_forward(s->m, s->prompt, s->n_prompt, s->xa, s->caches[0], s->rows);
+  if (rc) return rc;
+  memcpy(first, s->rows, sizeof(float) * (size_t)V);
+  memcpy(last, s->rows + (size_t)(s->n_prompt - 1) * V, sizeof(float) * (size_t)V);
+  return 0;
+}
+
+static int ms_step(void* ctx, int b, int32_t token, float* out) {
+  model_src* s = (model_src*)ctx;
+  return orc_forward(s->m, &token, 1, s->xa, s->caches[b], out);
+}
+
+/* Beam cache rearrangement (:342-361): hypothesis b continues src[b]'s map (the same map when
+ * src[b] == b, a copy sharing the tensors otherwise); src[b] < 0 aliases new hypothesis 0's map. */
+static int ms_rearrange(void* ctx, const int32_t* src, int saved, int beam) {
+  model_src* s = (model_src*)ctx;
+  orc_cache** nc = (orc_cache**)calloc((size_t)beam, sizeof(orc_cache*));
+  for (int b = 0; b < saved; b++) {
+    if (src[b] == b) {
+      nc[b] = s->caches[b];
+      s->caches[b]->refs++;
+    } else {
+      nc[b] = cache_copy(s->caches[src[b]]);
+    }
+  }
+  for (int b = saved; b < beam; b++) {
+    nc[b] = nc[0];
+    nc[0]->refs++;
+  }
+  for (int b = 0; b < beam; b++) orc_cache_destroy(s->caches[b]);
+  free(s->caches);
+  s->caches = nc;
+  return 0;
+}
+
+static void ms_init(model_src* s, orc_ops* ops, const orc_model* m, const float* xa, const int32_t* prompt,
+                    int n_prompt, int n) {
+  s->m = m;
+  s->xa = xa;
+  s->prompt = prompt;
+  s->n_prompt = n_prompt;
+  s->n = n;
+  s->caches = (orc_cache**)calloc((size_t)n, sizeof(orc_cache*));
+  s->caches[0] = orc_cache_create(m);
+  for (int b = 1; b < n; b++) { /* every map starts empty (:223-229) */
+    s->caches[b] = orc_cache_create(m);
+  }
+  s->rows = (float*)malloc(sizeof(float) * (size_t)(n_prompt > 0 ? n_prompt : 1) * m->d.n_vocab);
+  ops->ctx = s;
+  ops->prefill = ms_prefill;
+  ops->step = ms_step;
+  ops->rearrange = ms_rearrange;
+}
+
+static void ms_free(model_src* s) {
+  for (int b = 0; b < s->n; b++) orc_cache_destroy(s->caches[b]);
+  free(s->caches);
+  free(s->rows);
+}
+
+int orc_decode(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, int eot, int max_tokens,
+               const int32_t* suppress, int n_suppress, int no_speech, float temperature, int ts_begin,
+               uint64_t seed, orc_result* out) {
+  if (n_prompt < 1) return -3;
+  model_src s;
+  orc_ops ops;
+  ms_init(&s, &ops, m, xa, prompt, n_prompt, 1);
+  int rc = orc_greedy_drive(&ops, m->d.n_vocab, eot, max_tokens, suppress, n_suppress, no_speech, temperature,
+                            ts_begin, seed, out);
+  ms_free(&s);
+  return rc;
+}
+
+int orc_decode_beam(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, int eot,
+                    int max_tokens, const int32_t* suppress, int n_suppress, int no_speech, int ts_begin, int beam,
+                    orc_result* out) {
+  if (n_prompt < 1 || beam < 1 || beam > 16) return -3;
+  model_src s;
+  orc_ops ops;
+  ms_init(&s, &ops, m, xa, prompt, n_prompt, beam);
+  int rc = orc_beam_drive(&ops, m->d.n_vocab, eot, max_tokens, suppress, n_suppress, no_speech, ts_begin, beam, out,
+                          NULL);
+  ms_free(&s);
+  return rc;
+}
+
+int orc_decode_beam_gaps(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, int eot,
+                         int max_tokens, const int32_t* suppress, int n_suppress, int no_speech, int ts_begin, int beam,
+                         orc_result* out, double* gaps) {
+  if (n_prompt < 1 || beam < 1 || beam > 16) return -3;
+  model_src s;
+  orc_ops ops;
+  ms_init(&s, &ops, m, xa, prompt, n_prompt, beam);
+  int rc = orc_beam_drive(&ops, m->d.n_vocab, eot, max_tokens, suppress, n_suppress, no_speech, ts_begin, beam, out,
+                          gaps);
+  ms_free(&s);
+  return rc;
+}
+
+/* WhisperDecoder.decodeWithFallback: main/nn/WhisperDecoder.java:119-149 (the sampling draws of
+ * temperature i use seed + i). */
 int orc_decode_with_fallback(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, int eot,
                              int max_tokens, const int32_t* suppress, int n_suppress, int no_speech, int ts_begin,
                              int beam, uint64_t seed, orc_result* out) {
-  const float temps[6] = {0.0f, 0.2f, 0.4f, 0.6f, 0.8f, 1.0f};
   orc_result cur, best;
   int have = 0;
   for (int i = 0; i < 6; i++) {
-    float t = temps[i];
+    float t = kTemps[i];
     int rc = (beam > 1 && t == 0.0f)
                  ? orc_decode_beam(m, xa, prompt, n_prompt, eot, max_tokens, suppress, n_suppress, no_speech, ts_begin,
                                    beam, &cur)
                  : orc_decode(m, xa, prompt, n_prompt, eot, max_tokens, suppress, n_suppress, no_speech, t, ts_begin,
                               seed + (uint64_t)i, &cur);
     if (rc) return rc;
-    if (!needs_fallback(&cur)) {
-      *out = cur;
-      return 0;
-    }
-    if (!have || cur.avg_logprob > best.avg_logprob) {
-      best = cur;
-      have = 1;
-    }
-    if (t == 0.0f && cur.compression_ratio <= 2.4f) break;
-    if (t > 0.0f && cur.avg_logprob < best.avg_logprob - 1.0f) break;
+    if (fallback_feed(&cur, t, &best, &have)) break;
   }
   *out = best;
   return 0;
 }
-
 /* Teacher-forced greedy sweep (the workload of the parity tests and the CPU baseline). */
 int orc_forced(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, const int32_t* forced,
                int n_steps, int32_t* argmax_out, float* max_out, float* second_out, float* lse_out,

@@ -88,13 +88,57 @@ int orc_cache_len(const orc_cache* c);
 int orc_forward(const orc_model* m, const int32_t* tokens, int n, const float* xa, orc_cache* cache,
                 float* logits);
 
-/* ---- decode drivers (main/nn/WhisperDecoder.java) ---- */
+/* Fixed logit bias [V] added to every logits row after the tied projection (NULL: none).  Not a
+ * reference feature: the seeded bias of the beam-search workload. */
+void orc_model_set_logit_bias(orc_model* m, const float* bias);
+
+/* ---- logit rules (main/nn/WhisperDecoder.java:435-598), each sets -inf in place ---- */
+void orc_suppress_blank(float* logits, int n, int eot);                                   /* :450-455 */
+void orc_apply_suppress(float* logits, const int32_t* ids, int n_ids, int n);             /* :457-466 */
+void orc_ngram_block(float* logits, const int32_t* gen, int cnt, int ngram, int n);       /* :543-564 */
+void orc_timestamp_rules(float* logits, const int32_t* gen, int cnt, int ts_begin, int eot, int n,
+                         int first_step);                                                  /* :484-541 */
+int orc_needs_fallback(float compression_ratio, float avg_logprob, float no_speech_prob); /* :435-440 */
+/* sample (:576-598) with the uniform draw u in [0,1) given; overwrites logits with exp weights */
+int orc_sample_u(float* logits, int n, float temperature, double u);
+/* SplitMix64 (the seeded stand-in for Math.random): next 64-bit output, and a double in [0,1) */
+uint64_t orc_splitmix64_next(uint64_t* state);
+double orc_rng_uniform(uint64_t* state);
+
+/* ---- decode drivers over a logits source (main/nn/WhisperDecoder.java) ---- */
+typedef struct {
+  void* ctx;
+  /* the prompt: logits rows of its first position (no-speech probe) and its last position */
+  int (*prefill)(void* ctx, float* first_row, float* last_row);
+  /* one token appended to hypothesis `beam` (0 when greedy): its logits row */
+  int (*step)(void* ctx, int beam, int32_t token, float* row);
+  /* beam rearrangement: hypothesis b continues src[b] for b < saved; src[b] = -1 for b >= saved
+   * (those continue new hypothesis 0) */
+  int (*rearrange)(void* ctx, const int32_t* src, int saved, int beam);
+} orc_ops;
+int orc_greedy_drive(const orc_ops* ops, int n_vocab, int eot, int max_tokens, const int32_t* suppress, int n_suppress,
+                     int no_speech, float temperature, int ts_begin, uint64_t seed, orc_result* out);
+/* gaps (nullable, [max_tokens]): gaps[i] for search step i = the score of the last hypothesis kept
+ * minus that of the first non-end candidate left out (+inf when none was left out); gaps[0] = the
+ * final pick's margin over the runner-up.  Decisions with a gap above the checker's tolerance cannot
+ * flip under a logit error below it (test instrumentation, not part of the reference). */
+int orc_beam_drive(const orc_ops* ops, int n_vocab, int eot, int max_tokens, const int32_t* suppress, int n_suppress,
+                   int no_speech, int ts_begin, int beam, orc_result* out, double* gaps);
+/* decodeWithFallback's choice over results already decoded at temperatures 0, 0.2, .., 1.0: the
+ * index it returns; *n_used = how many of the decodes it would have run. */
+int orc_fallback_pick(const orc_result* per_temp /*[6]*/, int* n_used);
+
+/* ---- decode drivers on the model (main/nn/WhisperDecoder.java) ---- */
 int orc_decode(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, int eot,
                int max_tokens, const int32_t* suppress, int n_suppress, int no_speech, float temperature,
                int ts_begin, uint64_t seed, orc_result* out);
 int orc_decode_beam(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, int eot,
                     int max_tokens, const int32_t* suppress, int n_suppress, int no_speech, int ts_begin,
                     int beam, orc_result* out);
+/* decode_beam that also records the decision gaps of orc_beam_drive */
+int orc_decode_beam_gaps(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, int eot,
+                         int max_tokens, const int32_t* suppress, int n_suppress, int no_speech, int ts_begin, int beam,
+                         orc_result* out, double* gaps);
 int orc_decode_with_fallback(const orc_model* m, const float* xa, const int32_t* prompt, int n_prompt, int eot,
                              int max_tokens, const int32_t* suppress, int n_suppress, int no_speech,
                              int ts_begin, int beam, uint64_t seed, orc_result* out);

@@ -21,14 +21,17 @@ def say(*a):
 
 
 # 80 encoder frames give one cross-attention key chunk per (encoder, head); 300 frames give three
-# (chunks of at most 128 keys), merged by the last chunk workgroup of each head: 10 rows on one
-# encoder (two row groups of 8 and 2) and 4 rows with their own encoders.
+# (chunks of at most 128 keys), whose (max, sum, value) partials k_w_cmerge merges: 10 rows on one
+# encoder (two row groups of 8 and 2) and 4 rows with their own encoders.  Sessions of fewer than 5
+# rows at d < 768 would run on the persistent kernel, so the 4-row case sets W4H_ENGINE=wide.
 @pytest.mark.parametrize("d,heads,n_rows,n_enc,wtype,a_ctx", [(384, 6, 12, 12, "f16", 80), (512, 8, 20, 20, "f16", 80),
                                                               (1280, 20, 32, 32, "f16", 80), (1024, 16, 16, 16, "q8_0", 80),
                                                               (768, 12, 10, 1, "f16", 80), (384, 6, 10, 1, "f16", 300),
                                                               (384, 6, 4, 4, "f16", 300)])
-def test_batched_streams_forced(gpu, orc, d, heads, n_rows, n_enc, wtype, a_ctx):
+def test_batched_streams_forced(gpu, orc, monkeypatch, d, heads, n_rows, n_enc, wtype, a_ctx):
     dims = synth.Dims(n_vocab=1200, n_text_ctx=48, n_text_state=d, n_text_head=heads, n_text_layer=2, n_audio_ctx=a_ctx)
+    if n_rows < 5:
+        monkeypatch.setenv("W4H_ENGINE", "wide")
     say(f"d={d} heads={heads} rows={n_rows} encoders={n_enc} {wtype} frames={a_ctx}")
     T = synth.make_decoder(dims, seed=41, wtype=wtype, ln_random=True)
     xas = [synth.encoder_output(dims, 41, stream=e) for e in range(n_enc)]

@@ -184,7 +184,7 @@ def test_beam_reorder_gather(gpu, orc):
 
 
 def test_decode_drivers_match_oracle(gpu, orc):
-    say("decode / decode_beam / fallback vs oracle")
+    say("decode / decode_beam vs oracle")
     T = make(TINY, 26)
     xa = synth.encoder_output(TINY, 26)
     om = orc.Model(TINY, T)
@@ -357,3 +357,103 @@ def test_greedy_decode_rules_on_device_variants(gpu, orc, monkeypatch, d, heads,
     say(f"greedy rules d={d} {wtype}: {len(res['1'].tokens)} tokens")
     assert res["1"].tokens == og["tokens"]
     assert res["1"].avg_logprob == pytest.approx(og["avg_logprob"], abs=1e-3)
+
+
+# ---- temperature sampling and the fallback driver ------------------------------------------------
+
+FB_DIMS = synth.Dims(n_vocab=600, n_text_ctx=320, n_text_state=128, n_text_head=2, n_text_layer=2, n_audio_ctx=50)
+
+
+def _fb_model(seed=71):
+    T = make(FB_DIMS, seed)
+    xa = synth.encoder_output(FB_DIMS, seed)
+    return T, xa
+
+
+def _draw_margins(orc, om, xa, prompt, eot, suppress, temperature, seed, tokens, n_steps):
+    """Relative distance of each sampling draw of the oracle's decode from the nearest bucket edge of
+    the cumulative weights (0 where a 1e-4 change of the weights could move it to a neighbouring id)."""
+    lg = om.forced(xa, prompt, np.array(tokens[: n_steps - 1], np.int32), want_logits=True)["logits"]
+    us = orc.rng_uniform(seed, n_steps)
+    out = []
+    for i in range(n_steps):
+        row = lg[i]
+        if i == 0:
+            row = orc.suppress_blank(row, eot)
+        row = orc.apply_suppress(row, suppress)
+        row = orc.ngram_block(orc.ngram_block(row, tokens[:i], 3), tokens[:i], 4)
+        w = np.exp(((row - row.max()) / np.float32(temperature)).astype(np.float64)).astype(np.float32).astype(np.float64)
+        cum = np.cumsum(w)
+        r = us[i] * cum[-1]
+        k = int(np.searchsorted(cum, r))
+        lo = cum[k - 1] if k > 0 else 0.0
+        out.append(min(r - lo, cum[k] - r) / cum[-1])
+    return out
+
+
+@pytest.mark.parametrize("temperature,seed", [(0.4, 3), (1.0, 11)])
+def test_sampled_decode_matches_oracle(gpu, orc, temperature, seed):
+    """WhisperDecoder.decode at T > 0 (sample, main/nn/WhisperDecoder.java:576-598) with the seeded
+    draw: tokens equal to the oracle's decode with the same seed up to the first draw that lies within
+    1e-4 (relative) of a bucket edge of the cumulative weights (logits agree to ~1e-4, so such a draw
+    may legitimately pick a neighbour); average log-probability within 1e-3 when the decodes agree."""
+    T, xa = _fb_model()
+    om = orc.Model(FB_DIMS, T)
+    m = gpu.Model.from_tensors(FB_DIMS, T)
+    dec = gpu.WhisperDecoder(m, beam_size=1)
+    prompt, eot, sup = [10, 11, 12], 599, [1, 2]
+    g = dec.decode(xa, prompt, eot, 60, sup, temperature=temperature, seed=seed)
+    o = om.decode(xa, prompt, eot=eot, max_tokens=60, suppress=sup, temperature=temperature, seed=seed)
+    dec.close()
+    m.close()
+    n = len(o["tokens"]) + (1 if len(o["tokens"]) < 60 else 0)
+    marg = _draw_margins(orc, om, xa, prompt, eot, sup, temperature, seed, list(o["tokens"]), n)
+    first = next((i for i in range(min(len(g.tokens), len(o["tokens"]))) if g.tokens[i] != o["tokens"][i]), None)
+    say(f"T={temperature} seed={seed}: {len(g.tokens)} tokens (oracle {len(o['tokens'])}), first difference {first}, "
+        f"smallest draw margin {min(marg):.2e}")
+    if first is None:
+        assert g.tokens == o["tokens"]
+        assert g.avg_logprob == pytest.approx(o["avg_logprob"], abs=1e-3)
+        assert g.temperature == pytest.approx(temperature)
+    else:
+        assert min(marg[: first + 1]) < 1e-4, f"decodes part at step {first} with every draw margin >= 1e-4"
+
+
+@pytest.mark.parametrize("beam", [1, 3])
+def test_decode_with_fallback_matches_oracle(gpu, orc, beam):
+    """WhisperDecoder.decodeWithFallback (main/nn/WhisperDecoder.java:119-149) on a model whose greedy
+    decode compresses better than 2.4 (a fixed logit bias favours six ids), so needsFallback holds at
+    T = 0 and the loop decodes the sampled temperatures (seed + i) before it returns: the device
+    driver's result (tokens, temperature, average log-probability, compression ratio) equals the
+    oracle's driver on the same inputs; beam 3 runs the T = 0 decode as beam search.  Each sampled
+    temperature's decode is also compared on its own with the oracle's."""
+    T, xa = _fb_model()
+    bias = np.zeros(FB_DIMS.n_vocab, np.float32)
+    bias[100:106] = 8.0
+    om = orc.Model(FB_DIMS, T)
+    om.set_logit_bias(bias)
+    m = gpu.Model.from_tensors(FB_DIMS, T)
+    dec = gpu.WhisperDecoder(m, beam_size=beam)
+    dec.set_logit_bias(bias)
+    prompt, eot, sup, n, seed = [10, 11, 12], 599, [1, 2], 250, 5
+    o0 = om.decode(xa, prompt, eot=eot, max_tokens=n, suppress=sup) if beam == 1 else \
+        om.decode_beam(xa, prompt, eot=eot, max_tokens=n, suppress=sup, beam=beam)
+    say(f"fallback beam={beam}: oracle T=0 compression {o0['compression_ratio']:.3f} avg {o0['avg_logprob']:.3f}")
+    assert o0["compression_ratio"] > 2.4  # the loop goes past T = 0
+    g = dec.decode_with_fallback(xa, prompt, eot, n, sup, beam_size=beam, seed=seed)
+    o = om.decode_with_fallback(xa, prompt, eot=eot, max_tokens=n, suppress=sup, beam=beam, seed=seed)
+    say(f"fallback beam={beam}: device T={g.temperature} {len(g.tokens)} tokens avg {g.avg_logprob:.4f}; "
+        f"oracle T={o['temperature']} avg {o['avg_logprob']:.4f}")
+    assert g.tokens == o["tokens"]
+    assert g.temperature == pytest.approx(o["temperature"])
+    assert g.avg_logprob == pytest.approx(o["avg_logprob"], abs=1e-3)
+    assert g.compression_ratio == pytest.approx(o["compression_ratio"], rel=1e-6)
+    if beam == 1:
+        for i, t in enumerate([0.2, 0.4, 0.6, 0.8, 1.0], start=1):
+            gs = dec.decode(xa, prompt, eot, n, sup, temperature=t, seed=seed + i)
+            os_ = om.decode(xa, prompt, eot=eot, max_tokens=n, suppress=sup, temperature=t, seed=seed + i)
+            say(f"fallback T={t}: device avg {gs.avg_logprob:.4f} oracle {os_['avg_logprob']:.4f} "
+                f"equal tokens {gs.tokens == os_['tokens']}")
+            assert gs.tokens == os_["tokens"]
+    dec.close()
+    m.close()

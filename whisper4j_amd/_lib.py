@@ -31,7 +31,7 @@ EXPORTS = (
     "w4h_last_error", "w4h_device_count", "w4h_model_create", "w4h_model_load_ggml", "w4h_model_dims",
     "w4h_model_destroy", "w4h_ggml_inspect", "w4h_ggml_read_tensor", "w4h_session_create", "w4h_session_destroy",
     "w4h_session_set_encoder", "w4h_session_set_encoder_device", "w4h_session_reset", "w4h_session_kv_len", "w4h_session_set_suppress",
-    "w4h_session_set_probe", "w4h_session_step", "w4h_session_run", "w4h_session_reorder", "w4h_session_time_run",
+    "w4h_session_set_probe", "w4h_session_set_logit_bias", "w4h_session_step", "w4h_session_run", "w4h_session_reorder", "w4h_session_time_run",
     "w4h_session_trace_run",
     "w4h_decode", "w4h_decode_beam", "w4h_decode_with_fallback", "w4h_compression_ratio", "w4h_op_linear",
     "w4h_op_layernorm", "w4h_op_gelu", "w4h_op_attention", "w4h_op_select",
@@ -108,6 +108,7 @@ def lib():
         "w4h_session_kv_len": (i32, [vp, i32p]),
         "w4h_session_set_suppress": (i32, [vp, i32p, i32]),
         "w4h_session_set_probe": (i32, [vp, i32]),
+        "w4h_session_set_logit_bias": (i32, [vp, f32p]),
         "w4h_session_step": (i32, [vp, i32p, u32p, i32, ctypes.POINTER(StepOut), f32p]),
         "w4h_session_run": (i32, [vp, i32p, i32p, i32, i32, ctypes.POINTER(StepOut)]),
         "w4h_session_reorder": (i32, [vp, i32p]),

@@ -12,6 +12,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -429,7 +430,7 @@ struct w4h_session {
   size_t item_bytes = 0;  // LDS bytes of one resident vocabulary item
   size_t lds = 0;
   hipStream_t stream = nullptr;
-  DevBuf kvk, kvv, xk, xv, ll, out, forced, mask, logits, xa_tmp, trace;
+  DevBuf kvk, kvv, xk, xv, ll, out, forced, mask, logits, xa_tmp, trace, bias;
   // Per-step inputs in one device area (error word, tokens, extra mask, slot table) filled by one
   // copy from its page-locked staging twin; forced rows and results are staged separately.
   DevBuf in;
@@ -445,6 +446,7 @@ struct w4h_session {
   uint32_t next_tag = 1;
   int probe = -1;
   bool has_mask = false;
+  bool bias_on = false;  // the fixed logit bias in `bias` is applied
   std::vector<int32_t> slots_host;
   bool slots_identity = true, slots_dirty = false;
   bool closed = false;
@@ -506,6 +508,7 @@ static StepParams base_params(w4h_session* s) {
   p.rep_stride = s->rep_stride;
   p.nres = s->nres;
   p.res_off = s->res_off;
+  p.bias = s->bias_on ? s->bias.as<float>() : nullptr;
   return p;
 }
 
@@ -556,6 +559,8 @@ static WideParams wide_params(w4h_session* s) {
   p.mask = s->has_mask ? s->mask.as<uint32_t>() : nullptr;
   p.mw = s->mw;
   p.probe = s->probe;
+  p.bias = s->bias.as<float>();
+  p.bias_on = s->bias_on ? 1 : 0;
   return p;
 }
 
@@ -596,6 +601,15 @@ static size_t rules_layout(const w4h_session* s, int hist_cap, StepParams& p) {
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, s->m->device) != hipSuccess || lds > (size_t)prop.sharedMemPerBlock) return 0;
   return lds;
+}
+
+// The persistent step kernel is a cooperative launch whose workgroups (one per compute unit) must all
+// be resident at once; two of them on one device, from sessions driven on different threads, could
+// each hold compute units the other waits for.  Its launches are serialized per device, from the
+// launch until the results are back on the host.
+static std::mutex& coop_lock(int device) {
+  static std::mutex m[64];
+  return m[device & 63];
 }
 
 // Launch n_steps steps; tokens/forced are host arrays.  Results (if out) are copied back.  With
@@ -697,6 +711,7 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
     p.hist_cap = rules->nhist + n_steps;
     if (!(lds = rules_layout(s, p.hist_cap, p))) return fail(W4H_ERR_INVALID, "no LDS left for the device decode rules");
   }
+  std::unique_lock<std::mutex> coop(coop_lock(s->m->device));
   hipEvent_t e0 = nullptr, e1 = nullptr;
   if (ms) {
     HIPCHK(hipEventCreate(&e0));
@@ -781,29 +796,32 @@ int create_wide(std::unique_ptr<w4h_session>& s, const hipDeviceProp_t& prop, w4
   if ((rc = s->kvk.alloc(kv_elems * 2)) || (rc = s->kvv.alloc(kv_elems * 2))) return rc;
   const size_t x_elems = (size_t)s->X * L * H * A * kHeadDim;
   if ((rc = s->xk.alloc(x_elems * 2)) || (rc = s->xv.alloc(x_elems * 2))) return rc;
-  HIPCHK(hipMemset(s->xk.p, 0, x_elems * 2));
-  HIPCHK(hipMemset(s->xv.p, 0, x_elems * 2));
+  // device buffers are cleared on the session's own stream (not the legacy stream, which other
+  // threads' sessions may be capturing beside)
+  HIPCHK(hipStreamCreate(&s->stream));
+  HIPCHK(hipMemsetAsync(s->xk.p, 0, x_elems * 2, s->stream));
+  HIPCHK(hipMemsetAsync(s->xv.p, 0, x_elems * 2, s->stream));
   s->slots_host.resize((size_t)s->S * s->max_ctx);
   for (int r = 0; r < s->S; r++)
     for (int q = 0; q < s->max_ctx; q++) s->slots_host[(size_t)r * s->max_ctx + q] = r;
   if ((rc = init_inputs(s.get()))) return rc;
   if ((rc = s->wx.alloc(sizeof(float) * (size_t)s->S * d))) return rc;
   if ((rc = s->wact.alloc(sizeof(float) * (size_t)s->Rp * 4 * d))) return rc;
-  HIPCHK(hipMemset(s->wact.p, 0, sizeof(float) * (size_t)s->Rp * 4 * d));
+  HIPCHK(hipMemsetAsync(s->wact.p, 0, sizeof(float) * (size_t)s->Rp * 4 * d, s->stream));
   if ((rc = s->whid.alloc(sizeof(float) * (size_t)s->Rp * 4 * d))) return rc;
-  HIPCHK(hipMemset(s->whid.p, 0, sizeof(float) * (size_t)s->Rp * 4 * d));
+  HIPCHK(hipMemsetAsync(s->whid.p, 0, sizeof(float) * (size_t)s->Rp * 4 * d, s->stream));
   if ((rc = s->wpart.alloc(sizeof(float) * pmax))) return rc;
   if ((rc = s->wcpart.alloc(sizeof(float) * (size_t)s->S * H * s->nch * kPartWords))) return rc;
   if ((rc = s->wselp.alloc(sizeof(float) * (size_t)s->S * s->nsel * kSelWords))) return rc;
   if ((rc = s->wnext.alloc(sizeof(int32_t) * s->S))) return rc;
   if ((rc = s->wctl.alloc(sizeof(WideCtl)))) return rc;
-  HIPCHK(hipMemset(s->wctl.p, 0, sizeof(WideCtl)));
+  HIPCHK(hipMemsetAsync(s->wctl.p, 0, sizeof(WideCtl), s->stream));
   HIPCHK(wide_prepare(s->Rp, m->wq8));
   // One step is captured as a HIP graph and replayed per step; W4H_GRAPH=0 launches every kernel.
   if (const char* e = getenv("W4H_GRAPH")) s->use_graph = atoi(e) != 0;
-  HIPCHK(hipStreamCreate(&s->stream));
   if ((rc = s->mask.alloc(sizeof(uint32_t) * (size_t)s->S * s->mw))) return rc;
-  HIPCHK(hipDeviceSynchronize());
+  if ((rc = s->bias.alloc(sizeof(float) * (size_t)V))) return rc;
+  HIPCHK(hipStreamSynchronize(s->stream));
   m->refs.fetch_add(1);
   *out = s.release();
   return W4H_OK;
@@ -859,6 +877,18 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   if ((d / 8 + s->grid - 1) / s->grid > kResItems)
     return fail(W4H_ERR_INVALID, "n_text_state %d needs more than %d compute units", d, d / (8 * kResItems));
   s->rpw = (((V + 7) / 8 + s->grid - 1) / s->grid) * 8;
+  const size_t kv_elems = (size_t)L * s->S * H * s->max_ctx * kHeadDim;
+  {
+    // The step kernel reads its weights, self-KV and cross-KV through buffer resources with 32-bit
+    // byte offsets, so each of those arrays must stay below 2 GiB.
+    const size_t lim = 0x7fffffffu, xb = (size_t)s->X * L * H * A * kHeadDim * 2;
+    const size_t wb = std::max((size_t)V * d, (size_t)4 * d * d) * 2;
+    if (kv_elems * 2 > lim || xb > lim || wb > lim)
+      return fail(W4H_ERR_INVALID,
+                  "self-KV (%zu bytes), cross-KV (%zu bytes) or a weight matrix (%zu bytes) exceeds the step kernel's 2 GiB "
+                  "addressing; use fewer rows or a smaller max_ctx",
+                  kv_elems * 2, xb, wb);
+  }
   StepParams probe_p{};
   probe_p.S = s->S;
   probe_p.d = d;
@@ -887,12 +917,12 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   if (s->lds > (size_t)prop.sharedMemPerBlock)
     return fail(W4H_ERR_INVALID, "n_rows %d x n_text_state %d needs %zu bytes of LDS per workgroup (max %zu)", s->S, d, s->lds,
                 (size_t)prop.sharedMemPerBlock);
-  const size_t kv_elems = (size_t)L * s->S * H * s->max_ctx * kHeadDim;
   if ((rc = s->kvk.alloc(kv_elems * 2)) || (rc = s->kvv.alloc(kv_elems * 2))) return rc;
   const size_t x_elems = (size_t)s->X * L * H * A * kHeadDim;
   if ((rc = s->xk.alloc(x_elems * 2)) || (rc = s->xv.alloc(x_elems * 2))) return rc;
-  HIPCHK(hipMemset(s->xk.p, 0, x_elems * 2));
-  HIPCHK(hipMemset(s->xv.p, 0, x_elems * 2));
+  HIPCHK(hipStreamCreate(&s->stream));
+  HIPCHK(hipMemsetAsync(s->xk.p, 0, x_elems * 2, s->stream));
+  HIPCHK(hipMemsetAsync(s->xv.p, 0, x_elems * 2, s->stream));
   s->slots_host.resize((size_t)s->S * s->max_ctx);
   for (int r = 0; r < s->S; r++)
     for (int q = 0; q < s->max_ctx; q++) s->slots_host[(size_t)r * s->max_ctx + q] = r;
@@ -915,9 +945,9 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   s->x3 = b; b += n_vec;
   s->lp = b; b += n_lp;
   s->lpa = b;
-  HIPCHK(hipStreamCreate(&s->stream));
   HIPCHK(launch_fill_u64(s->ll.as<u64>(), total * kRep, s->stream));
   if ((rc = s->mask.alloc(sizeof(uint32_t) * (size_t)s->S * s->mw))) return rc;
+  if ((rc = s->bias.alloc(sizeof(float) * (size_t)V))) return rc;
   HIPCHK(hipStreamSynchronize(s->stream));
   m->refs.fetch_add(1);
   *out = s.release();
@@ -1003,6 +1033,18 @@ int w4h_session_set_suppress(w4h_session* s, const int32_t* ids, int32_t n) {
   HIPCHK(hipSetDevice(s->m->device));
   HIPCHK(hipMemcpy(s->mask.p, bits.data(), bits.size() * 4, hipMemcpyHostToDevice));
   s->has_mask = n > 0;
+  return W4H_OK;
+}
+
+int w4h_session_set_logit_bias(w4h_session* s, const float* bias) {
+  if (!s) return fail(W4H_ERR_INVALID, "null argument");
+  if (!bias) {
+    s->bias_on = false;
+    return W4H_OK;
+  }
+  HIPCHK(hipSetDevice(s->m->device));
+  HIPCHK(hipMemcpy(s->bias.p, bias, sizeof(float) * (size_t)s->m->dims.n_vocab, hipMemcpyHostToDevice));
+  s->bias_on = true;
   return W4H_OK;
 }
 
@@ -1219,9 +1261,11 @@ int device_beam_search(w4h_session* s, const BeamSearchIn& in, BeamSearchOut* ou
   int remaining = in.max_steps;
   bool first = true;
   while (remaining > 0) {
-    const int n = std::min(kChunk, remaining);
-    if (s->kv_len + n > s->max_ctx)
-      return fail(W4H_ERR_CAPACITY, "self-KV capacity %d exceeded (kv_len %d + %d steps)", s->max_ctx, s->kv_len, n);
+    // a launch takes at most the steps the self-KV still has room for; the search fails only when it
+    // has not ended and no room is left (as the host loop, which checks one step at a time)
+    const int n = std::min(std::min(kChunk, remaining), s->max_ctx - s->kv_len);
+    if (n <= 0)
+      return fail(W4H_ERR_CAPACITY, "self-KV capacity %d exceeded (kv_len %d, %d steps left)", s->max_ctx, s->kv_len, remaining);
     WideParams wp = wide_params(s);
     wp.nsteps = n;
     wp.kv_len0 = s->kv_len;

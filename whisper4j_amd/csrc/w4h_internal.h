@@ -57,6 +57,7 @@ struct StepParams {
   int mw, probe, topk;
   w4h_step_out* out;            // [nsteps][S] or null
   float* logits_out;            // [nsteps][S][V] or null
+  const float* bias;            // [V] fixed logit bias added before selection, or null
   unsigned* err;
   int rows_per_wg;              // vocab rows one workgroup keeps in LDS in the logits phase
   int ngroups;                  // phase q runs on workgroup group q % ngroups (1 or 2)
@@ -121,7 +122,7 @@ struct WideGemm {
 struct WideCtl {
   int i;           // step index within the run (advanced by the last selection-merge workgroup)
   int kv_len0;     // KV length before the run
-  int forced_on, out_on, logits_on, mask_on, mask2_on, slots_on, topk, probe;
+  int forced_on, out_on, logits_on, mask_on, mask2_on, slots_on, bias_on, topk, probe;
   unsigned done;   // selection-merge arrivals in the current step
   int tok_dev;     // the run's first tokens come from next_tok (a continued device beam search)
   int stop;        // set by the device beam step when the search has ended: later kernels return
@@ -186,6 +187,8 @@ struct WideParams {
   int mw, probe, topk;
   w4h_step_out* out;        // [nsteps][S] or null
   float* logits_out;        // [nsteps][S][V] or null
+  const float* bias;        // [V] fixed logit bias (session buffer, always present)
+  int bias_on;
 };
 
 // Enqueue p.nsteps wide steps on st.

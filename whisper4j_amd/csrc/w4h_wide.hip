@@ -660,6 +660,7 @@ __global__ __launch_bounds__(64) void k_w_cmerge(const WideCtl* __restrict__ ctl
 __global__ __launch_bounds__(256) void k_w_select(const WideCtl* __restrict__ ctl, const float* __restrict__ P, int ks, size_t ss,
                                                   int S, int V,
                                                   const uint32_t* mask_buf, const uint32_t* mask2_buf, int mw,
+                                                  const float* __restrict__ bias_buf,
                                                   float* __restrict__ selp, int nsel, float* __restrict__ logits_buf) {
   __shared__ float lg[4][kWideSelChunk], rw[4][kWideSelChunk];
   __shared__ int idx[4][kWideSelChunk];
@@ -669,12 +670,13 @@ __global__ __launch_bounds__(256) void k_w_select(const WideCtl* __restrict__ ct
   const uint32_t* mask2 = ctl->mask2_on ? mask2_buf : nullptr;
   const int probe = ctl->probe, topk = ctl->topk;
   float* logits_out = ctl->logits_on ? logits_buf + (size_t)ctl->i * S * V : nullptr;
+  const float* bias = ctl->bias_on ? bias_buf : nullptr;
   const int part = blockIdx.y * 4 + wv;
   const int v0 = part * kWideSelChunk;
   const int nl = max(0, min(kWideSelChunk, V - v0));
   for (int j = lane; j < nl; j += 64) {
     const int v = v0 + j;
-    const float x = slice_sum<4>(P, ks, ss, (size_t)s * V + v);
+    const float x = slice_sum<4>(P, ks, ss, (size_t)s * V + v) + (bias ? bias[v] : 0.f);
     rw[wv][j] = x;
     lg[wv][j] = (masked(mask, mw, s, v) || masked(mask2, mw, s, v)) ? -INFINITY : x;
     idx[wv][j] = v;
@@ -1110,7 +1112,7 @@ static hipError_t enqueue_step(const WideParams& p, hipStream_t st) {
   WCHK(gemm(p, p.g_v, p.emb, p.emb_s, p.act, st));
   const int nblk = (p.nsel + 3) / 4;
   hipLaunchKernelGGL(k_w_select, dim3(p.S, nblk), dim3(256), 0, st, p.ctl, p.part, p.g_v.ks, sstride(p, p.g_v), p.S, p.V, p.mask,
-                     p.mask2, p.mw, p.selp, p.nsel, p.logits_out);
+                     p.mask2, p.mw, p.bias, p.selp, p.nsel, p.logits_out);
   WCHK(hipGetLastError());
   hipLaunchKernelGGL(k_w_selmerge, dim3(p.S), dim3(64), 0, st, p.ctl, p.selp, p.S, p.nsel, p.out, p.next_tok);
   WCHK(hipGetLastError());
@@ -1140,6 +1142,7 @@ hipError_t launch_wide(const WideParams& p, hipStream_t st) {
   c.mask_on = p.mask != nullptr;
   c.mask2_on = p.mask2 != nullptr;
   c.slots_on = p.slots != nullptr;
+  c.bias_on = p.bias_on;
   c.topk = p.topk;
   c.probe = p.probe;
   c.done = 0;
@@ -1174,10 +1177,17 @@ hipError_t launch_wide(const WideParams& p, hipStream_t st) {
     q.mask = static_cast<const uint32_t*>(key[5]);
     q.slots = static_cast<const int32_t*>(key[6]);
     wide_graph_release(p.graph);
+    // Captured on a stream of its own that does not synchronize with the legacy stream, in this
+    // thread's capture mode: other threads may keep using the legacy stream (memsets, copies of
+    // their sessions) while the capture is open.  Capturing runs nothing, so the step needs no
+    // ordering with st here; every replay is launched on st.
+    hipStream_t cs = nullptr;
+    WCHK(hipStreamCreateWithFlags(&cs, hipStreamNonBlocking));
     hipGraph_t graph = nullptr;
-    WCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-    const hipError_t ce = enqueue_step(q, st);
-    const hipError_t ee = hipStreamEndCapture(st, &graph);
+    hipError_t be = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+    const hipError_t ce = be == hipSuccess ? enqueue_step(q, cs) : be;
+    const hipError_t ee = be == hipSuccess ? hipStreamEndCapture(cs, &graph) : be;
+    (void)hipStreamDestroy(cs);
     WCHK(ce);
     WCHK(ee);
     hipGraphExec_t exec = nullptr;

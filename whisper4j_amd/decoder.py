@@ -159,6 +159,13 @@ class Session:
     def set_probe(self, token: int) -> None:
         check(lib().w4h_session_set_probe(self._h, token))
 
+    def set_logit_bias(self, bias) -> None:
+        """Fixed bias [n_vocab] added to the raw logits of every row before selection (None: off)."""
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32).reshape(-1)
+        if b is not None and b.size != self.vocab:
+            raise ValueError(f"logit bias needs {self.vocab} values, got {b.size}")
+        check(lib().w4h_session_set_logit_bias(self._h, _ptr(b, _f32p)))
+
     def step(self, tokens, extra_mask=None, topk: int = 0, want_logits: bool = False):
         t = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
         out = (_lib.StepOut * self.n_rows)()
@@ -220,6 +227,9 @@ class WhisperDecoder:
 
     def close(self):
         self.session.close()
+
+    def set_logit_bias(self, bias) -> None:
+        self.session.set_logit_bias(bias)
 
     def _opts(self, prompt, eot, max_tokens, suppress, no_speech, temperature, timestamp_begin, beam_size, seed):
         p = np.ascontiguousarray(prompt, dtype=np.int32)

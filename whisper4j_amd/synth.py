@@ -28,6 +28,9 @@ GGML_MAGIC = 0x67676D6C
 # Prompt used by every benchmark configuration: <|endoftext|> <|startoftranscript|> ... as in the
 # reference's stage validation harness.
 BENCH_PREFIX = (50257, 50258, 50359, 50363)
+# <|endoftext|> of the multilingual vocabulary (51865 ids), the end token of the beam workload
+EOT_MULTILINGUAL = 50257
+BEAM_BIAS_SIGMA = 1.0
 
 
 @dataclasses.dataclass(frozen=True)
@@ -177,6 +180,15 @@ def make_decoder(dims: Dims, seed: int = 0, wtype: str = "f16", ln_random: bool 
 def encoder_output(dims: Dims, seed: int = 0, stream: int = 0) -> np.ndarray:
     return _rng(seed, f"encoder_output.{stream}").standard_normal((dims.n_audio_ctx, dims.n_text_state),
                                                                   dtype=np.float32)
+
+
+def logit_bias(dims: Dims, seed: int = 0, sigma: float = 1.0, eot: int | None = None) -> np.ndarray:
+    """The beam workload's fixed logit bias: N(0, sigma) per vocabulary id, the end token at -inf so
+    every hypothesis runs the full step count."""
+    b = _rng(seed, "logit_bias").standard_normal(dims.n_vocab, dtype=np.float32) * np.float32(sigma)
+    if eot is not None:
+        b[eot] = -np.inf
+    return b
 
 
 def forced_tokens(n: int, seed: int = 0, high: int = 50256) -> np.ndarray:
