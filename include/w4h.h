@@ -222,6 +222,17 @@ int w4h_op_attention(const float* q, const uint16_t* k, const uint16_t* v, int32
  * logsumexp and top-k (k <= W4H_TOPK_MAX). */
 int w4h_op_select(const float* logits, int32_t rows, int32_t n, const uint32_t* mask, int32_t k, w4h_step_out* out);
 
+/* No counterpart in the reference: w4h_op_select for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  logits [rows][n],
+ * mask (nullable) [rows][ceil(n/32)] and out [rows] are DEVICE pointers on the calling thread's
+ * current device; the work is enqueued on `stream` (a hipStream_t, NULL for the default stream) and
+ * not waited for.  It allocates nothing: the per-row partials live in a fixed device array of the
+ * library (W4H_SELECT_MAX_ROWS rows, 360 KiB, held on each device it runs on until the process
+ * ends).  Every call on a device shares that array, so calls that overlap on one device race:
+ * issue them on one stream or wait between them.  rows > W4H_SELECT_MAX_ROWS -> W4H_ERR_INVALID. */
+#define W4H_SELECT_MAX_ROWS 64
+int w4h_op_select_noalloc(const float* logits, int32_t rows, int32_t n, const uint32_t* mask, int32_t k,
+                          w4h_step_out* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1205,6 +1205,20 @@ int w4h_op_select(const float* logits, int32_t rows, int32_t n, const uint32_t* 
   return W4H_OK;
 }
 
+int w4h_op_select_noalloc(const float* logits, int32_t rows, int32_t n, const uint32_t* mask, int32_t k,
+                          w4h_step_out* out, void* stream) {
+  if (!logits || !out || rows <= 0 || n <= 0 || k < 0 || k > W4H_TOPK_MAX) return fail(W4H_ERR_INVALID, "bad argument");
+  if (rows > W4H_SELECT_MAX_ROWS)
+    return fail(W4H_ERR_INVALID, "rows %d exceeds the fixed selection scratch of %d rows", rows, W4H_SELECT_MAX_ROWS);
+  if (select_lds_bytes(n) > (size_t)kSelectMaxLds) return fail(W4H_ERR_INVALID, "row length %d too long", n);
+  int dev = 0;
+  HIPCHK(hipGetDevice(&dev));
+  float* scratch = nullptr;
+  HIPCHK(select_scratch(dev, &scratch));
+  HIPCHK(launch_op_select_noalloc(logits, rows, n, mask, k, out, scratch, static_cast<hipStream_t>(stream)));
+  return W4H_OK;
+}
+
 }  // extern "C"
 
 namespace w4h {

@@ -1,6 +1,8 @@
 // Device code of whisper4j_amd for gfx950 outside the step kernels: the op kernels behind the
 // kernel-level entry points and their launchers.
 
+#include <mutex>
+
 #include "w4h_kernels.h"
 
 namespace w4h {
@@ -234,6 +236,56 @@ hipError_t launch_op_attention(const float* q, const uint16_t* k, const uint16_t
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------------------------------------------
+// Selection without allocation (w4h_op_select_noalloc): the partials live in a fixed device array of
+// this file, kSelScratchRows rows of kSelParts partials.  Its address is resolved per device once, with
+// that device current; host code only ever uses the resolved pointer (the array's name on the host
+// side is a stand-in, not a device address).
+
+constexpr int kSelParts = 64;  // partials (workgroups) per row, as launch_op_select
+constexpr int kSelScratchRows = W4H_SELECT_MAX_ROWS;
+static __device__ __align__(256) float scratch[(size_t)kSelScratchRows * kSelParts * kSelWords];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+float* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+}  // namespace
+
+hipError_t select_scratch(int device, float** ptr) {
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::call_once(g_scratch_once[device], [device]() {
+    int prev = 0;
+    hipError_t e = hipGetDevice(&prev);
+    if (e == hipSuccess) e = hipSetDevice(device);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    // the partial kernel may need more than the default LDS for long rows
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void*)k_op_select_part, hipFuncAttributeMaxDynamicSharedMemorySize, kSelectMaxLds);
+    if (prev != device) (void)hipSetDevice(prev);
+    g_scratch_ptr[device] = e == hipSuccess ? static_cast<float*>(p) : nullptr;
+    g_scratch_err[device] = e;
+  });
+  *ptr = g_scratch_ptr[device];
+  return g_scratch_err[device];
+}
+
+size_t select_lds_bytes(int n) {
+  const size_t rpw = (size_t)(((n + 7) / 8 + kSelParts - 1) / kSelParts) * 8;
+  return (3 * rpw + kSelWords) * sizeof(float);
+}
+
+hipError_t launch_op_select_noalloc(const float* logits, int rows, int n, const uint32_t* mask, int k, w4h_step_out* out,
+                                    float* scratch_ptr, hipStream_t st) {
+  const int rpw = (((n + 7) / 8 + kSelParts - 1) / kSelParts) * 8;
+  hipLaunchKernelGGL(k_op_select_part, dim3(kSelParts, rows), dim3(kThreads), select_lds_bytes(n), st, logits, n, mask,
+                     (n + 31) / 32, k, rpw, scratch_ptr);
+  hipLaunchKernelGGL(k_op_select_final, dim3(rows), dim3(64), 0, st, scratch_ptr, kSelParts, k, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_op_select(const float* logits, int rows, int n, const uint32_t* mask, int k, w4h_step_out* out,
                             hipStream_t st) {
   const int G = 64;
@@ -242,7 +294,10 @@ hipError_t launch_op_select(const float* logits, int rows, int n, const uint32_t
   hipError_t e = hipMallocAsync((void**)&parts, (size_t)rows * G * kSelWords * sizeof(float), st);
   if (e != hipSuccess) return e;
   size_t lds = ((size_t)3 * rpw + kSelWords) * sizeof(float);
-  e = hipFuncSetAttribute((const void*)k_op_select_part, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  // one limit for every caller of the partial kernel (the allocation-free entry point shares it)
+  e = lds <= (size_t)kSelectMaxLds ? hipFuncSetAttribute((const void*)k_op_select_part,
+                                                          hipFuncAttributeMaxDynamicSharedMemorySize, kSelectMaxLds)
+                                   : hipErrorInvalidValue;
   if (e == hipSuccess) {
     hipLaunchKernelGGL(k_op_select_part, dim3(G, rows), dim3(kThreads), lds, st, logits, n, mask, (n + 31) / 32, k, rpw,
                        parts);

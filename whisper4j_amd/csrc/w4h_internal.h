@@ -217,5 +217,12 @@ hipError_t launch_op_attention(const float* q, const uint16_t* k, const uint16_t
                                float* out, hipStream_t st);
 hipError_t launch_op_select(const float* logits, int rows, int n, const uint32_t* mask, int k, w4h_step_out* out,
                             hipStream_t st);
+// Allocation-free selection: the partials go to the library's fixed device array (W4H_SELECT_MAX_ROWS
+// rows), whose address on `device` select_scratch resolves once per device.
+constexpr int kSelectMaxLds = 160 * 1024;  // LDS bytes the partial kernel may take (long rows)
+hipError_t select_scratch(int device, float** ptr);
+size_t select_lds_bytes(int n);
+hipError_t launch_op_select_noalloc(const float* logits, int rows, int n, const uint32_t* mask, int k, w4h_step_out* out,
+                                    float* scratch_ptr, hipStream_t st);
 
 }  // namespace w4h
