@@ -55,25 +55,85 @@ def read_traffic():
     return None
 
 
-def cpu_baseline(dims, T, xa, prompt, forced, min_seconds, max_sweeps):
+def cpu_host():
+    """The host CPU the baselines run on: model name, logical CPUs, and the one core they are pinned to."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    allowed = sorted(os.sched_getaffinity(0))
+    return {"cpu_model": model, "nproc": os.cpu_count(), "cpus_allowed": len(allowed), "pinned_core": allowed[-1]}
+
+
+class _Pinned:
+    """Runs the enclosed CPU work on one core (as `taskset -c <core>`), restoring the affinity after."""
+
+    def __init__(self, core):
+        self.core = core
+
+    def __enter__(self):
+        self.old = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, {self.core})
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.old)
+
+
+def cpu_baseline(dims, T, xa, prompt, forced, min_seconds, max_sweeps, core):
     """The oracle (single-threaded C restatement of the reference's Linux decode path) on a bounded
-    sample of the same workload: whole 444-step teacher-forced sweeps, each after an untimed 4-token
-    prefill into a fresh cache, repeated until min_seconds of timed CPU work (at most max_sweeps)."""
+    sample of the same workload, pinned to one core: whole 444-step teacher-forced sweeps, each after
+    an untimed 4-token prefill, repeated until min_seconds of timed CPU work (at most max_sweeps).
+    Returns the rate and the records of the last sweep (argmax, max, second, logsumexp per step)."""
     from oracle import oracle as orc
 
-    m = orc.Model(dims, T)
-    dt, sweeps = 0.0, 0
-    while sweeps < max_sweeps and (sweeps == 0 or dt < min_seconds):
+    with _Pinned(core):
+        m = orc.Model(dims, T)
+        dt, sweeps, rec = 0.0, 0, None
+        while sweeps < max_sweeps and (sweeps == 0 or dt < min_seconds):
+            c = m.new_cache()
+            m.forward(prompt, xa, c)
+            t0 = time.perf_counter()
+            for i in range(N_STEPS):
+                m.forward([int(forced[i])], xa, c)
+            dt += time.perf_counter() - t0
+            c.close()
+            sweeps += 1
+        rec = m.forced(xa, prompt, forced[:N_STEPS])
+        m.close()
+    return N_STEPS * sweeps / dt, dt, sweeps, rec
+
+
+def cpu_step_rate(name, wtype, seconds, core, rows=1, bias=False):
+    """Oracle single-token forwards per second on one core for another workload, after an untimed
+    prompt prefill (which includes the cross-K/V projection); `rows` forwards make one step of that
+    workload (the reference's beam search runs one batch-1 forward per hypothesis, independent streams
+    one per stream).  Returns (steps per second, forwards timed, seconds timed)."""
+    from oracle import oracle as orc
+    from whisper4j_amd import synth
+
+    dims = synth.SHAPES[name]
+    T = synth.make_decoder(dims, seed=0, wtype=wtype)
+    forced = synth.forced_tokens(64, 0)
+    with _Pinned(core):
+        m = orc.Model(dims, T)
+        if bias:
+            m.set_logit_bias(synth.logit_bias(dims, 0, synth.BEAM_BIAS_SIGMA, synth.EOT_MULTILINGUAL))
+        xa = synth.encoder_output(dims, 0)
         c = m.new_cache()
-        m.forward(prompt, xa, c)
-        t0 = time.perf_counter()
-        for i in range(N_STEPS):
-            m.forward([int(forced[i])], xa, c)
-        dt += time.perf_counter() - t0
+        m.forward(list(synth.BENCH_PREFIX), xa, c)
+        n, dt = 0, 0.0
+        while n < len(forced) and (n == 0 or dt < seconds):
+            t0 = time.perf_counter()
+            m.forward([int(forced[n])], xa, c)
+            dt += time.perf_counter() - t0
+            n += 1
         c.close()
-        sweeps += 1
-    m.close()
-    return N_STEPS * sweeps / dt, dt, sweeps
+        m.close()
+    return n / dt / rows, n, dt
 
 
 def copy_calibration(mib):
@@ -221,24 +281,30 @@ def measure_forced(w4h, synth, name, wtype, n_steps, repeats, n_rows=1, n_encode
 def measure_beam(w4h, synth, name, n_steps, beam):
     """Beam search through the library's beam driver (w4h_decode_beam: the prompt prefill, then for a
     batched session candidate scoring, sorting, finished list, masks and KV reorder on the device in
-    32-step launches); EOT is suppressed so every hypothesis runs all steps."""
+    32-step launches), with the workload's seeded logit bias N(0, 1) and the end token at -inf, so every
+    hypothesis runs all steps.  Returns (steps/s, hypothesis tokens/s, us per step, steps, roofline
+    fraction of the mean step: the 5 rows' bytes per step over the measured step time)."""
     from whisper4j_amd.decoder import WhisperDecoder
 
     dims = synth.SHAPES[name]
     T = synth.make_decoder(dims, seed=0, wtype="f16")
     model = w4h.Model.from_tensors(dims, T)
     dec = WhisperDecoder(model, beam_size=beam)
+    dec.set_logit_bias(synth.logit_bias(dims, 0, synth.BEAM_BIAS_SIGMA, synth.EOT_MULTILINGUAL))
     xa = synth.encoder_output(dims, 0)
-    eot = 50256
+    eot = synth.EOT_MULTILINGUAL
     prompt = list(synth.BENCH_PREFIX)
-    dec.decode_beam(xa, prompt, eot, 16, suppress_tokens=[eot])  # warm-up
+    dec.decode_beam(xa, prompt, eot, 16)  # warm-up
     t0 = time.perf_counter()
-    r = dec.decode_beam(xa, prompt, eot, n_steps, suppress_tokens=[eot])
+    r = dec.decode_beam(xa, prompt, eot, n_steps)
     dt = time.perf_counter() - t0
     dec.close()
     model.close()
     steps = len(r.tokens)
-    return steps / dt, beam * steps / dt, dt * 1e6 / steps, steps
+    kv0 = len(prompt)
+    byts = sum(algorithmic_bytes_per_step(dims, kv0 + i, rows=beam, encoders=1) for i in range(steps))
+    frac = byts / dt / 1e9 / HBM_PEAK_GBS
+    return steps / dt, beam * steps / dt, dt * 1e6 / steps, steps, frac
 
 
 def measure_greedy_driver(w4h, synth, name, n_tokens):
@@ -284,10 +350,10 @@ def other_configs(w4h, synth):
         "tokens_per_s": round(drv["device_rules"][0], 1), "us_per_token": round(drv["device_rules"][1], 2),
         "rules": "on the device, one launch",
         "host_loop_tokens_per_s": round(drv["host_loop"][0], 1), "host_loop_us_per_token": round(drv["host_loop"][1], 2)}
-    sps, hps, us, steps = measure_beam(w4h, synth, "small", 224, 5)
-    out["small beam 5, 224 steps (library beam driver w4h_decode_beam: prompt prefill, then the search on the device; EOT suppressed)"] = {
+    sps, hps, us, steps, frac = measure_beam(w4h, synth, "small", 224, 5)
+    out["small beam 5, 224 steps (library beam driver w4h_decode_beam: prompt prefill, then the search on the device; seeded logit bias N(0,1), end token at -inf)"] = {
         "steps_per_s": round(sps, 1), "hypothesis_tokens_per_s": round(hps, 1), "us_per_step": round(us, 2),
-        "steps": steps}
+        "steps": steps, "roofline_frac": round(frac, 4)}
     tps, us, frac, setup = measure_forced(w4h, synth, "small", "f16", 224, 2, n_rows=5, n_encoders=1)
     out["small 5 beam rows on one encoder, 224 forced steps in one run (device step only)"] = {
         "steps_per_s": round(1e6 / us, 1), "hypothesis_tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
@@ -308,6 +374,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum timed oracle work for the CPU baseline")
     ap.add_argument("--cpu-max-sweeps", type=int, default=8)
+    ap.add_argument("--cpu-config-seconds", type=float, default=2.0,
+                    help="timed oracle forwards per other workload for its CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the tiny/small/turbo/medium lines")
     ap.add_argument("--only", choices=["turbo", "small-beam-rows", "greedy-driver", "medium", "tiny"],
@@ -385,13 +453,40 @@ def main():
 
     configs = None if args.no_configs else other_configs(w4h, synth)
 
-    cpu = None
+    cpu, parity = None, None
     if not args.no_cpu:
-        cps, dt, sweeps = cpu_baseline(dims, T, xa, prompt, forced, args.cpu_seconds, args.cpu_max_sweeps)
+        host = cpu_host()
+        core = host["pinned_core"]
+        cps, dt, sweeps, rec = cpu_baseline(dims, T, xa, prompt, forced, args.cpu_seconds, args.cpu_max_sweeps, core)
         cpu = {"value": round(cps, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
                "sample": f"the same base.en workload on the oracle: {sweeps} whole {N_STEPS}-step teacher-forced "
-                         f"sweeps (positions 4..447, each after an untimed 4-token prefill), one thread, "
-                         f"{dt:.1f} s timed"}
+                         f"sweeps (positions 4..447, each after an untimed 4-token prefill), one thread pinned to "
+                         f"core {core}, {dt:.1f} s timed",
+               "host": host}
+        # parity of the timed sweep: device record i follows forced[i], the oracle's row i + 1
+        am = np.array([o[0].argmax for o in outs])
+        mx = np.array([o[0].max_logit for o in outs])
+        lse = np.array([o[0].logsumexp for o in outs])
+        covered = (rec["max"] - rec["second"])[1:] > 1e-2
+        parity = {"tol": 1e-2, "steps": int(len(am)), "margin_coverage": round(float(covered.mean()), 4),
+                  "argmax_equal_where_covered": f"{int((am[covered] == rec['argmax'][1:][covered]).sum())}/{int(covered.sum())}",
+                  "max_abs_dmax": float(np.abs(mx - rec["max"][1:]).max()),
+                  "max_abs_dlogsumexp": float(np.abs(lse - rec["lse"][1:]).max())}
+        if not args.no_configs:
+            cfg = {}
+            for key, name, wtype, rows, unit, note in (
+                    ("tiny.en", "tiny.en", "f16", 1, "tokens/s", "greedy b=1"),
+                    ("small beam 5", "small", "f16", 5, "beam steps/s",
+                     "one beam step = 5 batch-1 forwards (the reference runs one per hypothesis), seeded logit bias"),
+                    ("large-v3-turbo 32 streams", "large-v3-turbo", "f16", 1, "tokens/s",
+                     "per stream; the 32 streams run one after another on one core at this rate"),
+                    ("medium q8_0", "medium", "q8_0", 1, "tokens/s", "greedy b=1, weights dequantized to fp32")):
+                rate, n, t = cpu_step_rate(name, wtype, args.cpu_config_seconds, core, rows=rows,
+                                           bias=name == "small")
+                cfg[key] = {"value": round(rate, 3), "unit": unit, "cores": 1, "kind": "port",
+                            "sample": f"{n} single-token forwards on the oracle after an untimed prompt prefill, "
+                                      f"{t:.1f} s timed; {note}"}
+            cpu["configs"] = cfg
 
     line = {
         "metric": METRIC,
@@ -416,6 +511,7 @@ def main():
                      "kernel": "w4h::k_step<1,0> (persistent decoder step, whole sweep per launch)",
                      "algorithmic_bytes_per_launch": int(bytes_launch)},
         "cpu_baseline": cpu,
+        "parity": parity,
         "setup": setup,
         "other_configs": configs,
     }

@@ -57,7 +57,6 @@ struct StepParams {
   int mw, probe, topk;
   w4h_step_out* out;            // [nsteps][S] or null
   float* logits_out;            // [nsteps][S][V] or null
-  const float* bias;            // [V] fixed logit bias added before selection, or null
   unsigned* err;
   int rows_per_wg;              // vocab rows one workgroup keeps in LDS in the logits phase
   int ngroups;                  // phase q runs on workgroup group q % ngroups (1 or 2)
@@ -73,6 +72,7 @@ struct StepParams {
   const int32_t* hist0;         // [nhist0] tokens generated before the run
   int nhist0, hist_cap;         // history length before the run; LDS history capacity (>= nhist0 + nsteps)
   size_t rules_off;             // byte offset of the rules region in dynamic LDS
+  const float* bias;            // [V] fixed logit bias added before selection, or null
 };
 
 // Attention partial chunks the one-row out phases keep room for in LDS: every chunk either

@@ -1798,7 +1798,8 @@ DEV bool phase_mlp2(const StepParams& p, const Lds& m, const StepCtx& c, int l, 
 // Final LN + tied-embedding logits over this workgroup's 8-row vocabulary items (items g, g+G, ...)
 // + masks + the workgroup's selection partial per row (a full record and a (max, argmax) pair).
 // The session's fixed logit bias (the beam workload's seeded bias) added to this workgroup's
-// masked and raw rows before selection; the biased raw rows go to logits_out when requested.
+// masked and raw rows before selection; when logits_out is requested the biased raw rows overwrite
+// the unbiased ones the GEMV wrote there.
 DEV void add_bias_rows(const StepParams& p, float* lg, float* rw, const int* lidx, int nl, int S, int rpw, int st) {
   for (int e = threadIdx.x; e < S * nl; e += kThreads) {
     const int s = e / nl, j = e - s * nl, row = lidx[j];
@@ -1852,7 +1853,7 @@ DEV bool phase_logits(const StepParams& p, const Lds& m, const StepCtx& c) {
         rw[s * rpw + li] = v;
         lg[s * rpw + li] = (masked(p.mask, p.mw, s, row) || masked(p.mask2, p.mw, s, row)) ? -INFINITY : v;
         if (s == 0) lidx[li] = row;
-        if (p.logits_out && !p.bias) p.logits_out[((size_t)c.st * S + s) * V + row] = v;
+        if (p.logits_out) p.logits_out[((size_t)c.st * S + s) * V + row] = v;
       } else if (s == 0) {
         lidx[li] = -1;
       }
@@ -1881,7 +1882,7 @@ DEV bool phase_logits(const StepParams& p, const Lds& m, const StepCtx& c) {
     const int last_row0 = (g + (nmine - 1) * G) * 8;
     nl = (nmine - 1) * 8 + min(8, V - last_row0);
   }
-  if (p.bias) add_bias_rows(p, lg, rw, lidx, nl, S, rpw, c.st);
+  if (__builtin_expect(p.bias != nullptr, 0)) add_bias_rows(p, lg, rw, lidx, nl, S, rpw, c.st);
   for (int s = tid >> 6; s < S; s += 4)
     sel_partial(lg + s * rpw, rw + s * rpw, lidx, nl, p.probe, p.topk, rec + s * kSelWords);
   lds_barrier();
@@ -2378,7 +2379,7 @@ DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
         rw[li] = v;
         lg[li] = (masked(p.mask, p.mw, 0, row) || masked(p.mask2, p.mw, 0, row) || rule_masked(p, m, row, li)) ? -INFINITY : v;
         lidx[li] = row;
-        if (p.logits_out && !p.bias) p.logits_out[(size_t)c.st * V + row] = v;
+        if (p.logits_out) p.logits_out[(size_t)c.st * V + row] = v;
       } else {
         lidx[li] = -1;
       }
@@ -2414,7 +2415,7 @@ DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
     const int last_row0 = (g + (nmine - 1) * G) * 8;
     nl = (nmine - 1) * 8 + min(8, V - last_row0);
   }
-  if (p.bias) add_bias_rows(p, lg, rw, lidx, nl, 1, rpw, c.st);
+  if (__builtin_expect(p.bias != nullptr, 0)) add_bias_rows(p, lg, rw, lidx, nl, 1, rpw, c.st);
   if (tid < 64) sel_partial(lg, rw, lidx, nl, p.probe, p.topk, rec);
   lds_barrier();
   kv_drain();
