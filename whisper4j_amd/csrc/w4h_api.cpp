@@ -866,14 +866,17 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
     else if (!strcmp(e, "persistent") && s->S <= kMaxRows) s->wide = false;
   }
   if (s->wide) return create_wide(s, prop, out);
-  // Phase groups (phase q runs on workgroup group q % ngroups, 1 or 2); W4H_NGROUPS overrides the
-  // default of 2 for tuning.  A workgroup owns at most kResItems of the d/8 residual-row items.
+  // Phase groups (1, 2 or 4; see phase_group in the kernels); W4H_NGROUPS overrides the default below
+  // for tuning.  A workgroup owns at most kResItems of the d/8 residual-row items.
+  // One row with at most 4 MLP1 items per quarter workgroup (d <= 512 on 256 CUs): quarters.
+  if (s->S == 1 && d / 2 <= s->grid) s->ngroups = 4;
   if (const char* e = getenv("W4H_NGROUPS")) {
     const int v = atoi(e);
-    if (v == 1 || v == 2) s->ngroups = v;
+    if (v == 1 || v == 2 || v == 4) s->ngroups = v;
   }
-  if (s->grid < 2 * s->ngroups) s->ngroups = 1;
-  if ((d / 8 + s->grid / s->ngroups - 1) / (s->grid / s->ngroups) > kResItems) s->ngroups = 1;
+  while (s->ngroups > 1 && (s->grid < 2 * s->ngroups ||
+                            (d / 8 + s->grid / s->ngroups - 1) / (s->grid / s->ngroups) > kResItems))
+    s->ngroups /= 2;
   if ((d / 8 + s->grid - 1) / s->grid > kResItems)
     return fail(W4H_ERR_INVALID, "n_text_state %d needs more than %d compute units", d, d / (8 * kResItems));
   s->rpw = (((V + 7) / 8 + s->grid - 1) / s->grid) * 8;

@@ -59,7 +59,7 @@ struct StepParams {
   float* logits_out;            // [nsteps][S][V] or null
   unsigned* err;
   int rows_per_wg;              // vocab rows one workgroup keeps in LDS in the logits phase
-  int ngroups;                  // phase q runs on workgroup group q % ngroups (1 or 2)
+  int ngroups;                  // phase groups: 1, 2 (halves) or 4 (quarters); see phase_group
   size_t rep_stride;            // words between replicas of the exchange buffers
   int nres;                     // vocabulary items (8 rows) a workgroup keeps resident in LDS (S = 1)
   size_t res_off;               // byte offset of the resident vocabulary rows in dynamic LDS

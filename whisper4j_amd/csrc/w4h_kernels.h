@@ -1350,15 +1350,24 @@ DEV void wg_layernorm_r(const float* x, float* y, int S, int d, const VecRegs& g
   lds_barrier();
 }
 
-// Workgroup group of a phase.  Consecutive phases run on different groups (phase q on group
-// q % ngroups), so a workgroup has ngroups - 1 phases of idle time in which the weights, key/value
-// rows and parameters of its next phase arrive, while the polling load on any one exchange buffer
-// is spread over fewer workgroups.
+// Workgroup group of a phase.  Consecutive phases run on different groups, so a workgroup has idle
+// phases in which the weights, key/value rows and parameters of its next phase arrive, while fewer
+// workgroups poll any one exchange buffer.  The out-projection, cross-out and MLP2 phases (odd
+// phase numbers) always share one group, which keeps the residual rows in its workgroups' LDS.
+//   ngroups 1: every phase on the whole grid;
+//   ngroups 2: phase q on half q % 2;
+//   ngroups 4: quarters: self-attention on quarter 0, the residual phases on quarter 1,
+//              cross-attention on quarter 2, MLP1 on quarter 3.
 struct Grp {
   int base, size;
 };
 DEV Grp phase_group(int q, int G, int ng) {
   const int sz = G / ng;
+  if (ng == 4) {
+    const int k = q % 6;
+    const int grp = (k & 1) ? 1 : (k == 0 ? 0 : (k == 2 ? 2 : 3));
+    return Grp{grp * sz, sz};
+  }
   return Grp{(q % ng) * sz, sz};
 }
 // First item of this workgroup in the group (items i, i + size, ...), or a value past any item count.
@@ -1909,8 +1918,13 @@ DEV bool phase_reduce(const StepParams& p, const Lds& m, const StepCtx& c) {
   // items to the first workgroups of their groups, so the merge stays off the next step's path.
   const Grp g0 = phase_group(0, G, ng), g1 = phase_group(1, G, ng);
   const int writer = G - 1;
+  // A workgroup of those groups that has no item in them at the next step skips the wait (the item
+  // counts are the phases' own: self-attention S * H * (cached chunks + 2), out-projection d / 8).
   // With decode rules every workgroup keeps the token history, so every workgroup needs the token.
-  const bool need_tok = !last_step && (p.rules || (g >= g0.base && g < g0.base + g0.size) || (g >= g1.base && g < g1.base + g1.size));
+  const int kvn = c.kv + 1;
+  const int self_items = S * p.H * ((kvn + kSelfChunk - 1) / kSelfChunk + 2), out_items = (p.d + 7) / 8;
+  const bool need_tok = !last_step && (p.rules || (g >= g0.base && g < g0.base + g0.size && g - g0.base < self_items) ||
+                                       (g >= g1.base && g < g1.base + g1.size && g - g1.base < out_items));
   const bool is_writer = g == writer && p.out != nullptr;
   if (!need_tok && !is_writer) return true;
   float* pairs = m.big;  // [G][S][2]
@@ -2416,11 +2430,27 @@ DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
     nl = (nmine - 1) * 8 + min(8, V - last_row0);
   }
   if (__builtin_expect(p.bias != nullptr, 0)) add_bias_rows(p, lg, rw, lidx, nl, 1, rpw, c.st);
-  if (tid < 64) sel_partial(lg, rw, lidx, nl, p.probe, p.topk, rec);
+  if (tid < 64) {
+    // The (max, argmax) pair goes out first: the next step waits on it, while the full record
+    // (log-sum-exp, top-k, probe) only feeds the step outputs.  Same order and ties as sel_partial.
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int j = tid; j < nl; j += 64) {
+      const float v = lg[j];
+      const int id = lidx[j];
+      if (v > bv || (v == bv && id < bi)) {
+        bv = v;
+        bi = id;
+      }
+    }
+    wave_argmax(bv, bi);
+    // this wave appended the step's self-KV rows: they are complete before the pair is visible
+    kv_drain();
+    if (tid < 2) ll_st(p.lpa + (size_t)g * 2 + tid, tid == 0 ? bv : __int_as_float(bi), c.tag, p.rep_stride);
+    sel_partial(lg, rw, lidx, nl, p.probe, p.topk, rec);
+  }
   lds_barrier();
-  kv_drain();
   for (int i = tid; i < kSelWords; i += kThreads) ll_st(p.lp + (size_t)g * kSelWords + i, rec[i], c.tag, p.rep_stride);
-  if (tid < 2) ll_st(p.lpa + (size_t)g * 2 + tid, rec[tid], c.tag, p.rep_stride);
   return true;
 }
 
