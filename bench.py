@@ -339,6 +339,40 @@ def measure_greedy_driver(w4h, synth, name, n_tokens):
     return out
 
 
+def measure_sampled_driver(w4h, synth, name, n_tokens, temperature=0.6, seed=3):
+    """The library's decode driver at temperature > 0 (w4h_decode: prompt prefill, then sampled
+    tokens with the suppress, n-gram and timestamp rules; EOT suppressed so every token runs), with
+    the sampling on the device (a sampling kernel chained after each one-step launch, no host round
+    trip per token) and, for comparison, on the host (each logits row fetched and sampled there).
+    Returns {mode: (tokens/s, us per token)}."""
+    from whisper4j_amd.decoder import WhisperDecoder
+
+    dims = synth.SHAPES[name]
+    T = synth.make_decoder(dims, seed=0, wtype="f16")
+    model = w4h.Model.from_tensors(dims, T)
+    xa = synth.encoder_output(dims, 0)
+    eot, tsb = 50256, 50363
+    prompt = list(synth.BENCH_PREFIX)
+    out = {}
+    old = os.environ.get("W4H_DEVICE_SAMPLE")
+    for mode, env in (("device_sampling", "1"), ("host_loop", "0")):
+        os.environ["W4H_DEVICE_SAMPLE"] = env
+        dec = WhisperDecoder(model, beam_size=1, max_ctx=dims.n_text_ctx)
+        dec.decode(xa, prompt, eot, 16, suppress_tokens=[eot], temperature=temperature, seed=seed, timestamp_begin=tsb)
+        t0 = time.perf_counter()
+        r = dec.decode(xa, prompt, eot, n_tokens, suppress_tokens=[eot], temperature=temperature, seed=seed,
+                       timestamp_begin=tsb)
+        dt = time.perf_counter() - t0
+        dec.close()
+        out[mode] = (len(r.tokens) / dt, dt * 1e6 / len(r.tokens))
+    if old is None:
+        os.environ.pop("W4H_DEVICE_SAMPLE", None)
+    else:
+        os.environ["W4H_DEVICE_SAMPLE"] = old
+    model.close()
+    return out
+
+
 def other_configs(w4h, synth):
     """Absolute decode rates of the four other workload shapes (one bounded run each)."""
     out = {}
@@ -350,6 +384,11 @@ def other_configs(w4h, synth):
         "tokens_per_s": round(drv["device_rules"][0], 1), "us_per_token": round(drv["device_rules"][1], 2),
         "rules": "on the device, one launch",
         "host_loop_tokens_per_s": round(drv["host_loop"][0], 1), "host_loop_us_per_token": round(drv["host_loop"][1], 2)}
+    smp = measure_sampled_driver(w4h, synth, "base.en", 224)
+    out["base.en sampled decode driver w4h_decode at T = 0.6, 224 tokens (prompt prefill, then sampled tokens with suppress + n-gram + timestamp rules; EOT suppressed)"] = {
+        "tokens_per_s": round(smp["device_sampling"][0], 1), "us_per_token": round(smp["device_sampling"][1], 2),
+        "sampling": "on the device, one sampling kernel after each one-step launch",
+        "host_loop_tokens_per_s": round(smp["host_loop"][0], 1), "host_loop_us_per_token": round(smp["host_loop"][1], 2)}
     sps, hps, us, steps, frac = measure_beam(w4h, synth, "small", 224, 5)
     out["small beam 5, 224 steps (library beam driver w4h_decode_beam: prompt prefill, then the search on the device; seeded logit bias N(0,1), end token at -inf)"] = {
         "steps_per_s": round(sps, 1), "hypothesis_tokens_per_s": round(hps, 1), "us_per_step": round(us, 2),
@@ -378,7 +417,7 @@ def main():
                     help="timed oracle forwards per other workload for its CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the tiny/small/turbo/medium lines")
-    ap.add_argument("--only", choices=["turbo", "small-beam-rows", "greedy-driver", "medium", "tiny"],
+    ap.add_argument("--only", choices=["turbo", "small-beam-rows", "greedy-driver", "sampled-driver", "medium", "tiny"],
                     help="run only this other workload (one JSON line; for profiling it alone)")
     ap.add_argument("--only-steps", type=int, default=224, help="forced steps of the --only workload")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -402,6 +441,11 @@ def main():
         if args.only == "greedy-driver":
             drv = measure_greedy_driver(w4h, synth, "base.en", n)
             print(json.dumps({"workload": f"base.en greedy decode driver, {n} tokens",
+                              **{k: {"tokens_per_s": round(v[0], 1), "us_per_token": round(v[1], 2)} for k, v in drv.items()}}))
+            return
+        if args.only == "sampled-driver":
+            drv = measure_sampled_driver(w4h, synth, "base.en", n)
+            print(json.dumps({"workload": f"base.en sampled decode driver (T = 0.6), {n} tokens",
                               **{k: {"tokens_per_s": round(v[0], 1), "us_per_token": round(v[1], 2)} for k, v in drv.items()}}))
             return
         if args.only == "turbo":

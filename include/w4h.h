@@ -222,6 +222,17 @@ int w4h_op_attention(const float* q, const uint16_t* k, const uint16_t* v, int32
  * logsumexp and top-k (k <= W4H_TOPK_MAX). */
 int w4h_op_select(const float* logits, int32_t rows, int32_t n, const uint32_t* mask, int32_t k, w4h_step_out* out);
 
+/* The sampling step of a decode at temperature > 0 on one logits row [n] (n <= 65536), as the
+ * device-sampled decode runs it: the suppress bitmask (nullable, [ceil(n/32)]), the n-gram repeats of
+ * history[n_history] and the timestamp rules after the first step (timestamp_begin <= 0: none) set
+ * tokens to -inf; then WhisperDecoder.sample with the first SplitMix64 draw after rng_state picks
+ * *token, and *logprob is the log-probability the decode loop adds for it (logSoftmax over the
+ * weights sample leaves in the row).  main/nn/WhisperDecoder.java:176-195, 457-466, 484-564,
+ * 576-598, 614-626. */
+int w4h_op_sample(const float* logits, int32_t n, const uint32_t* suppress_mask, const int32_t* history,
+                  int32_t n_history, int32_t eot, int32_t timestamp_begin, float temperature, uint64_t rng_state,
+                  int32_t* token, double* logprob);
+
 /* No counterpart in the reference: w4h_op_select for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  logits [rows][n],
  * mask (nullable) [rows][ceil(n/32)] and out [rows] are DEVICE pointers on the calling thread's

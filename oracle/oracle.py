@@ -99,6 +99,8 @@ def lib():
                                           ctypes.c_int]
         L.orc_needs_fallback.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_float]
         L.orc_sample_u.argtypes = [_f32p, ctypes.c_int, ctypes.c_float, ctypes.c_double]
+        L.orc_log_softmax_at.restype = ctypes.c_double
+        L.orc_log_softmax_at.argtypes = [_f32p, ctypes.c_int, ctypes.c_int]
         L.orc_splitmix64_next.restype = ctypes.c_uint64
         L.orc_splitmix64_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
         L.orc_rng_uniform.restype = ctypes.c_double
@@ -258,6 +260,11 @@ def sample_u(row, temperature, u):
     r = f32(row).copy()
     k = lib().orc_sample_u(_p(r), r.size, ctypes.c_float(temperature), ctypes.c_double(u))
     return int(k), r
+
+
+def log_softmax_at(row, index) -> float:
+    r = f32(row)
+    return float(lib().orc_log_softmax_at(_p(r), r.size, int(index)))
 
 
 def splitmix64(seed, n):

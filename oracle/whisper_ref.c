@@ -716,6 +716,8 @@ static double log_softmax_at(const float* l, int n, int index) { /* :614-626 */
   return (double)(l[index] - max) - log(logSum);
 }
 
+double orc_log_softmax_at(const float* l, int n, int index) { return log_softmax_at(l, n, index); }
+
 /* suppressBlank :450-455 */
 void orc_suppress_blank(float* l, int n, int eot) {
   l[eot] = -INFINITY;

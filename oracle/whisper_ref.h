@@ -101,6 +101,8 @@ void orc_timestamp_rules(float* logits, const int32_t* gen, int cnt, int ts_begi
 int orc_needs_fallback(float compression_ratio, float avg_logprob, float no_speech_prob); /* :435-440 */
 /* sample (:576-598) with the uniform draw u in [0,1) given; overwrites logits with exp weights */
 int orc_sample_u(float* logits, int n, float temperature, double u);
+/* logSoftmax (:614-626) of one entry: (l[index] - max) - log(sum exp(l - max)), exp and sum in double */
+double orc_log_softmax_at(const float* l, int n, int index);
 /* SplitMix64 (the seeded stand-in for Math.random): next 64-bit output, and a double in [0,1) */
 uint64_t orc_splitmix64_next(uint64_t* state);
 double orc_rng_uniform(uint64_t* state);

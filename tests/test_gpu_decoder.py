@@ -419,6 +419,31 @@ def test_sampled_decode_matches_oracle(gpu, orc, temperature, seed):
         assert min(marg[: first + 1]) < 1e-4, f"decodes part at step {first} with every draw margin >= 1e-4"
 
 
+@pytest.mark.parametrize("temperature,seed,ts_begin,rows", [(0.6, 7, -1, 1), (1.0, 21, 500, 1), (0.4, 9, -1, 3)])
+def test_device_sampling_equals_host_sampling(gpu, monkeypatch, temperature, seed, ts_begin, rows):
+    """A decode at T > 0 samples every step after the first on the device (w4h_sample.hip, chained
+    after one-step launches of the step kernel, the token handed over in device memory).  Against the
+    host loop that fetches each row and samples it (W4H_DEVICE_SAMPLE=0) on the same session, inputs
+    and seed: identical tokens and average log-probability within 1e-9 (both draw from the device's
+    logits with the same generator; the rules and the suppress list run on both sides)."""
+    T, xa = _fb_model(seed=73)
+    m = gpu.Model.from_tensors(FB_DIMS, T)
+    dec = gpu.WhisperDecoder(m, beam_size=rows)
+    prompt, eot, sup = [10, 11, 12], 599, [1, 2]
+    res = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("W4H_DEVICE_SAMPLE", mode)
+        res[mode] = dec.decode(xa, prompt, eot, 120, sup, temperature=temperature, seed=seed, timestamp_begin=ts_begin)
+    dec.close()
+    m.close()
+    h, d = res["0"], res["1"]
+    say(f"T={temperature} seed={seed} ts={ts_begin} rows={rows}: host {len(h.tokens)} tokens avg {h.avg_logprob:.6f}, "
+        f"device {len(d.tokens)} tokens avg {d.avg_logprob:.6f}")
+    assert d.tokens == h.tokens
+    assert abs(d.avg_logprob - h.avg_logprob) <= 1e-6
+    assert len(d.tokens) > 5
+
+
 @pytest.mark.parametrize("beam", [1, 3])
 def test_decode_with_fallback_matches_oracle(gpu, orc, beam):
     """WhisperDecoder.decodeWithFallback (main/nn/WhisperDecoder.java:119-149) on a model whose greedy

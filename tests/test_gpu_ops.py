@@ -2,6 +2,8 @@
 oracle on the same inputs.  Integer/table work is bit-exact; floating-point work is held to the
 bound stated in each test."""
 
+import math
+
 import numpy as np
 import pytest
 
@@ -109,3 +111,74 @@ def test_select(gpu):
         order = sorted(range(V), key=lambda i: (-row[i], i))[:6]
         fin = [i for i in order if np.isfinite(row[i])]
         assert res[r].topk_ids[: len(fin)] == fin
+
+
+def _oracle_sample(orc, row, temperature, rng_state, history, eot, ts_begin, suppress):
+    """The oracle's sampling step of a decode at T > 0 after the first step: the rules, sample with the
+    first draw after rng_state, the log-probability of the decode loop (over the rewritten row), and
+    the draw's distance from the nearest cumulative-weight edge relative to the total."""
+    r = orc.apply_suppress(row, suppress)
+    r = orc.ngram_block(orc.ngram_block(r, history, 3), history, 4)
+    if ts_begin > 0:
+        r = orc.timestamp_rules(r, history, ts_begin, eot, first_step=False)
+    u = orc.rng_uniform(rng_state, 1)[0]
+    k, w = orc.sample_u(r, temperature, u)
+    lp = orc.log_softmax_at(w, k)
+    cum = np.cumsum(w.astype(np.float64))
+    total = float(np.exp(((r - r.max()) / np.float32(temperature)).astype(np.float64)).sum())
+    rr = u * total
+    edge = float(np.min(np.abs(cum - rr))) / total
+    return k, lp, edge
+
+
+@pytest.mark.parametrize("V,temperature", [(51864, 0.2), (51864, 0.6), (51865, 1.0), (600, 0.4)])
+def test_sample_matches_oracle(gpu, orc, V, temperature):
+    """The device sampling step (w4h_op_sample, the kernel the T > 0 decode runs after each step)
+    against the oracle's rules + sample + logSoftmax (main/nn/WhisperDecoder.java:176-195, 576-598,
+    614-626) on the same row and draw: the same token wherever the draw lies further than 1e-9
+    (relative) from a cumulative-weight edge, and the log-probability within 1e-9."""
+    rng = np.random.default_rng(V + int(temperature * 10))
+    eot, tsb = (V - 50, V - 40) if V > 1000 else (V - 1, -1)
+    cases = [
+        ([], [], -1),
+        ([5, 6, 7, 5, 6], [1, 2, 3], -1),                       # 3-gram repeat: 7 is blocked
+        ([9, 8, 7, 6, 9, 8, 7], [], -1),                         # 4-gram repeat: 6 is blocked
+        ([11, 12, 13, 14], list(range(20, 60)), tsb),            # text after text: timestamp floor
+        ([11, tsb + 3 if tsb > 0 else 3], [], tsb),              # single timestamp after text
+        ([11, tsb + 2 if tsb > 0 else 2, tsb + 5 if tsb > 0 else 5], [], tsb),  # timestamp pair
+    ]
+    checked = 0
+    for ci, (hist, sup, ts) in enumerate(cases):
+        for rep in range(3):
+            row = (rng.standard_normal(V) * 0.5).astype(np.float32)
+            if rep == 2:
+                row[rng.integers(0, V, 20)] = 4.0  # a few dominant ids
+            state = int(rng.integers(0, 2**63))
+            mask = gpu.make_mask(1, V, [sup])[0] if sup else None
+            tok, lp = gpu.op_sample(row, temperature, state, hist, eot=eot, timestamp_begin=ts, suppress_mask=mask)
+            k, lp_o, edge = _oracle_sample(orc, row, temperature, state, hist, eot, ts, sup)
+            if edge > 1e-9:
+                assert tok == k, f"case {ci}.{rep}: device {tok}, oracle {k} (edge {edge:.2e})"
+                assert abs(lp - lp_o) <= 1e-9, f"case {ci}.{rep}: logprob {lp} vs {lp_o}"
+                checked += 1
+    say(f"sample V={V} T={temperature}: {checked}/{3 * len(cases)} draws compared (the rest lie on an edge)")
+    assert checked >= 3 * len(cases) - 2
+
+
+def test_sample_edge_cases(gpu, orc):
+    """Every id but one suppressed: that id is drawn whatever the draw; a row of equal logits draws
+    the id the uniform draw falls on (u * V, by the cumulative sum)."""
+    V = 1000
+    row = np.zeros(V, np.float32)
+    mask = gpu.make_mask(1, V, [[i for i in range(V) if i != 617]])[0]
+    for state in (1, 99, 2**40 + 3):
+        tok, lp = gpu.op_sample(row, 0.7, state, [], eot=V - 1, suppress_mask=mask)
+        assert tok == 617
+        k, lp_o, _ = _oracle_sample(orc, row, 0.7, state, [], V - 1, -1, [i for i in range(V) if i != 617])
+        assert k == 617 and abs(lp - lp_o) <= 1e-9
+    for state in (5, 77):
+        # every weight is exactly 1, so the cumulative weight of id i is i + 1 and r = u * V
+        u = orc.rng_uniform(state, 1)[0]
+        tok, lp = gpu.op_sample(row, 1.0, state, [], eot=V - 1)
+        assert tok == max(0, math.ceil(u * V) - 1)
+        assert abs(lp - (0.0 - math.log(V))) <= 1e-12  # logSoftmax over V weights equal to 1

@@ -282,3 +282,17 @@ def test_beam_unfinished_fill_at_max_tokens(orc):
     assert r["tokens"] == [0, 2, 6]
     a0 = -math.log(1 + math.exp(-1.0))
     assert r["avg_logprob"] == pytest.approx((a0 - math.log(1 + math.exp(-2.0))) / 3, abs=1e-5)
+
+
+# ---- logSoftmax (:614-626) of one entry, as the sampled decode loop takes it --------------------
+
+def test_log_softmax_at_hand_values(orc):
+    # (3 - 3) - log(e^-2 + e^-1 + e^0) = -log(1.5032147244) = -0.40760596444
+    assert orc.log_softmax_at([1.0, 2.0, 3.0], 2) == pytest.approx(-0.40760596444, abs=1e-10)
+    # index 0 of the same row: (1 - 3) - log(1.5032147244) = -2.40760596444
+    assert orc.log_softmax_at([1.0, 2.0, 3.0], 0) == pytest.approx(-2.40760596444, abs=1e-10)
+    # -inf entries add exp(-inf) = 0: two equal finite entries give log(1/2)
+    assert orc.log_softmax_at([NEG, 0.5, 0.5, NEG], 1) == pytest.approx(-math.log(2.0), abs=1e-15)
+    # after sample rewrote a row into weights (max weight 1, a suppressed id weight 0): the decode
+    # loop's logSoftmax sees weights [1, 0, 1]: (1 - 1) - log(1 + e^-1 + 1) = -log(2.3678794412)
+    assert orc.log_softmax_at([1.0, 0.0, 1.0], 0) == pytest.approx(-0.86199480406, abs=1e-10)

@@ -18,5 +18,6 @@ from .decoder import (  # noqa: F401
     op_gelu,
     op_layernorm,
     op_linear,
+    op_sample,
     op_select,
 )

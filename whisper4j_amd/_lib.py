@@ -35,7 +35,8 @@ EXPORTS = (
     "w4h_session_set_probe", "w4h_session_set_logit_bias", "w4h_session_step", "w4h_session_run", "w4h_session_reorder", "w4h_session_time_run",
     "w4h_session_trace_run",
     "w4h_decode", "w4h_decode_beam", "w4h_decode_with_fallback", "w4h_compression_ratio", "w4h_op_linear",
-    "w4h_op_layernorm", "w4h_op_gelu", "w4h_op_attention", "w4h_op_select", "w4h_op_select_noalloc",
+    "w4h_op_layernorm", "w4h_op_gelu", "w4h_op_attention", "w4h_op_select", "w4h_op_sample",
+    "w4h_op_select_noalloc",
 )
 
 
@@ -124,6 +125,8 @@ def lib():
         "w4h_op_gelu": (i32, [f32p, i32, f32p]),
         "w4h_op_attention": (i32, [f32p, u16p, u16p, i32, i32, ctypes.c_float, f32p]),
         "w4h_op_select": (i32, [f32p, i32, i32, u32p, i32, ctypes.POINTER(StepOut)]),
+        "w4h_op_sample": (i32, [f32p, i32, u32p, i32p, i32, i32, i32, ctypes.c_float, ctypes.c_uint64, i32p,
+                                ctypes.POINTER(ctypes.c_double)]),
         "w4h_op_select_noalloc": (i32, [vp, i32, i32, vp, i32, vp, vp]),
     }
     for name, (res, args) in sig.items():

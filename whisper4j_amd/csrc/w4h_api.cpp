@@ -458,6 +458,8 @@ struct w4h_session {
   WideGraph wgraph, wgraph_beam;
   DevBuf wbeam, wbsup;
   bool use_graph = true;
+  // device-sampled decodes (T > 0): sampler state, the step's logits rows, the static suppress mask
+  DevBuf samp, samp_row, samp_sup;
 };
 
 namespace w4h {
@@ -1208,6 +1210,46 @@ int w4h_op_select(const float* logits, int32_t rows, int32_t n, const uint32_t* 
   return W4H_OK;
 }
 
+int w4h_op_sample(const float* logits, int32_t n, const uint32_t* suppress_mask, const int32_t* history,
+                  int32_t n_history, int32_t eot, int32_t timestamp_begin, float temperature, uint64_t rng_state,
+                  int32_t* token, double* logprob) {
+  if (!logits || !token || !logprob || n <= 0 || n > kSampleMaxV || n_history < 0 || n_history >= kSampleHist ||
+      (n_history > 0 && !history) || !(temperature > 0.0f))
+    return fail(W4H_ERR_INVALID, "bad argument");
+  int rc = op_prepare();
+  if (rc) return rc;
+  DevBuf dl, dm, dst;
+  std::vector<char> hb(sizeof(SampleDev), 0);
+  SampleDev* h = reinterpret_cast<SampleDev*>(hb.data());
+  h->n = n_history;
+  if (n_history > 0) std::copy(history, history + n_history, h->hist);
+  if ((rc = upload(dl, logits, (size_t)n * 4))) return rc;
+  if (suppress_mask && (rc = upload(dm, suppress_mask, (size_t)(n + 31) / 32 * 4))) return rc;
+  if ((rc = upload(dst, hb.data(), hb.size()))) return rc;
+  SampleParams sp{};
+  sp.logits = dl.as<float>();
+  sp.sup = suppress_mask ? dm.as<uint32_t>() : nullptr;
+  sp.V = n;
+  sp.eot = eot;
+  sp.tsb = timestamp_begin > 0 ? timestamp_begin : 0;
+  sp.rows = 1;
+  sp.max_steps = 1;
+  sp.temperature = temperature;
+  sp.rng = rng_state;
+  sp.st = dst.as<SampleDev>();
+  sp.parts_out = sp.st->parts;
+  sp.parts = sp.st->parts;
+  sp.nparts = kSampleBlocks;
+  sp.part_stride = 1;
+  HIPCHK(launch_sample_mask(sp, nullptr));
+  HIPCHK(launch_sample(sp, nullptr));
+  HIPCHK(hipMemcpy(hb.data(), dst.p, hb.size(), hipMemcpyDeviceToHost));
+  if (h->steps != 1) return fail(W4H_ERR_DEVICE, "sampling kernel did not run");
+  *token = h->out_tok[0];
+  *logprob = h->lp[0];
+  return W4H_OK;
+}
+
 int w4h_op_select_noalloc(const float* logits, int32_t rows, int32_t n, const uint32_t* mask, int32_t k,
                           w4h_step_out* out, void* stream) {
   if (!logits || !out || rows <= 0 || n <= 0 || k < 0 || k > W4H_TOPK_MAX) return fail(W4H_ERR_INVALID, "bad argument");
@@ -1244,6 +1286,95 @@ int device_greedy_run(w4h_session* s, const RulesRun& r, int n_steps, const uint
   if (r.nhist < 1 || !r.hist) return fail(W4H_ERR_INVALID, "device decode rules need the generated tokens");
   const int32_t tok = r.hist[r.nhist - 1];
   return run_steps(s, &tok, nullptr, n_steps, mask2, 1, out, nullptr, nullptr, nullptr, &r, steps_done);
+}
+
+bool session_device_sample(const w4h_session* s) {
+  if (s->wide || s->S > kMaxRows || s->m->dims.n_vocab > kSampleMaxV) return false;
+  if (const char* e = getenv("W4H_DEVICE_SAMPLE"))
+    if (!strcmp(e, "0")) return false;
+  return true;
+}
+
+// Sampled decode steps chained on the session stream: per step one launch of the step kernel (one
+// step, raw logits of every row into samp_row), one of the masking kernel (the rules applied to row
+// 0 in place) and one of the sampling kernel, which draws the token and leaves it as every row's
+// next input.  After the end token
+// the sampler sets the stop word and the remaining launches of the run return at once.  The host
+// synchronises once per run.
+int device_sampled_run(w4h_session* s, const SampleRun& r, int n_steps, const uint32_t* sup, SampleRunOut* out) {
+  if (!session_device_sample(s)) return fail(W4H_ERR_INVALID, "device sampling needs a persistent session");
+  if (r.nhist < 1 || !r.hist || r.nhist >= kSampleHist) return fail(W4H_ERR_INVALID, "device sampling needs the generated tokens");
+  if (!(r.temperature > 0.0f)) return fail(W4H_ERR_INVALID, "device sampling needs a temperature above 0");
+  if (n_steps < 1 || n_steps > kSampleHist) return fail(W4H_ERR_INVALID, "n_steps outside [1, %d]", kSampleHist);
+  if (s->kv_len + n_steps > s->max_ctx)
+    return fail(W4H_ERR_CAPACITY, "self-KV capacity %d exceeded (kv_len %d + %d steps)", s->max_ctx, s->kv_len, n_steps);
+  if ((uint64_t)s->next_tag + (uint64_t)n_steps >= 0xfffffff0ull) return fail(W4H_ERR_INVALID, "tag space exhausted; recreate the session");
+  const int V = s->m->dims.n_vocab;
+  int rc;
+  HIPCHK(hipSetDevice(s->m->device));
+  if ((rc = ensure(s->samp, sizeof(SampleDev))) || (rc = ensure(s->samp_row, sizeof(float) * (size_t)s->S * V)) ||
+      (rc = ensure(s->samp_sup, sizeof(uint32_t) * (size_t)s->mw)))
+    return rc;
+  std::vector<char> hb(sizeof(SampleDev), 0);
+  SampleDev* h = reinterpret_cast<SampleDev*>(hb.data());
+  h->n = r.nhist;
+  std::copy(r.hist, r.hist + r.nhist, h->hist);
+  for (int q = 0; q < s->S; q++) h->tok[q] = r.hist[r.nhist - 1];
+  // error word (and the slot table, when a reorder changed it) as run_steps stages them
+  char* hp = static_cast<char*>(s->h_in.p);
+  *reinterpret_cast<unsigned*>(hp) = 0u;
+  if (s->slots_dirty) memcpy(hp + s->o_slots, s->slots_host.data(), sizeof(int32_t) * s->slots_host.size());
+  HIPCHK(hipMemcpyAsync(s->in.p, hp, s->slots_dirty ? s->in_bytes : sizeof(unsigned), hipMemcpyHostToDevice, s->stream));
+  s->slots_dirty = false;
+  HIPCHK(hipMemcpyAsync(s->samp.p, hb.data(), offsetof(SampleDev, out_tok), hipMemcpyHostToDevice, s->stream));
+  if (sup) HIPCHK(hipMemcpyAsync(s->samp_sup.p, sup, sizeof(uint32_t) * (size_t)s->mw, hipMemcpyHostToDevice, s->stream));
+  SampleDev* dst = s->samp.as<SampleDev>();
+  SampleParams sp{};
+  sp.logits = s->samp_row.as<float>();
+  sp.sup = sup ? s->samp_sup.as<uint32_t>() : nullptr;
+  sp.V = V;
+  sp.eot = r.eot;
+  sp.tsb = r.tsb;
+  sp.rows = s->S;
+  sp.max_steps = n_steps;
+  sp.temperature = r.temperature;
+  sp.rng = r.rng;
+  sp.st = dst;
+  sp.parts_out = dst->parts;
+  sp.parts = dst->parts;
+  sp.nparts = kSampleBlocks;
+  sp.part_stride = 1;
+  StepParams p = base_params(s);
+  p.nsteps = 1;
+  p.tokens0 = dst->tok;
+  p.mask = nullptr;  // the sampler applies every mask to the raw row itself
+  p.topk = 0;
+  p.out = nullptr;
+  p.logits_out = sp.logits;
+  p.nres = 0;  // one step per launch: loading resident vocabulary rows would not pay
+  p.stop = &dst->stop;
+  {
+    std::unique_lock<std::mutex> coop(coop_lock(s->m->device));
+    for (int i = 0; i < n_steps; i++) {
+      p.kv_len0 = s->kv_len + i;
+      p.tag0 = s->next_tag++;
+      hipError_t le = launch_step(p, s->grid, s->lds, s->stream);
+      if (le != hipSuccess) return fail(W4H_ERR_DEVICE, "decoder step launch failed: %s", hipGetErrorString(le));
+      if ((le = launch_sample_mask(sp, s->stream)) != hipSuccess || (le = launch_sample(sp, s->stream)) != hipSuccess)
+        return fail(W4H_ERR_DEVICE, "sampling launch failed: %s", hipGetErrorString(le));
+    }
+    HIPCHK(hipMemcpyAsync(hb.data(), s->samp.p, sizeof(SampleDev), hipMemcpyDeviceToHost, s->stream));
+    unsigned herr = 0;
+    HIPCHK(hipMemcpyAsync(&herr, s->in.p, sizeof(unsigned), hipMemcpyDeviceToHost, s->stream));
+    HIPCHK(hipStreamSynchronize(s->stream));
+    if (herr) return fail(W4H_ERR_TIMEOUT, "a device-side wait expired during the step (code %u); step aborted", herr);
+  }
+  s->kv_len += h->steps;  // one step-kernel launch ran per sampled step
+  out->steps = h->steps;
+  out->ended = h->steps > 0 && h->out_tok[h->steps - 1] == r.eot;
+  out->tokens.assign(h->out_tok, h->out_tok + h->steps);
+  out->lps.assign(h->lp, h->lp + h->steps);
+  return W4H_OK;
 }
 
 int device_beam_search(w4h_session* s, const BeamSearchIn& in, BeamSearchOut* out) {

@@ -4,7 +4,8 @@
 // The rules depend only on the token history, so they are evaluated on the host as a per-row
 // suppression bitmask; the device applies it inside the logits pass and returns argmax,
 // logsumexp and top-k, so no logits row crosses PCIe on greedy or beam steps.  Sampling (T > 0)
-// needs the full row and fetches it.
+// runs on the device for persistent sessions after the first step (w4h_sample.hip); the host loop
+// below samples only the first step and the steps of batched sessions, from the fetched row.
 
 #include <zlib.h>
 
@@ -222,7 +223,31 @@ int w4h_decode(w4h_session* s, const w4h_decode_opts* o, w4h_decode_result* r) {
   // step kernel from the generated tokens, for as many steps as the self-KV holds (the host loop
   // below takes over if the decode has not ended by then).
   const bool on_device = greedy && w4h::session_device_rules(s);
+  // A sampled decode (T > 0) runs its steps after the first on the device as well: each step's
+  // logits stay in device memory, where the sampling kernel applies the rules and draws the token
+  // with the same generator, continued from the host's state.
+  const bool sample_on_device = !greedy && w4h::session_device_sample(s);
   for (int step = 0; step < o->max_tokens; step++) {
+    if (sample_on_device && step == 1) {
+      int32_t kv = 0;
+      if ((rc = w4h_session_kv_len(s, &kv))) return rc;
+      const int n = std::min(o->max_tokens - 1, (int)(w4h::session_max_ctx(s) - kv));
+      if (n > 0) {
+        Mask sup(V, 1);
+        apply_suppress(sup, 0, o->suppress, o->n_suppress);
+        const w4h::SampleRun sr{gen.data(), (int)gen.size(), o->eot, o->timestamp_begin > 0 ? o->timestamp_begin : 0,
+                                o->temperature, rng.s};
+        w4h::SampleRunOut so;
+        if ((rc = w4h::device_sampled_run(s, sr, n, sup.bits.data(), &so))) return rc;
+        rng.s += (uint64_t)so.steps * 0x9e3779b97f4a7c15ull;  // the draws the device took
+        for (int i = 0; i < so.steps; i++) {
+          sumLogprob += so.lps[i];
+          if (so.tokens[i] != o->eot) gen.push_back(so.tokens[i]);
+        }
+        step = 1 + so.steps;
+        if (so.ended || step >= o->max_tokens) break;
+      }
+    }
     if (on_device && step == 1) {
       int32_t kv = 0;
       if ((rc = w4h_session_kv_len(s, &kv))) return rc;

@@ -44,4 +44,24 @@ bool session_device_rules(const w4h_session* s);
 int session_max_ctx(const w4h_session* s);
 int device_greedy_run(w4h_session* s, const RulesRun& r, int n_steps, const uint32_t* mask2, w4h_step_out* out,
                       int* steps_done);
+
+// Sampled decode steps (temperature > 0) on the device for persistent sessions: the run starts with
+// the last generated token; after every step the sampling kernel applies the suppress mask `sup`
+// and the history rules to row 0, draws the next token from the SplitMix64 generator in state `rng`
+// (the run's step k takes its (k + 1)-th output) and feeds it to every row; the run ends after the
+// end token or n_steps steps.
+struct SampleRun {
+  const int32_t* hist;  // tokens generated so far (the last one is the run's first input)
+  int nhist, eot, tsb;
+  float temperature;
+  uint64_t rng;
+};
+struct SampleRunOut {
+  int steps = 0;      // steps run (each sampled one token and appended one self-KV row)
+  bool ended = false; // the last sampled token is the end token
+  std::vector<int32_t> tokens;
+  std::vector<double> lps;
+};
+bool session_device_sample(const w4h_session* s);
+int device_sampled_run(w4h_session* s, const SampleRun& r, int n_steps, const uint32_t* sup, SampleRunOut* out);
 }  // namespace w4h

@@ -73,7 +73,49 @@ struct StepParams {
   int nhist0, hist_cap;         // history length before the run; LDS history capacity (>= nhist0 + nsteps)
   size_t rules_off;             // byte offset of the rules region in dynamic LDS
   const float* bias;            // [V] fixed logit bias added before selection, or null
+  const int* stop;              // device word: the launch does nothing when it is non-zero (chained
+                                // sampled decodes), or null
 };
+
+// Device temperature sampling of one decode row (WhisperDecoder.sample and the log-probability the
+// decode loop takes of the sampled token, main/nn/WhisperDecoder.java:186-187, 576-598, 614-626).
+// A masking kernel applies the rules to the raw row in place and records the maximum of each
+// block's part of it; the sampling kernel runs kSampleBlocks workgroups, block b owning the vocabulary range
+// [b * kSampleSpan, (b + 1) * kSampleSpan) and thread t of it the kSamplePer entries from t * that,
+// so per-block sums in block order and a block scan inside the chosen block give the cumulative
+// weights in vocabulary order.  The last block to finish draws the token.
+constexpr int kSampleBlocks = 64;
+constexpr int kSamplePer = 4;
+constexpr int kSampleSpan = kSamplePer * kThreads;          // 1024 entries per block
+constexpr int kSampleMaxV = kSampleBlocks * kSampleSpan;   // 65536
+constexpr int kSampleHist = 1024;  // generated tokens a sampled run keeps (the decode limit)
+struct SampleDev {
+  int n;                         // generated tokens in hist
+  int steps;                     // steps sampled by this run
+  int stop;                      // set after the end token or the last step of the run
+  unsigned done;                 // blocks of the current sampling launch that have finished
+  int32_t tok[kMaxRows];         // input token of the next step, every row
+  u64 parts[kSampleBlocks];      // per-block maxima of the masked row (low 32 bits)
+  double bsum[kSampleBlocks][3]; // per-block sums: double weights, float weights, exp(weight - 1)
+  int32_t hist[kSampleHist];     // generated tokens (the end token is never appended)
+  int32_t out_tok[kSampleHist];  // token sampled at each step of the run (the end token included)
+  double lp[kSampleHist];        // its log-probability, as the decode loop accumulates it
+};
+struct SampleParams {
+  float* logits;        // [V] masked logits of the row (bias included); overwritten with the weights
+  const u64* parts;     // maxima of parts of the row: low 32 bits of parts[k * part_stride], k < nparts
+  int nparts, part_stride;
+  int V, eot, rows, max_steps;
+  float temperature;
+  uint64_t rng;         // SplitMix64 state before the run's first draw; step k of the run draws k + 1
+  SampleDev* st;
+  // the masking kernel (rules from st->hist)
+  const uint32_t* sup;  // [ceil(V / 32)] static suppress bitmask, or null
+  int tsb;              // first timestamp token (<= 0: no timestamp rules)
+  u64* parts_out;       // [kSampleBlocks] per-block maxima it writes
+};
+hipError_t launch_sample_mask(const SampleParams& p, hipStream_t st);
+hipError_t launch_sample(const SampleParams& p, hipStream_t st);
 
 // Attention partial chunks the one-row out phases keep room for in LDS: every chunk either
 // attention phase produces, and with q8_0 weights at least kMergeChunks (their attn_merge reads that

@@ -2457,6 +2457,8 @@ DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
 template <int SM, int WQ8, int DR>
 __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
   extern __shared__ float lds_raw[];
+  // a chained sampled decode that has ended: nothing left to compute (uniform across the grid)
+  if (__builtin_expect(p.stop != nullptr, 0) && *p.stop) return;
   const int tid = threadIdx.x, S = p.S, d = p.d;
   Lds m;
   // persistent: scratch words, tokens, residual rows; then the per-phase region

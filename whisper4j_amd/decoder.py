@@ -327,6 +327,18 @@ def op_select(logits, k=0, mask=None):
     return [StepResult._from(out[i], k) for i in range(lg.shape[0])]
 
 
+def op_sample(logits, temperature, rng_state, history=(), eot=0, timestamp_begin=-1, suppress_mask=None):
+    """The device sampling step of a T > 0 decode on one row: (token, log-probability)."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32).ravel()
+    m = np.ascontiguousarray(suppress_mask, dtype=np.uint32).ravel() if suppress_mask is not None else None
+    h = np.ascontiguousarray(list(history) or [0], dtype=np.int32)
+    tok, lp = ctypes.c_int32(0), ctypes.c_double(0.0)
+    check(lib().w4h_op_sample(_ptr(lg, _f32p), lg.size, _ptr(m, _u32p), _ptr(h, _i32p), len(history), eot,
+                              timestamp_begin, ctypes.c_float(temperature), ctypes.c_uint64(rng_state),
+                              ctypes.byref(tok), ctypes.byref(lp)))
+    return int(tok.value), float(lp.value)
+
+
 def make_mask(rows: int, vocab: int, ids_per_row) -> np.ndarray:
     """Bitmask [rows][ceil(vocab/32)] with the listed token ids set."""
     mw = (vocab + 31) // 32
