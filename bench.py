@@ -373,6 +373,40 @@ def measure_sampled_driver(w4h, synth, name, n_tokens, temperature=0.6, seed=3):
     return out
 
 
+def encoder_flops(ed):
+    """Algorithmic FLOPs of one encoder forward: conv1 over 2T frames, conv2 over T, per layer the
+    q/k/v/out projections and the MLP (24 T d^2) and the attention products (4 T^2 d)."""
+    T, d, nm, L = ed.n_audio_ctx, ed.n_audio_state, ed.n_mels, ed.n_audio_layer
+    conv = 2 * (2 * T) * d * 3 * nm + 2 * T * d * 3 * d
+    gemm = L * 24 * T * d * d
+    attn = L * 4 * T * T * d
+    return conv + gemm, attn
+
+
+def measure_encoder(w4h, synth, name, reps=5):
+    """WhisperEncoder.forward on the GPU (w4h_encoder_forward_device: mel and output in device memory,
+    the call returns when the output is written), seed-0 f16 weights and mel, wall clock per forward
+    over `reps` forwards after one warm-up.  MFMA work: two f16 products per GEMM multiply-add
+    (activation hi/lo) and three per attention product."""
+    from whisper4j_amd.device import DeviceArray
+
+    ed = synth.ENC_SHAPES[name]
+    T = synth.make_encoder(ed, seed=0)
+    mel = synth.mel_input(ed, 0)
+    enc = w4h.Encoder.from_tensors(ed, T)
+    with DeviceArray(mel) as dm, DeviceArray(np.zeros((ed.n_audio_ctx, ed.n_audio_state), np.float32)) as dx:
+        enc.forward_device(dm.address, dx.address)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            enc.forward_device(dm.address, dx.address)
+        dt = (time.perf_counter() - t0) / reps
+    enc.close()
+    gf, af = encoder_flops(ed)
+    mfma = 2 * gf + 3 * af
+    return {"ms": round(dt * 1e3, 3), "gflop": round((gf + af) / 1e9, 1), "tflop_s": round((gf + af) / dt / 1e12, 1),
+            "mfma_tflop_s": round(mfma / dt / 1e12, 1), "mfma_frac_of_f16_peak": round(mfma / dt / 2.5e15, 4)}
+
+
 def other_configs(w4h, synth):
     """Absolute decode rates of the four other workload shapes (one bounded run each)."""
     out = {}
@@ -403,6 +437,8 @@ def other_configs(w4h, synth):
     tps, us, frac, setup = measure_forced(w4h, synth, "medium", "q8_0", 444, 2)
     out["medium q8_0 greedy b=1, 444 forced steps"] = {"tokens_per_s": round(tps, 1), "us_per_step": round(us, 2),
                                                       "roofline_frac": round(frac, 4), "setup": setup}
+    out["audio encoder forward (80/128 mels x 3000 frames -> 1500 frames, f16 weights, MFMA)"] = {
+        name: measure_encoder(w4h, synth, name) for name in ("tiny.en", "base.en", "large-v3-turbo")}
     return out
 
 
@@ -417,7 +453,8 @@ def main():
                     help="timed oracle forwards per other workload for its CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the tiny/small/turbo/medium lines")
-    ap.add_argument("--only", choices=["turbo", "small-beam-rows", "greedy-driver", "sampled-driver", "medium", "tiny"],
+    ap.add_argument("--only", choices=["turbo", "small-beam-rows", "greedy-driver", "sampled-driver", "medium", "tiny",
+                                       "encoder"],
                     help="run only this other workload (one JSON line; for profiling it alone)")
     ap.add_argument("--only-steps", type=int, default=224, help="forced steps of the --only workload")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -442,6 +479,10 @@ def main():
             drv = measure_greedy_driver(w4h, synth, "base.en", n)
             print(json.dumps({"workload": f"base.en greedy decode driver, {n} tokens",
                               **{k: {"tokens_per_s": round(v[0], 1), "us_per_token": round(v[1], 2)} for k, v in drv.items()}}))
+            return
+        if args.only == "encoder":
+            print(json.dumps({"workload": "audio encoder forward", **{k: measure_encoder(w4h, synth, k)
+                                                                       for k in ("tiny.en", "base.en", "large-v3-turbo")}}))
             return
         if args.only == "sampled-driver":
             drv = measure_sampled_driver(w4h, synth, "base.en", n)

@@ -91,6 +91,35 @@ int w4h_ggml_inspect(const char* path, w4h_dims* dims, int32_t* n_tensors, int64
 int w4h_ggml_read_tensor(const char* path, const char* name, int32_t* type, int32_t* n_dims, int64_t ne[4],
                          void* dst, int64_t dst_bytes);
 
+/* ================================ encoder ================================ */
+/* The audio encoder (WhisperEncoder, main/nn/WhisperEncoder.java:27-76): conv1 + GELU, conv2 (stride
+ * 2) + GELU, + positional embedding, n_audio_layer pre-LN blocks of self-attention over the frames and
+ * a GELU MLP, ln_post.  Its output is the decoder's xa (w4h_session_set_encoder[_device]). */
+
+typedef struct w4h_encoder w4h_encoder;
+
+typedef struct {
+  int32_t n_mels, n_audio_ctx, n_audio_state, n_audio_head, n_audio_layer;
+} w4h_encoder_dims;
+
+/* Upload an encoder from a tensor table ("encoder.conv1.weight", "encoder.blocks.i.attn.query.weight",
+ * ... as whisper.cpp GGML files name them): WhisperEncoder(WeightStore, ModelDimensions),
+ * main/nn/WhisperEncoder.java:27-38, 86-105.  Matrices f16 / f32 (rounded to f16) or q8_0, conv
+ * weights f16 / f32; the key projection has no bias.  A handle must not be used after destroy. */
+int w4h_encoder_create(const w4h_encoder_dims* dims, const w4h_tensor* tensors, int32_t n_tensors, int32_t device,
+                       w4h_encoder** out);
+/* Parse a whisper.cpp GGML file (mmap) and upload its encoder (hparams n_audio_*, n_mels). */
+int w4h_encoder_load_ggml(const char* path, int32_t device, w4h_encoder** out);
+int w4h_encoder_get_dims(const w4h_encoder* e, w4h_encoder_dims* out);
+/* WhisperEncoder.forward (main/nn/WhisperEncoder.java:42-76): mel [n_mels][2 * n_audio_ctx] fp32 (host
+ * memory) -> out [n_audio_ctx][n_audio_state] fp32 (host memory). */
+int w4h_encoder_forward(w4h_encoder* e, const float* mel, float* out);
+/* The same with mel and out in device memory of the encoder's device, enqueued on `stream` (a
+ * hipStream_t) and not waited for; NULL runs on the encoder's own stream and returns when done.  out
+ * can go straight to w4h_session_set_encoder_device.  One forward at a time per encoder. */
+int w4h_encoder_forward_device(w4h_encoder* e, const float* mel_dev, float* out_dev, void* stream);
+int w4h_encoder_destroy(w4h_encoder* e);
+
 /* =============================== session ================================ */
 
 typedef struct w4h_session w4h_session;

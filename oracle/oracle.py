@@ -29,6 +29,11 @@ class OrcDims(ctypes.Structure):
                 ("n_text_head", ctypes.c_int32), ("n_text_layer", ctypes.c_int32), ("n_audio_ctx", ctypes.c_int32)]
 
 
+class OrcEncDims(ctypes.Structure):
+    _fields_ = [("n_mels", ctypes.c_int32), ("n_audio_ctx", ctypes.c_int32), ("n_audio_state", ctypes.c_int32),
+                ("n_audio_head", ctypes.c_int32), ("n_audio_layer", ctypes.c_int32)]
+
+
 class OrcResult(ctypes.Structure):
     _fields_ = [("n_tokens", ctypes.c_int32), ("tokens", ctypes.c_int32 * 1024), ("avg_logprob", ctypes.c_float),
                 ("compression_ratio", ctypes.c_float), ("no_speech_prob", ctypes.c_float),
@@ -99,6 +104,14 @@ def lib():
                                           ctypes.c_int]
         L.orc_needs_fallback.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_float]
         L.orc_sample_u.argtypes = [_f32p, ctypes.c_int, ctypes.c_float, ctypes.c_double]
+        L.orc_encoder_create.restype = ctypes.c_void_p
+        L.orc_encoder_create.argtypes = [ctypes.POINTER(OrcEncDims), ctypes.POINTER(OrcTensor), ctypes.c_int,
+                                         ctypes.c_char_p, ctypes.c_int]
+        L.orc_encoder_destroy.argtypes = [ctypes.c_void_p]
+        L.orc_encoder_forward.restype = ctypes.c_int
+        L.orc_encoder_forward.argtypes = [ctypes.c_void_p, _f32p, _f32p]
+        L.orc_conv1d.argtypes = [_f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                 _f32p, ctypes.c_int, _f32p]
         L.orc_log_softmax_at.restype = ctypes.c_double
         L.orc_log_softmax_at.argtypes = [_f32p, ctypes.c_int, ctypes.c_int]
         L.orc_splitmix64_next.restype = ctypes.c_uint64
@@ -349,6 +362,59 @@ def beam_drive(src, eot, max_tokens, beam, suppress=(), no_speech=-1, ts_begin=-
 
 
 # ---- model ---------------------------------------------------------------------------------
+
+def conv1d(w, bias, stride, pad, x):
+    """Conv1d.forward (w [out][in][k], x [in][len]) -> [out][out_len]."""
+    w, x = f32(w), f32(x)
+    out_ch, in_ch, k = w.shape
+    n = x.shape[1]
+    out = np.empty((out_ch, (n + 2 * pad - k) // stride + 1), np.float32)
+    b = f32(bias) if bias is not None else None
+    lib().orc_conv1d(_p(w), _p(b) if b is not None else None, out_ch, in_ch, k, stride, pad, _p(x), n, _p(out))
+    return out
+
+
+class Encoder:
+    """Oracle audio encoder (WhisperEncoder) from a GGML tensor table."""
+
+    def __init__(self, edims, tensors):
+        self.edims = edims
+        self._keep = []
+        arr = (OrcTensor * len(tensors))()
+        for i, t in enumerate(tensors):
+            raw = np.ascontiguousarray(t.raw())
+            nm = t.name.encode()
+            self._keep += [raw, nm]
+            arr[i].name = nm
+            arr[i].type = t.ggml_type
+            arr[i].n_dims = len(t.ne)
+            for j, v in enumerate(t.ne):
+                arr[i].ne[j] = int(v)
+            arr[i].data = raw.ctypes.data
+        self._dims = OrcEncDims(edims.n_mels, edims.n_audio_ctx, edims.n_audio_state, edims.n_audio_head,
+                                edims.n_audio_layer)
+        err = ctypes.create_string_buffer(256)
+        self._h = lib().orc_encoder_create(ctypes.byref(self._dims), arr, len(tensors), err, 256)
+        if not self._h:
+            raise RuntimeError(err.value.decode())
+
+    def forward(self, mel) -> np.ndarray:
+        m = f32(mel)
+        out = np.empty((self.edims.n_audio_ctx, self.edims.n_audio_state), np.float32)
+        lib().orc_encoder_forward(self._h, _p(m), _p(out))
+        return out
+
+    def close(self):
+        if self._h:
+            lib().orc_encoder_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
 
 class Model:
     """Oracle decoder built from a GGML tensor table (list of whisper4j_amd.synth.GgmlTensor)."""

@@ -819,6 +819,182 @@ int orc_needs_fallback(float compression_ratio, float avg_logprob, float no_spee
 }
 
 /* ------------------------------------------------------------------------------------------ */
+/* Audio encoder: WhisperEncoder (main/nn/WhisperEncoder.java:27-76).                           */
+
+typedef struct {
+  orc_lin q, k, v, o, mlp1, mlp2;
+  float *attn_ln_g, *attn_ln_b, *mlp_ln_g, *mlp_ln_b;
+} orc_enc_block;
+
+struct orc_encoder {
+  orc_enc_dims d;
+  float *c1w, *c1b, *c2w, *c2b; /* conv weights [out][in][3] */
+  float* pos;                   /* [n_audio_ctx][d] */
+  float *lnp_g, *lnp_b;
+  orc_enc_block* blocks;
+};
+
+/* Conv1d.forward: im2col col[(ic * k + kk)][t] = in[ic][t * stride - pad + kk] (0 outside), then the
+ * M>1 tiled matmul weightMatrix [out][in * k] . col (ascending-k sum from 0, main/tensor/Tensor.java:460-489)
+ * and addBias rd[oc][t] += bias[oc] (main/nn/Conv1d.java:38-80). */
+void orc_conv1d(const float* w, const float* bias, int out_ch, int in_ch, int ksize, int stride, int pad,
+                const float* in, int len, float* out) {
+  int out_len = (len + 2 * pad - ksize) / stride + 1;
+  int rows = in_ch * ksize;
+  float* col = (float*)malloc(sizeof(float) * (size_t)rows * out_len);
+  for (int t = 0; t < out_len; t++) {
+    int start = t * stride - pad;
+    for (int ic = 0; ic < in_ch; ic++)
+      for (int kk = 0; kk < ksize; kk++) {
+        int idx = start + kk;
+        col[(size_t)(ic * ksize + kk) * out_len + t] = (idx >= 0 && idx < len) ? in[(size_t)ic * len + idx] : 0.0f;
+      }
+  }
+  for (int oc = 0; oc < out_ch; oc++) {
+    float* o = out + (size_t)oc * out_len;
+    const float* wr = w + (size_t)oc * rows;
+    for (int t = 0; t < out_len; t++) {
+      float sum = 0.0f;
+      for (int j = 0; j < rows; j++) sum += wr[j] * col[(size_t)j * out_len + t];
+      o[t] = sum;
+    }
+    if (bias)
+      for (int t = 0; t < out_len; t++) o[t] += bias[oc];
+  }
+  free(col);
+}
+
+void orc_encoder_destroy(orc_encoder* e) {
+  if (!e) return;
+  free(e->c1w); free(e->c1b); free(e->c2w); free(e->c2b); free(e->pos); free(e->lnp_g); free(e->lnp_b);
+  if (e->blocks) {
+    for (int i = 0; i < e->d.n_audio_layer; i++) {
+      orc_enc_block* b = &e->blocks[i];
+      free_lin(&b->q); free_lin(&b->k); free_lin(&b->v); free_lin(&b->o); free_lin(&b->mlp1); free_lin(&b->mlp2);
+      free(b->attn_ln_g); free(b->attn_ln_b); free(b->mlp_ln_g); free(b->mlp_ln_b);
+    }
+    free(e->blocks);
+  }
+  free(e);
+}
+
+/* WhisperEncoder(WeightStore, ModelDimensions): main/nn/WhisperEncoder.java:27-38, 86-105 */
+orc_encoder* orc_encoder_create(const orc_enc_dims* dims, const orc_tensor* tab, int ntab, char* err, int errlen) {
+  orc_encoder* e = (orc_encoder*)calloc(1, sizeof(orc_encoder));
+  e->d = *dims;
+  int d = dims->n_audio_state, nm = dims->n_mels, T = dims->n_audio_ctx;
+  char nb[256], bb[256];
+#define ELOAD(dst, name, n) do { if (!((dst) = load_f32(tab, ntab, (name), (n), err, errlen))) goto fail; } while (0)
+  ELOAD(e->c1w, "encoder.conv1.weight", (int64_t)d * nm * 3);
+  ELOAD(e->c1b, "encoder.conv1.bias", d);
+  ELOAD(e->c2w, "encoder.conv2.weight", (int64_t)d * d * 3);
+  ELOAD(e->c2b, "encoder.conv2.bias", d);
+  ELOAD(e->pos, "encoder.positional_embedding", (int64_t)T * d);
+  ELOAD(e->lnp_g, "encoder.ln_post.weight", d);
+  ELOAD(e->lnp_b, "encoder.ln_post.bias", d);
+  e->blocks = (orc_enc_block*)calloc((size_t)dims->n_audio_layer, sizeof(orc_enc_block));
+  for (int i = 0; i < dims->n_audio_layer; i++) {
+    orc_enc_block* b = &e->blocks[i];
+    const char* pj[4] = {"query", "key", "value", "out"};
+    orc_lin* lj[4] = {&b->q, &b->k, &b->v, &b->o};
+    for (int j = 0; j < 4; j++) {
+      snprintf(nb, sizeof nb, "encoder.blocks.%d.attn.%s.weight", i, pj[j]);
+      snprintf(bb, sizeof bb, "encoder.blocks.%d.attn.%s.bias", i, pj[j]);
+      if (load_lin(lj[j], tab, ntab, nb, bb, d, d, err, errlen)) goto fail;
+    }
+    snprintf(nb, sizeof nb, "encoder.blocks.%d.mlp.0.weight", i);
+    snprintf(bb, sizeof bb, "encoder.blocks.%d.mlp.0.bias", i);
+    if (load_lin(&b->mlp1, tab, ntab, nb, bb, d, 4 * d, err, errlen)) goto fail;
+    snprintf(nb, sizeof nb, "encoder.blocks.%d.mlp.2.weight", i);
+    snprintf(bb, sizeof bb, "encoder.blocks.%d.mlp.2.bias", i);
+    if (load_lin(&b->mlp2, tab, ntab, nb, bb, 4 * d, d, err, errlen)) goto fail;
+    snprintf(nb, sizeof nb, "encoder.blocks.%d.attn_ln.weight", i);
+    ELOAD(b->attn_ln_g, nb, d);
+    snprintf(nb, sizeof nb, "encoder.blocks.%d.attn_ln.bias", i);
+    ELOAD(b->attn_ln_b, nb, d);
+    snprintf(nb, sizeof nb, "encoder.blocks.%d.mlp_ln.weight", i);
+    ELOAD(b->mlp_ln_g, nb, d);
+    snprintf(nb, sizeof nb, "encoder.blocks.%d.mlp_ln.bias", i);
+    ELOAD(b->mlp_ln_b, nb, d);
+  }
+#undef ELOAD
+  return e;
+fail:
+  orc_encoder_destroy(e);
+  return NULL;
+}
+
+/* WhisperEncoder.forward: conv1 + gelu, conv2 + gelu, transpose, + positional embedding, blocks
+ * (ResidualAttentionBlock.forwardWithAttn with no mask, no cross-attention and no cache:
+ * main/nn/ResidualAttentionBlock.java:42-60; MultiHeadAttention.forward qLen > 1 branch:
+ * main/nn/MultiHeadAttention.java:84-95), ln_post. */
+int orc_encoder_forward(const orc_encoder* e, const float* mel, float* out) {
+  int d = e->d.n_audio_state, nm = e->d.n_mels, T = e->d.n_audio_ctx, H = e->d.n_audio_head, hd = 64;
+  int F = 2 * T;
+  float scale = (float)(1.0 / sqrt((double)hd));
+  float* c1 = (float*)malloc(sizeof(float) * (size_t)d * F);
+  float* c2 = (float*)malloc(sizeof(float) * (size_t)d * T);
+  orc_conv1d(e->c1w, e->c1b, d, nm, 3, 1, 1, mel, F, c1);
+  orc_gelu(c1, d * F);
+  orc_conv1d(e->c2w, e->c2b, d, d, 3, 2, 1, c1, F, c2);
+  orc_gelu(c2, d * T);
+  float* x = (float*)malloc(sizeof(float) * (size_t)T * d);
+  for (int t = 0; t < T; t++)
+    for (int c = 0; c < d; c++) x[(size_t)t * d + c] = c2[(size_t)c * T + t] + e->pos[(size_t)t * d + c];
+  free(c1);
+  free(c2);
+  float* xn = (float*)malloc(sizeof(float) * (size_t)T * d);
+  float* q = (float*)malloc(sizeof(float) * (size_t)T * d);
+  float* k = (float*)malloc(sizeof(float) * (size_t)T * d);
+  float* v = (float*)malloc(sizeof(float) * (size_t)T * d);
+  float* qh = (float*)malloc(sizeof(float) * (size_t)T * hd);
+  float* kh = (float*)malloc(sizeof(float) * (size_t)T * hd);
+  float* vh = (float*)malloc(sizeof(float) * (size_t)T * hd);
+  float* w = (float*)malloc(sizeof(float) * (size_t)T * T);
+  float* merged = (float*)malloc(sizeof(float) * (size_t)T * d);
+  float* o = (float*)malloc(sizeof(float) * (size_t)T * d);
+  float* hbuf = (float*)malloc(sizeof(float) * (size_t)T * 4 * d);
+  for (int l = 0; l < e->d.n_audio_layer; l++) {
+    const orc_enc_block* b = &e->blocks[l];
+    orc_layernorm(x, T, d, b->attn_ln_g, b->attn_ln_b, 1e-5f, xn);
+    orc_linear(xn, T, d, b->q.wt, d, b->q.b, q);
+    orc_linear(xn, T, d, b->k.wt, d, b->k.b, k);
+    orc_linear(xn, T, d, b->v.wt, d, b->v.b, v);
+    for (int h = 0; h < H; h++) {
+      for (int t = 0; t < T; t++)
+        for (int c = 0; c < hd; c++) {
+          qh[(size_t)t * hd + c] = q[(size_t)t * d + h * hd + c];
+          kh[(size_t)t * hd + c] = k[(size_t)t * d + h * hd + c];
+          vh[(size_t)t * hd + c] = v[(size_t)t * d + h * hd + c];
+        }
+      /* qr.matmulTransB(kr, scale): lane dot times scale; softmax rows; attnWeights.matmul(vr) */
+      for (int i = 0; i < T; i++)
+        for (int j = 0; j < T; j++) w[(size_t)i * T + j] = orc_dot(qh + (size_t)i * hd, kh + (size_t)j * hd, hd) * scale;
+      orc_softmax_rows(w, T, T);
+      for (int i = 0; i < T; i++) {
+        float* mo = merged + (size_t)i * d + h * hd;
+        for (int c = 0; c < hd; c++) mo[c] = 0.0f;
+        for (int j = 0; j < T; j++) {
+          float p = w[(size_t)i * T + j];
+          const float* vv = vh + (size_t)j * hd;
+          for (int c = 0; c < hd; c++) mo[c] = mo[c] + p * vv[c];
+        }
+      }
+    }
+    orc_linear(merged, T, d, b->o.wt, d, b->o.b, o);
+    for (size_t i = 0; i < (size_t)T * d; i++) x[i] = o[i] + x[i]; /* attnOut.addInPlace(x) */
+    orc_layernorm(x, T, d, b->mlp_ln_g, b->mlp_ln_b, 1e-5f, xn);
+    orc_linear(xn, T, d, b->mlp1.wt, 4 * d, b->mlp1.b, hbuf);
+    orc_gelu(hbuf, T * 4 * d);
+    orc_linear(hbuf, T, 4 * d, b->mlp2.wt, d, b->mlp2.b, o);
+    for (size_t i = 0; i < (size_t)T * d; i++) x[i] = x[i] + o[i]; /* result.addInPlace(mlpOut) */
+  }
+  orc_layernorm(x, T, d, e->lnp_g, e->lnp_b, 1e-5f, out);
+  free(x); free(xn); free(q); free(k); free(v); free(qh); free(kh); free(vh); free(w); free(merged); free(o); free(hbuf);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------------------------ */
 /* Decode drivers over a logits source.  The model-backed source below runs orc_forward with one
  * KV cache per hypothesis; tests drive the same drivers from hand-built logit tables.           */
 

@@ -88,6 +88,19 @@ int orc_cache_len(const orc_cache* c);
 int orc_forward(const orc_model* m, const int32_t* tokens, int n, const float* xa, orc_cache* cache,
                 float* logits);
 
+/* ---- audio encoder (main/nn/WhisperEncoder.java:27-76) ---- */
+typedef struct {
+  int32_t n_mels, n_audio_ctx, n_audio_state, n_audio_head, n_audio_layer;
+} orc_enc_dims;
+typedef struct orc_encoder orc_encoder;
+orc_encoder* orc_encoder_create(const orc_enc_dims* dims, const orc_tensor* tensors, int n_tensors, char* err, int errlen);
+void orc_encoder_destroy(orc_encoder* e);
+/* forward(mel): mel [n_mels][2 * n_audio_ctx] -> out [n_audio_ctx][n_audio_state] */
+int orc_encoder_forward(const orc_encoder* e, const float* mel, float* out);
+/* Conv1d.forward (main/nn/Conv1d.java:38-80): w [out][in][k], in [in][len] -> out [out][out_len] */
+void orc_conv1d(const float* w, const float* bias, int out_ch, int in_ch, int ksize, int stride, int pad,
+                const float* in, int len, float* out);
+
 /* Fixed logit bias [V] added to every logits row after the tied projection (NULL: none).  Not a
  * reference feature: the seeded bias of the beam-search workload. */
 void orc_model_set_logit_bias(orc_model* m, const float* bias);

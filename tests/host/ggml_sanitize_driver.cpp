@@ -1,7 +1,8 @@
 // Drives the GGML file parser (whisper4j_amd/csrc/w4h_ggml.cpp) over the files named on the command
 // line, for a build with AddressSanitizer and UndefinedBehaviorSanitizer: every file is inspected and
 // each of its tensors read back, and every outcome must be a return code (never a memory error or
-// undefined behaviour).  Model creation, the only device step the parser reaches, is stubbed out.
+// undefined behaviour).  Model and encoder creation, the only device steps the parser reaches, are
+// stubbed out.
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -22,6 +23,9 @@ int fail(int code, const char* fmt, ...) {
 }  // namespace w4h
 
 extern "C" int w4h_model_create(const w4h_dims*, const w4h_tensor*, int32_t, int32_t, w4h_model**) {
+  return W4H_ERR_DEVICE;
+}
+extern "C" int w4h_encoder_create(const w4h_encoder_dims*, const w4h_tensor*, int32_t, int32_t, w4h_encoder**) {
   return W4H_ERR_DEVICE;
 }
 

@@ -8,6 +8,7 @@ generator used by the tests and the benchmark.
 from ._lib import EXPORTS, W4HError, device_count, lib  # noqa: F401
 from .decoder import (  # noqa: F401
     DecodeResult,
+    Encoder,
     Model,
     Session,
     StepResult,

@@ -30,7 +30,8 @@ TYPE_F32, TYPE_F16, TYPE_Q8_0 = 0, 1, 8
 # Every symbol include/w4h.h declares.
 EXPORTS = (
     "w4h_last_error", "w4h_device_count", "w4h_model_create", "w4h_model_load_ggml", "w4h_model_dims",
-    "w4h_model_destroy", "w4h_ggml_inspect", "w4h_ggml_read_tensor", "w4h_session_create", "w4h_session_destroy",
+    "w4h_model_destroy", "w4h_encoder_create", "w4h_encoder_load_ggml", "w4h_encoder_get_dims",
+    "w4h_encoder_forward", "w4h_encoder_forward_device", "w4h_encoder_destroy", "w4h_ggml_inspect", "w4h_ggml_read_tensor", "w4h_session_create", "w4h_session_destroy",
     "w4h_session_set_encoder", "w4h_session_set_encoder_device", "w4h_session_reset", "w4h_session_kv_len", "w4h_session_set_suppress",
     "w4h_session_set_probe", "w4h_session_set_logit_bias", "w4h_session_step", "w4h_session_run", "w4h_session_reorder", "w4h_session_time_run",
     "w4h_session_trace_run",
@@ -54,6 +55,11 @@ class Tensor(ctypes.Structure):
 class Dims(ctypes.Structure):
     _fields_ = [("n_vocab", ctypes.c_int32), ("n_text_ctx", ctypes.c_int32), ("n_text_state", ctypes.c_int32),
                 ("n_text_head", ctypes.c_int32), ("n_text_layer", ctypes.c_int32), ("n_audio_ctx", ctypes.c_int32)]
+
+
+class EncoderDims(ctypes.Structure):
+    _fields_ = [("n_mels", ctypes.c_int32), ("n_audio_ctx", ctypes.c_int32), ("n_audio_state", ctypes.c_int32),
+                ("n_audio_head", ctypes.c_int32), ("n_audio_layer", ctypes.c_int32)]
 
 
 class SessionDesc(ctypes.Structure):
@@ -99,6 +105,12 @@ def lib():
         "w4h_model_load_ggml": (i32, [ctypes.c_char_p, i32, ctypes.POINTER(vp)]),
         "w4h_model_dims": (i32, [vp, ctypes.POINTER(Dims)]),
         "w4h_model_destroy": (i32, [vp]),
+        "w4h_encoder_create": (i32, [ctypes.POINTER(EncoderDims), ctypes.POINTER(Tensor), i32, i32, ctypes.POINTER(vp)]),
+        "w4h_encoder_load_ggml": (i32, [ctypes.c_char_p, i32, ctypes.POINTER(vp)]),
+        "w4h_encoder_get_dims": (i32, [vp, ctypes.POINTER(EncoderDims)]),
+        "w4h_encoder_forward": (i32, [vp, f32p, f32p]),
+        "w4h_encoder_forward_device": (i32, [vp, vp, vp, vp]),
+        "w4h_encoder_destroy": (i32, [vp]),
         "w4h_ggml_inspect": (i32, [ctypes.c_char_p, ctypes.POINTER(Dims), i32p, ctypes.POINTER(ctypes.c_int64)]),
         "w4h_ggml_read_tensor": (i32, [ctypes.c_char_p, ctypes.c_char_p, i32p, i32p, ctypes.c_int64 * 4, vp,
                                        ctypes.c_int64]),

@@ -26,8 +26,8 @@ HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__", "
 # compile in parallel; the shared device code is w4h_kernels.h.
 STEP_VARIANTS = ["1_f16_r2", "1_f16_r3", "1_q8_r2", "8_f16_r2", "8_f16_r3", "8_q8_r2"]
 SOURCES = ([("w4h_device.hip", HIPCC, DEVICE_FLAGS), ("w4h_wide.hip", HIPCC, DEVICE_FLAGS),
-            ("w4h_xkv.hip", HIPCC, DEVICE_FLAGS), ("w4h_sample.hip", HIPCC, DEVICE_FLAGS)] + [(f"w4h_step_{v}.hip", HIPCC, DEVICE_FLAGS) for v in STEP_VARIANTS] +
-           [("w4h_api.cpp", CLANG, HOST_FLAGS), ("w4h_ggml.cpp", CLANG, HOST_FLAGS), ("w4h_decode.cpp", CLANG, HOST_FLAGS)])
+            ("w4h_xkv.hip", HIPCC, DEVICE_FLAGS), ("w4h_sample.hip", HIPCC, DEVICE_FLAGS), ("w4h_encoder.hip", HIPCC, DEVICE_FLAGS)] + [(f"w4h_step_{v}.hip", HIPCC, DEVICE_FLAGS) for v in STEP_VARIANTS] +
+           [("w4h_api.cpp", CLANG, HOST_FLAGS), ("w4h_ggml.cpp", CLANG, HOST_FLAGS), ("w4h_decode.cpp", CLANG, HOST_FLAGS), ("w4h_encoder_api.cpp", CLANG, HOST_FLAGS)])
 
 
 def _compile(src, cxx, flags):

@@ -1,0 +1,422 @@
+// Audio encoder for gfx950 (WhisperEncoder.forward, main/nn/WhisperEncoder.java:42-76): conv1 (k 3,
+// pad 1) + GELU, conv2 (k 3, stride 2, pad 1) + GELU, + positional embedding, N pre-LN blocks of
+// unmasked self-attention over the frames and a GELU MLP (main/nn/ResidualAttentionBlock.java:42-60),
+// then ln_post.  Activations live in HBM as [frames][channels] fp32 rows.
+//
+// Every product runs on the matrix cores (v_mfma_f32_16x16x32_f16, fp32 accumulation) with fp32
+// operands entering as f16 hi/lo pairs, hi = f16(x), lo = f16(x - hi):
+//   - projections and convolutions: weight (f16, or q8_0 as exact int8 with the block scale applied
+//     per 32-k step) x activation (hi, lo): two products per pair, ~22 bits of the activation;
+//   - attention: both operands are activations, so q.k and p.v take three products each
+//     (hi.hi + hi.lo + lo.hi), ~22 bits of each operand.
+// The convolutions are implicit GEMMs: the input is kept time-major with one zero row of padding
+// at each end, so output frame t reads the 3 input frames it covers as ONE contiguous row of
+// 3 x channels values (stride 1: row t of the padded input; stride 2: row 2t), and the GEMM takes
+// rows at a stride smaller than their length.  The weights are repacked at load from [out][in][k]
+// to [out][k][in] to match.
+
+#include "w4h_mfma.h"
+#include "w4h_encoder.h"
+
+namespace w4h {
+
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+
+constexpr int kEncBM = 128;           // GEMM rows (frames) per workgroup: 32 per wave
+constexpr int kEncBN = 64;            // GEMM columns per workgroup: 4 MFMA column tiles per wave
+constexpr int kEncBK = 64;            // k per stage: two MFMA k steps
+constexpr int kEncLd = kEncBK + kPadH;  // LDS pitch in halves (144 bytes)
+
+// C = A . W^T + bias over [M][N], with the epilogue EPI:
+//   kEpiStore: out = C;  kEpiGelu: out = gelu(C);  kEpiResid: out = add + C (add may alias out);
+//   kEpiGeluPos: out = gelu(C) + add (the positional embedding, [M][N]);
+//   kEpiQkv: C's columns are q | k | v of H heads; each goes out as f16 hi/lo planes
+//   (q pre-multiplied by 0.125, the exact 1/sqrt(64) of the scores): q, k as [H][M][64],
+//   v transposed as [H][64][M] (the attention kernel's operand layouts).
+template <int EPI, int WQ8>
+__global__ __launch_bounds__(256) void k_enc_gemm(EncGemm g) {
+  __shared__ __attribute__((aligned(16))) _Float16 s_ah[kEncBM * kEncLd];
+  __shared__ __attribute__((aligned(16))) _Float16 s_al[kEncBM * kEncLd];
+  __shared__ __attribute__((aligned(16))) _Float16 s_b[kEncBN * kEncLd];
+  __shared__ float s_sc[kEncBN][2];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int m0 = blockIdx.x * kEncBM, n0 = blockIdx.y * kEncBN;
+  const int M = g.M, N = g.N, K = g.K;
+  // Stage registers.  A: 128 x 64 fp32 = 2048 float4, 8 per thread (c = j * 256 + tid: row c >> 4,
+  // k 4 * (c & 15)); rows past M read row M - 1 (results dropped), k past K reads zeros.  f16 W:
+  // 64 x 64 halves, 2 x 16 bytes per thread (row c >> 3, k 8 * (c & 7)); q8_0 W: 64 x 64 int8, 16
+  // bytes per thread (row tid >> 2, k 16 * (tid & 3)) and the scales (row tid >> 1, block tid & 1).
+  float4 ra[8];
+  uint4 rb[2];
+  uint4 rq;
+  uint16_t rs = 0;
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = j * 256 + tid;
+      const int r = min(m0 + (c >> 4), M - 1), k = k0 + 4 * (c & 15);
+      ra[j] = k < K ? *reinterpret_cast<const float4*>(g.a + (size_t)r * g.lda + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (!WQ8) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int c = j * 256 + tid;
+        const int r = min(n0 + (c >> 3), N - 1), k = k0 + 8 * (c & 7);
+        rb[j] = k < K ? *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(g.w) + (size_t)r * K + k)
+                      : make_uint4(0u, 0u, 0u, 0u);
+      }
+    } else {
+      const int r = min(n0 + (tid >> 2), N - 1);
+      rq = *reinterpret_cast<const uint4*>(static_cast<const int8_t*>(g.w) + (size_t)r * K + k0 + 16 * (tid & 3));
+      if (tid < 128) rs = g.ws[(size_t)min(n0 + (tid >> 1), N - 1) * (K >> 5) + (k0 >> 5) + (tid & 1)];
+    }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = j * 256 + tid;
+      const int o = (c >> 4) * kEncLd + 4 * (c & 15);
+      const float v[4] = {ra[j].x, ra[j].y, ra[j].z, ra[j].w};
+      half4 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        hi[e] = (_Float16)v[e];
+        lo[e] = (_Float16)(v[e] - (float)hi[e]);
+      }
+      *reinterpret_cast<half4*>(&s_ah[o]) = hi;
+      *reinterpret_cast<half4*>(&s_al[o]) = lo;
+    }
+    if (!WQ8) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int c = j * 256 + tid;
+        *reinterpret_cast<uint4*>(&s_b[(c >> 3) * kEncLd + 8 * (c & 7)]) = rb[j];
+      }
+    } else {
+      const int o = (tid >> 2) * kEncLd + 16 * (tid & 3);
+      *reinterpret_cast<half8*>(&s_b[o]) = i8x8_to_h8(make_uint2(rq.x, rq.y));
+      *reinterpret_cast<half8*>(&s_b[o + 8]) = i8x8_to_h8(make_uint2(rq.z, rq.w));
+      if (tid < 128) s_sc[tid >> 1][tid & 1] = h2f(rs);
+    }
+  };
+
+  floatx4 acc[2][4];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  load(0);
+  for (int k0 = 0; k0 < K; k0 += kEncBK) {
+    lds_barrier();  // every wave has read the previous stage
+    stash();
+    lds_barrier();
+    if (k0 + kEncBK < K) load(k0 + kEncBK);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int kk = ks * 32 + 8 * (lane >> 4);
+      half8 bfr[4];
+      float sc[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        bfr[nt] = *reinterpret_cast<const half8*>(&s_b[(nt * 16 + (lane & 15)) * kEncLd + kk]);
+        sc[nt] = WQ8 ? s_sc[nt * 16 + (lane & 15)][ks] : 1.f;
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int r = wv * 32 + mt * 16 + (lane & 15);
+        const half8 ah = *reinterpret_cast<const half8*>(&s_ah[r * kEncLd + kk]);
+        const half8 al = *reinterpret_cast<const half8*>(&s_al[r * kEncLd + kk]);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          if (!WQ8) {
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bfr[nt], acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bfr[nt], acc[mt][nt], 0, 0, 0);
+          } else {
+            floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bfr[nt], floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bfr[nt], t, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[mt][nt][e] = fmaf(sc[nt], t[e], acc[mt][nt][e]);
+          }
+        }
+      }
+    }
+  }
+
+  // Epilogue: lane holds rows wv * 32 + mt * 16 + 4 * (lane >> 4) + e of column nt * 16 + (lane & 15).
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int n = n0 + nt * 16 + (lane & 15);
+    if (n >= N) continue;
+    const float b = g.bias ? g.bias[n] : 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + wv * 32 + mt * 16 + 4 * (lane >> 4) + e;
+        if (m >= M) continue;
+        const float c = acc[mt][nt][e] + b;
+        if constexpr (EPI == kEpiStore) {
+          g.out[(size_t)m * g.ldo + n] = c;
+        } else if constexpr (EPI == kEpiGelu) {
+          g.out[(size_t)m * g.ldo + n] = gelu_f16(c);
+        } else if constexpr (EPI == kEpiResid) {
+          g.out[(size_t)m * g.ldo + n] = g.add[(size_t)m * g.ldo + n] + c;
+        } else if constexpr (EPI == kEpiGeluPos) {
+          g.out[(size_t)m * g.ldo + n] = gelu_f16(c) + g.add[(size_t)m * N + n];
+        } else {  // kEpiQkv
+          const int d = N / 3, part = n / d, h = (n - part * d) >> 6, ei = n & 63;
+          const float v = part == 0 ? c * 0.125f : c;
+          const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
+          const size_t plane = (size_t)(d >> 6) * g.Tp * kHeadDim;  // halves per (part, hi|lo) plane
+          const size_t idx = part == 2 ? ((size_t)h * kHeadDim + ei) * g.Tp + m : ((size_t)h * g.Tp + m) * kHeadDim + ei;
+          _Float16* q16 = reinterpret_cast<_Float16*>(g.qkv);
+          q16[(size_t)(part * 2) * plane + idx] = hi;
+          q16[(size_t)(part * 2 + 1) * plane + idx] = lo;
+        }
+      }
+  }
+}
+
+// Attention of every frame over every frame for one head (no mask), flash style: a workgroup owns
+// 64 query rows (16 per wave) and walks the keys in blocks of 64 (K and V staged in LDS, double
+// buffered), with an online softmax in fp32.  Products are taken transposed, S^T = K . Q^T and
+// O^T = V^T . P^T, so that the softmax weights come out of the first product (lane: query lane & 15,
+// keys 16 nt + 4 (lane >> 4) + [0, 4)) already where the second needs its B operand: the 32 keys of
+// one k step are taken in the order {4g + [0,4), 16 + 4g + [0,4)} for lane group g (any order of k
+// gives the same sum, V^T is read in the same order).  q.k and p.v each take three f16 products
+// (hi.hi + hi.lo + lo.hi).  The operand planes hold Tp frames (a multiple of 64, the frames past T
+// zero), so every block load is in range and aligned; keys past T are masked to -inf.
+// out[t][h * 64 + e].
+constexpr int kAttBQ = 64, kAttBK = 64, kAttLd = 64 + kPadH;
+
+__global__ __launch_bounds__(256) void k_enc_attn(const _Float16* __restrict__ qkv, int T, int Tp, int H, float* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) _Float16 s_k[2][2][kAttBK * kAttLd];    // [buffer][hi|lo][key][dim]
+  __shared__ __attribute__((aligned(16))) _Float16 s_v[2][2][kHeadDim * kAttLd];  // [buffer][hi|lo][dim][key]
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g4 = 4 * (lane >> 4), c16 = lane & 15;
+  const int q0 = blockIdx.x * kAttBQ, h = blockIdx.y;
+  const size_t plane = (size_t)H * Tp * kHeadDim;
+  const _Float16* Qh = qkv + (size_t)h * Tp * kHeadDim;
+  const _Float16* Ql = Qh + plane;
+  const _Float16* Kh = qkv + 2 * plane + (size_t)h * Tp * kHeadDim;
+  const _Float16* Kl = Kh + plane;
+  const _Float16* Vh = qkv + 4 * plane + (size_t)h * kHeadDim * Tp;
+  const _Float16* Vl = Vh + plane;
+  // this lane's query operand (B of S^T: column = query lane & 15, dims 8 * (lane >> 4) + 32 ks)
+  const int qr = q0 + wv * 16 + c16;
+  half8 qh[2], ql[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    qh[ks] = *reinterpret_cast<const half8*>(Qh + (size_t)qr * kHeadDim + 32 * ks + 8 * (lane >> 4));
+    ql[ks] = *reinterpret_cast<const half8*>(Ql + (size_t)qr * kHeadDim + 32 * ks + 8 * (lane >> 4));
+  }
+  // key / value block loads: 64 x 64 halves per plane = 512 x 16 bytes, 2 per thread per plane
+  // (key or dim tid >> 3 and 32 + that, 8 halves at 8 * (tid & 7)), held in named registers
+  const int lr = tid >> 3, lc = 8 * (tid & 7);
+  uint4 k0h, k0l, k1h, k1l, v0h, v0l, v1h, v1l;
+  auto load = [&](int k0) {
+    const size_t ka = (size_t)(k0 + lr) * kHeadDim + lc, kb = ka + (size_t)32 * kHeadDim;
+    k0h = *reinterpret_cast<const uint4*>(Kh + ka);
+    k0l = *reinterpret_cast<const uint4*>(Kl + ka);
+    k1h = *reinterpret_cast<const uint4*>(Kh + kb);
+    k1l = *reinterpret_cast<const uint4*>(Kl + kb);
+    const size_t va = (size_t)lr * Tp + k0 + lc, vb = va + (size_t)32 * Tp;
+    v0h = *reinterpret_cast<const uint4*>(Vh + va);
+    v0l = *reinterpret_cast<const uint4*>(Vl + va);
+    v1h = *reinterpret_cast<const uint4*>(Vh + vb);
+    v1l = *reinterpret_cast<const uint4*>(Vl + vb);
+  };
+  auto stash = [&](int buf) {
+    const int o0 = lr * kAttLd + lc, o1 = o0 + 32 * kAttLd;
+    *reinterpret_cast<uint4*>(&s_k[buf][0][o0]) = k0h;
+    *reinterpret_cast<uint4*>(&s_k[buf][1][o0]) = k0l;
+    *reinterpret_cast<uint4*>(&s_k[buf][0][o1]) = k1h;
+    *reinterpret_cast<uint4*>(&s_k[buf][1][o1]) = k1l;
+    *reinterpret_cast<uint4*>(&s_v[buf][0][o0]) = v0h;
+    *reinterpret_cast<uint4*>(&s_v[buf][1][o0]) = v0l;
+    *reinterpret_cast<uint4*>(&s_v[buf][0][o1]) = v1h;
+    *reinterpret_cast<uint4*>(&s_v[buf][1][o1]) = v1l;
+  };
+  floatx4 o[4];  // O^T: dims 16 nd + g4 + e of query c16
+#pragma unroll
+  for (int nd = 0; nd < 4; ++nd) o[nd] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float mrow = -INFINITY, lrow = 0.f;  // of this lane's query
+  load(0);
+  stash(0);
+  load(min(kAttBK, Tp - kAttBK));
+  lds_barrier();
+  int buf = 0;
+  for (int k0 = 0; k0 < T; k0 += kAttBK, buf ^= 1) {  // k0 + 64 <= Tp
+    // the next block goes to the other buffer, which every wave finished reading before the last
+    // barrier; then the loads of the block after it (the last one again at the end: every load is
+    // in range and unconditional)
+    stash(buf ^ 1);
+    load(min(k0 + 2 * kAttBK, Tp - kAttBK));
+    const _Float16* sk0 = s_k[buf][0];
+    const _Float16* sk1 = s_k[buf][1];
+    const _Float16* sv0 = s_v[buf][0];
+    const _Float16* sv1 = s_v[buf][1];
+    floatx4 s[4];  // S^T: keys 16 nt + g4 + e of query c16
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      s[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int off = (nt * 16 + c16) * kAttLd + 32 * ks + 8 * (lane >> 4);
+        const half8 kh = *reinterpret_cast<const half8*>(sk0 + off);
+        const half8 kl = *reinterpret_cast<const half8*>(sk1 + off);
+        s[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[ks], s[nt], 0, 0, 0);
+        s[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[ks], s[nt], 0, 0, 0);
+        s[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[ks], s[nt], 0, 0, 0);
+      }
+    }
+    // online softmax for this lane's query: its 16 keys here, the other 48 in lanes ^16, ^32, ^48
+    float mb = -INFINITY;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (k0 + nt * 16 + g4 + e >= T) s[nt][e] = -INFINITY;
+        mb = fmaxf(mb, s[nt][e]);
+      }
+    mb = fmaxf(mb, __shfl_xor(mb, 16));
+    mb = fmaxf(mb, __shfl_xor(mb, 32));
+    const float mn = fmaxf(mrow, mb);
+    const float alpha = __expf(mrow - mn);
+    mrow = mn;
+    float ls = 0.f;
+    half8 ph[2], pl[2];  // B of O^T for k step ks: keys {32 ks + g4 + [0,4), 32 ks + 16 + g4 + [0,4)}
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float pv = __expf(s[nt][e] - mn);
+        ls += pv;
+        const _Float16 hi = (_Float16)pv;
+        ph[nt >> 1][4 * (nt & 1) + e] = hi;
+        pl[nt >> 1][4 * (nt & 1) + e] = (_Float16)(pv - (float)hi);
+      }
+    ls += __shfl_xor(ls, 16);
+    ls += __shfl_xor(ls, 32);
+    lrow = lrow * alpha + ls;
+#pragma unroll
+    for (int nd = 0; nd < 4; ++nd)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[nd][e] *= alpha;
+    // O^T += V^T . P^T: A = V^T rows (dims 16 nd + c16) over the same key order
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int nd = 0; nd < 4; ++nd) {
+        const int off = (nd * 16 + c16) * kAttLd + 32 * ks + g4;
+        half8 vh, vl;
+        const half4 a0 = *reinterpret_cast<const half4*>(sv0 + off), a1 = *reinterpret_cast<const half4*>(sv0 + off + 16);
+        const half4 b0 = *reinterpret_cast<const half4*>(sv1 + off), b1 = *reinterpret_cast<const half4*>(sv1 + off + 16);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          vh[e] = a0[e];
+          vh[4 + e] = a1[e];
+          vl[e] = b0[e];
+          vl[4 + e] = b1[e];
+        }
+        o[nd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph[ks], o[nd], 0, 0, 0);
+        o[nd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph[ks], o[nd], 0, 0, 0);
+        o[nd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl[ks], o[nd], 0, 0, 0);
+      }
+    }
+    lds_barrier();  // this buffer is read; the other one is written
+  }
+  const int t = q0 + wv * 16 + c16;
+  if (t < T) {
+    const float inv = 1.f / lrow;
+    float* dst = out + (size_t)t * H * kHeadDim + h * kHeadDim;
+#pragma unroll
+    for (int nd = 0; nd < 4; ++nd)
+      *reinterpret_cast<float4*>(dst + nd * 16 + g4) =
+          make_float4(o[nd][0] * inv, o[nd][1] * inv, o[nd][2] * inv, o[nd][3] * inv);
+  }
+}
+
+// LayerNorm of rows of n (eps 1e-5), one wave per row, two passes in fp32 (main/tensor/Tensor.java:592-619).
+__global__ __launch_bounds__(256) void k_enc_ln(const float* __restrict__ x, int rows, int n, const float* __restrict__ gam,
+                                                const float* __restrict__ bet, float* __restrict__ y) {
+  const int lane = threadIdx.x & 63, r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* xr = x + (size_t)r * n;
+  float v[kEncLnPer];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kEncLnPer; ++i) {
+    const int j = lane + 64 * i;
+    v[i] = j < n ? xr[j] : 0.f;
+    s += v[i];
+  }
+  s = wave_sum(s);
+  const float mean = s / (float)n;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < kEncLnPer; ++i) {
+    const int j = lane + 64 * i;
+    const float dd = j < n ? v[i] - mean : 0.f;
+    q += dd * dd;
+  }
+  q = wave_sum(q);
+  const float inv = 1.f / sqrtf(q / (float)n + 1e-5f);
+#pragma unroll
+  for (int i = 0; i < kEncLnPer; ++i) {
+    const int j = lane + 64 * i;
+    if (j < n) y[(size_t)r * n + j] = (v[i] - mean) * inv * gam[j] + bet[j];
+  }
+}
+
+// Time-major copy of the mel input with a zero frame at each end: dst[r][c] = mel[c][r - 1] for
+// 1 <= r <= frames, 0 for r = 0 and r = frames + 1.
+__global__ void k_enc_mel_t(const float* __restrict__ mel, int n_mels, int frames, float* __restrict__ dst) {
+  const int r = blockIdx.x, c = threadIdx.x;
+  if (c >= n_mels) return;
+  dst[(size_t)r * n_mels + c] = (r >= 1 && r <= frames) ? mel[(size_t)c * frames + r - 1] : 0.f;
+}
+
+template <int EPI>
+static hipError_t gemm_t(const EncGemm& g, hipStream_t st) {
+  const dim3 grid((g.M + kEncBM - 1) / kEncBM, (g.N + kEncBN - 1) / kEncBN);
+  if (g.ws)
+    hipLaunchKernelGGL((k_enc_gemm<EPI, 1>), grid, dim3(256), 0, st, g);
+  else
+    hipLaunchKernelGGL((k_enc_gemm<EPI, 0>), grid, dim3(256), 0, st, g);
+  return hipGetLastError();
+}
+
+hipError_t launch_enc_gemm(int epi, const EncGemm& g, hipStream_t st) {
+  if (g.M < 1 || g.N < 1 || g.K < 1 || g.K % 8 || g.lda % 4 || (g.ws && g.K % 64)) return hipErrorInvalidValue;
+  if (epi == kEpiQkv && (g.N % 192 || g.Tp < g.M || g.Tp % kEncPad)) return hipErrorInvalidValue;
+  switch (epi) {
+    case kEpiStore: return gemm_t<kEpiStore>(g, st);
+    case kEpiGelu: return gemm_t<kEpiGelu>(g, st);
+    case kEpiResid: return gemm_t<kEpiResid>(g, st);
+    case kEpiGeluPos: return gemm_t<kEpiGeluPos>(g, st);
+    case kEpiQkv: return gemm_t<kEpiQkv>(g, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_enc_attn(const uint16_t* qkv, int T, int Tp, int H, float* out, hipStream_t st) {
+  if (T < 1 || Tp < T || Tp % kEncPad) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_enc_attn, dim3((T + kAttBQ - 1) / kAttBQ, H), dim3(256), 0, st,
+                     reinterpret_cast<const _Float16*>(qkv), T, Tp, H, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_enc_ln(const float* x, int rows, int n, const float* g, const float* b, float* y, hipStream_t st) {
+  if (n > 64 * kEncLnPer) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_enc_ln, dim3((rows + 3) / 4), dim3(256), 0, st, x, rows, n, g, b, y);
+  return hipGetLastError();
+}
+
+hipError_t launch_enc_mel_t(const float* mel, int n_mels, int frames, float* dst, hipStream_t st) {
+  if (n_mels > 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_enc_mel_t, dim3(frames + 2), dim3((n_mels + 63) & ~63), 0, st, mel, n_mels, frames, dst);
+  return hipGetLastError();
+}
+
+}  // namespace w4h

@@ -31,6 +31,7 @@ struct Mapped {
 
 struct Parsed {
   w4h_dims dims{};
+  w4h_encoder_dims edims{};
   std::vector<w4h_tensor> tensors;
   std::vector<std::string> names;
   int64_t data_bytes = 0;
@@ -90,6 +91,11 @@ int parse(const Mapped& mf, Parsed& out) {
   out.dims.n_text_state = hp[6];
   out.dims.n_text_head = hp[7];
   out.dims.n_text_layer = hp[8];
+  out.edims.n_mels = hp[9];
+  out.edims.n_audio_ctx = hp[1];
+  out.edims.n_audio_state = hp[2];
+  out.edims.n_audio_head = hp[3];
+  out.edims.n_audio_layer = hp[4];
   int32_t n_mel, n_fft;
   if (!rd32(&n_mel) || !rd32(&n_fft) || n_mel < 0 || n_fft < 0) return w4h::fail(W4H_ERR_FORMAT, "bad mel filter header");
   const size_t mel_bytes = (size_t)n_mel * (size_t)n_fft * 4;
@@ -193,6 +199,17 @@ int w4h_model_load_ggml(const char* path, int32_t device, w4h_model** out) {
   if ((rc = parse(mf, ps))) return rc;
   if (ps.tensors.empty()) return w4h::fail(W4H_ERR_FORMAT, "GGML file has no tensors: %s", path);
   return w4h_model_create(&ps.dims, ps.tensors.data(), (int32_t)ps.tensors.size(), device, out);
+}
+
+int w4h_encoder_load_ggml(const char* path, int32_t device, w4h_encoder** out) {
+  if (!path || !out) return w4h::fail(W4H_ERR_INVALID, "null argument");
+  Mapped mf;
+  int rc = map_file(path, mf);
+  if (rc) return rc;
+  Parsed ps;
+  if ((rc = parse(mf, ps))) return rc;
+  if (ps.tensors.empty()) return w4h::fail(W4H_ERR_FORMAT, "GGML file has no tensors: %s", path);
+  return w4h_encoder_create(&ps.edims, ps.tensors.data(), (int32_t)ps.tensors.size(), device, out);
 }
 
 }  // extern "C"

@@ -108,6 +108,74 @@ class Model:
         return Session(self, n_rows, n_encoders, max_ctx or self.dims.n_text_ctx)
 
 
+def _tensor_array(tensors):
+    arr = (_lib.Tensor * len(tensors))()
+    keep = []
+    for i, t in enumerate(tensors):
+        raw = np.ascontiguousarray(t.raw())
+        nm = t.name.encode()
+        keep += [raw, nm]
+        arr[i].name = nm
+        arr[i].type = t.ggml_type
+        arr[i].n_dims = len(t.ne)
+        for j, v in enumerate(t.ne):
+            arr[i].ne[j] = int(v)
+        arr[i].data = raw.ctypes.data
+    return arr, keep
+
+
+class Encoder:
+    """Device-resident audio encoder (WhisperEncoder(WeightStore, ModelDimensions) and forward(mel),
+    main/nn/WhisperEncoder.java:27-76)."""
+
+    def __init__(self, handle, dims: _lib.EncoderDims):
+        self._h = handle
+        self.dims = dims
+
+    @classmethod
+    def from_tensors(cls, edims, tensors, device: int = 0) -> "Encoder":
+        """edims: object with n_mels, n_audio_ctx, n_audio_state, n_audio_head, n_audio_layer."""
+        d = _lib.EncoderDims(edims.n_mels, edims.n_audio_ctx, edims.n_audio_state, edims.n_audio_head,
+                             edims.n_audio_layer)
+        arr, keep = _tensor_array(tensors)
+        h = ctypes.c_void_p()
+        check(lib().w4h_encoder_create(ctypes.byref(d), arr, len(tensors), device, ctypes.byref(h)))
+        del keep
+        return cls(h, d)
+
+    @classmethod
+    def load_ggml(cls, path: str, device: int = 0) -> "Encoder":
+        h = ctypes.c_void_p()
+        check(lib().w4h_encoder_load_ggml(path.encode(), device, ctypes.byref(h)))
+        d = _lib.EncoderDims()
+        check(lib().w4h_encoder_get_dims(h, ctypes.byref(d)))
+        return cls(h, d)
+
+    def forward(self, mel) -> np.ndarray:
+        """mel [n_mels][2 * n_audio_ctx] -> encoder output [n_audio_ctx][n_audio_state] (fp32)."""
+        m = np.ascontiguousarray(mel, dtype=np.float32)
+        if m.shape != (self.dims.n_mels, 2 * self.dims.n_audio_ctx):
+            raise ValueError(f"mel shape {m.shape}, expected ({self.dims.n_mels}, {2 * self.dims.n_audio_ctx})")
+        out = np.empty((self.dims.n_audio_ctx, self.dims.n_audio_state), np.float32)
+        check(lib().w4h_encoder_forward(self._h, _ptr(m, _f32p), _ptr(out, _f32p)))
+        return out
+
+    def forward_device(self, mel_dev: int, out_dev: int, stream: int = 0) -> None:
+        check(lib().w4h_encoder_forward_device(self._h, ctypes.c_void_p(mel_dev), ctypes.c_void_p(out_dev),
+                                               ctypes.c_void_p(stream or None)))
+
+    def close(self) -> None:
+        if self._h is not None:
+            check(lib().w4h_encoder_destroy(self._h))
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+
 class Session:
     """Per-decode-call state: self-KV cache, cross K/V, stream (the reference's kvCache map)."""
 

@@ -56,6 +56,25 @@ SHAPES = {
 }
 
 
+@dataclasses.dataclass(frozen=True)
+class EncDims:
+    """Audio encoder hyperparameters (WhisperEncoder, main/nn/WhisperEncoder.java:27-38)."""
+    n_mels: int
+    n_audio_ctx: int
+    n_audio_state: int
+    n_audio_head: int
+    n_audio_layer: int
+
+
+ENC_SHAPES = {
+    "tiny.en": EncDims(80, 1500, 384, 6, 4),
+    "base.en": EncDims(80, 1500, 512, 8, 6),
+    "small": EncDims(80, 1500, 768, 12, 12),
+    "large-v3-turbo": EncDims(128, 1500, 1280, 20, 32),
+    "medium": EncDims(80, 1500, 1024, 16, 24),
+}
+
+
 @dataclasses.dataclass
 class GgmlTensor:
     name: str
@@ -177,6 +196,55 @@ def make_decoder(dims: Dims, seed: int = 0, wtype: str = "f16", ln_random: bool 
     return out
 
 
+def make_encoder(edims: EncDims, seed: int = 0, wtype: str = "f16", ln_random: bool = False,
+                 qk_std: float = 0.02) -> list:
+    """Tensor table of a random-init Whisper audio encoder (names and GGML shapes as whisper.cpp):
+    conv weights f16 [out][in][3] (ne = [3, in, out]), conv biases f32 ne = [1, out], the positional
+    embedding f32 [n_audio_ctx][d], blocks as the decoder's without cross-attention, ln_post.  The
+    query and key matrices draw N(0, qk_std) (a larger value gives peaked attention)."""
+    d, T, nm, L = edims.n_audio_state, edims.n_audio_ctx, edims.n_mels, edims.n_audio_layer
+
+    def conv(name, n_out, n_in):
+        w = _rng(seed, name).standard_normal((n_out, n_in, 3), dtype=np.float32) * np.float32(0.02)
+        return GgmlTensor(name, GGML_F16, (3, n_in, n_out), w.astype(np.float16))
+
+    def bias2(name, n):
+        v = _rng(seed, name).standard_normal(n, dtype=np.float32) * np.float32(0.02)
+        return GgmlTensor(name, GGML_F32, (1, n), v)
+
+    def ln(name):
+        if ln_random:
+            g = 1.0 + 0.1 * _rng(seed, name + ".weight").standard_normal(d, dtype=np.float32)
+            b = 0.1 * _rng(seed, name + ".bias").standard_normal(d, dtype=np.float32)
+            return [GgmlTensor(name + ".weight", GGML_F32, (d,), g.astype(np.float32)),
+                    GgmlTensor(name + ".bias", GGML_F32, (d,), b.astype(np.float32))]
+        return [_vector(seed, name + ".weight", d, "ones"), _vector(seed, name + ".bias", d, "zeros")]
+
+    out = [conv("encoder.conv1.weight", d, nm), bias2("encoder.conv1.bias", d),
+           conv("encoder.conv2.weight", d, d), bias2("encoder.conv2.bias", d),
+           GgmlTensor("encoder.positional_embedding", GGML_F32, (d, T),
+                      _rng(seed, "encoder.positional_embedding").standard_normal((T, d), dtype=np.float32) * np.float32(0.02))]
+    for i in range(L):
+        p = f"encoder.blocks.{i}."
+        for proj in ("query", "key", "value", "out"):
+            std = qk_std if proj in ("query", "key") else 0.02
+            out.append(_matrix(seed, f"{p}attn.{proj}.weight", d, d, wtype, std=std))
+            if proj != "key":
+                out.append(_vector(seed, f"{p}attn.{proj}.bias", d, "normal"))
+        out += ln(p + "attn_ln") + ln(p + "mlp_ln")
+        out.append(_matrix(seed, p + "mlp.0.weight", 4 * d, d, wtype))
+        out.append(_vector(seed, p + "mlp.0.bias", 4 * d, "normal"))
+        out.append(_matrix(seed, p + "mlp.2.weight", d, 4 * d, wtype))
+        out.append(_vector(seed, p + "mlp.2.bias", d, "normal"))
+    out += ln("encoder.ln_post")
+    return out
+
+
+def mel_input(edims: EncDims, seed: int = 0) -> np.ndarray:
+    """A synthetic log-mel input [n_mels][2 * n_audio_ctx], N(0, 0.6) fp32."""
+    return _rng(seed, "mel").standard_normal((edims.n_mels, 2 * edims.n_audio_ctx), dtype=np.float32) * np.float32(0.6)
+
+
 def encoder_output(dims: Dims, seed: int = 0, stream: int = 0) -> np.ndarray:
     return _rng(seed, f"encoder_output.{stream}").standard_normal((dims.n_audio_ctx, dims.n_text_state),
                                                                   dtype=np.float32)
@@ -196,15 +264,20 @@ def forced_tokens(n: int, seed: int = 0, high: int = 50256) -> np.ndarray:
     return _rng(seed, "forced_tokens").integers(0, high + 1, size=n, dtype=np.int32)
 
 
-def write_ggml(path: str, dims: Dims, tensors: list, ftype: int = 1) -> None:
+def write_ggml(path: str, dims: Dims, tensors: list, ftype: int = 1, edims: EncDims | None = None) -> None:
     """Write a whisper.cpp GGML file (layout read by model/GgmlLoader.java:95-216).
 
-    The decoder-only files carry placeholder encoder hparams, no mel filters and no vocab.
+    Without ``edims`` the file carries placeholder encoder hparams; there are no mel filters and no
+    vocab.
     """
     with open(path, "wb") as f:
         f.write(struct.pack("<i", GGML_MAGIC))
-        hp = [dims.n_vocab, dims.n_audio_ctx, dims.n_text_state, dims.n_text_head, 0,
-              dims.n_text_ctx, dims.n_text_state, dims.n_text_head, dims.n_text_layer, 80, ftype]
+        if edims is None:
+            enc = [dims.n_audio_ctx, dims.n_text_state, dims.n_text_head, 0, 80]
+        else:
+            enc = [edims.n_audio_ctx, edims.n_audio_state, edims.n_audio_head, edims.n_audio_layer, edims.n_mels]
+        hp = [dims.n_vocab, enc[0], enc[1], enc[2], enc[3],
+              dims.n_text_ctx, dims.n_text_state, dims.n_text_head, dims.n_text_layer, enc[4], ftype]
         f.write(struct.pack("<11i", *hp))
         f.write(struct.pack("<ii", 0, 0))  # mel filters: n_mel, n_fft
         f.write(struct.pack("<i", 0))  # vocab count
