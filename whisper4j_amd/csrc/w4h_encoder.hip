@@ -22,7 +22,7 @@ namespace w4h {
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
-constexpr int kEncBM = 128;           // GEMM rows (frames) per workgroup: 32 per wave
+constexpr int kXcds = 8;              // accelerator complex dies of an MI355X, each with its own L2
 constexpr int kEncBN = 64;            // GEMM columns per workgroup: 4 MFMA column tiles per wave
 constexpr int kEncBK = 64;            // k per stage: two MFMA k steps
 constexpr int kEncLd = kEncBK + kPadH;  // LDS pitch in halves (144 bytes)
@@ -31,32 +31,51 @@ constexpr int kEncLd = kEncBK + kPadH;  // LDS pitch in halves (144 bytes)
 //   kEpiStore: out = C;  kEpiGelu: out = gelu(C);  kEpiResid: out = add + C (add may alias out);
 //   kEpiGeluPos: out = gelu(C) + add (the positional embedding, [M][N]);
 //   kEpiQkv: C's columns are q | k | v of H heads; each goes out as f16 hi/lo planes
-//   (q pre-multiplied by 0.125, the exact 1/sqrt(64) of the scores): q, k as [H][M][64],
-//   v transposed as [H][64][M] (the attention kernel's operand layouts).
+//   (q pre-multiplied by 0.125, the exact 1/sqrt(64) of the scores): q, k as [H][Tp][64],
+//   v transposed as [H][64][Tp] (the attention kernel's operand layouts).
+// Each wave owns MT x 16 rows x 64 columns (a workgroup 64 MT rows).  Its activation rows go from
+// memory straight into MFMA operand registers (lane: row lane & 15, 8 consecutive k per k step)
+// and are split into hi/lo there; only the weight tile, shared by the four waves, is staged in LDS.
+// Both are loaded one stage ahead.  MT = 1: two 16-row tiles per wave (half the weight reads per
+// product, half the workgroups) measured slower on the widest GEMM (turbo MLP1: 109 against 103 us).
 template <int EPI, int WQ8>
 __global__ __launch_bounds__(256) void k_enc_gemm(EncGemm g) {
-  __shared__ __attribute__((aligned(16))) _Float16 s_ah[kEncBM * kEncLd];
-  __shared__ __attribute__((aligned(16))) _Float16 s_al[kEncBM * kEncLd];
+  constexpr int MT = 1;
+  constexpr int kEncBM = 64 * MT;
   __shared__ __attribute__((aligned(16))) _Float16 s_b[kEncBN * kEncLd];
   __shared__ float s_sc[kEncBN][2];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int m0 = blockIdx.x * kEncBM, n0 = blockIdx.y * kEncBN;
   const int M = g.M, N = g.N, K = g.K;
-  // Stage registers.  A: 128 x 64 fp32 = 2048 float4, 8 per thread (c = j * 256 + tid: row c >> 4,
-  // k 4 * (c & 15)); rows past M read row M - 1 (results dropped), k past K reads zeros.  f16 W:
-  // 64 x 64 halves, 2 x 16 bytes per thread (row c >> 3, k 8 * (c & 7)); q8_0 W: 64 x 64 int8, 16
-  // bytes per thread (row tid >> 2, k 16 * (tid & 3)) and the scales (row tid >> 1, block tid & 1).
-  float4 ra[8];
+  // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs (id % 8), each with
+  // its own L2.  XCD x takes the consecutive tiles [x * per, (x + 1) * per) in row-block-major order,
+  // so the column tiles of one row block run on one XCD and read its activation rows from that L2.
+  const int ncb = (N + kEncBN - 1) / kEncBN, ntiles = ((M + kEncBM - 1) / kEncBM) * ncb;
+  const int per = (ntiles + kXcds - 1) / kXcds;
+  const int tile = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  if (tile >= ntiles) return;
+  const int m0 = (tile / ncb) * kEncBM, n0 = (tile % ncb) * kEncBN;
+  // activation operand of m tile mt: row (clamped; rows past M are dropped) m0 + wv * 16 MT + 16 mt +
+  // (lane & 15), k = k0 + 32 ks + 8 (lane >> 4) + [0, 8)
+  const float* arow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    arow[mt] = g.a + (size_t)min(m0 + wv * 16 * MT + 16 * mt + (lane & 15), M - 1) * g.lda + 8 * (lane >> 4);
+  float4 ra[MT][4];  // [mt][ks][half]
+  // f16 W: 64 x 64 halves, 2 x 16 bytes per thread (row c >> 3, k 8 * (c & 7)); q8_0 W: 64 x 64 int8,
+  // 16 bytes per thread (row tid >> 2, k 16 * (tid & 3)) and the scales (row tid >> 1, block tid & 1)
   uint4 rb[2];
   uint4 rq;
   uint16_t rs = 0;
   auto load = [&](int k0) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int c = j * 256 + tid;
-      const int r = min(m0 + (c >> 4), M - 1), k = k0 + 4 * (c & 15);
-      ra[j] = k < K ? *reinterpret_cast<const float4*>(g.a + (size_t)r * g.lda + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int k = k0 + 32 * ks + 8 * (lane >> 4);
+        const bool in = k < K;  // K % 8 == 0: a lane's 8 values are all in range or all out
+        ra[mt][2 * ks] = in ? *reinterpret_cast<const float4*>(arow[mt] + k0 + 32 * ks) : make_float4(0.f, 0.f, 0.f, 0.f);
+        ra[mt][2 * ks + 1] = in ? *reinterpret_cast<const float4*>(arow[mt] + k0 + 32 * ks + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
     if (!WQ8) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -72,20 +91,6 @@ __global__ __launch_bounds__(256) void k_enc_gemm(EncGemm g) {
     }
   };
   auto stash = [&]() {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int c = j * 256 + tid;
-      const int o = (c >> 4) * kEncLd + 4 * (c & 15);
-      const float v[4] = {ra[j].x, ra[j].y, ra[j].z, ra[j].w};
-      half4 hi, lo;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        hi[e] = (_Float16)v[e];
-        lo[e] = (_Float16)(v[e] - (float)hi[e]);
-      }
-      *reinterpret_cast<half4*>(&s_ah[o]) = hi;
-      *reinterpret_cast<half4*>(&s_al[o]) = lo;
-    }
     if (!WQ8) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -100,81 +105,86 @@ __global__ __launch_bounds__(256) void k_enc_gemm(EncGemm g) {
     }
   };
 
-  floatx4 acc[2][4];
+  floatx4 acc[MT][4];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   load(0);
   for (int k0 = 0; k0 < K; k0 += kEncBK) {
-    lds_barrier();  // every wave has read the previous stage
+    lds_barrier();  // every wave has read the previous weight tile
     stash();
+    // this stage's activation operand, split into hi/lo (registers of the loads just consumed)
+    half8 ah[MT][2], al[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const float v[8] = {ra[mt][2 * ks].x, ra[mt][2 * ks].y, ra[mt][2 * ks].z, ra[mt][2 * ks].w,
+                            ra[mt][2 * ks + 1].x, ra[mt][2 * ks + 1].y, ra[mt][2 * ks + 1].z, ra[mt][2 * ks + 1].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          ah[mt][ks][e] = (_Float16)v[e];
+          al[mt][ks][e] = (_Float16)(v[e] - (float)ah[mt][ks][e]);
+        }
+      }
     lds_barrier();
-    if (k0 + kEncBK < K) load(k0 + kEncBK);
+    load(min(k0 + kEncBK, ((K - 1) / kEncBK) * kEncBK));  // the last stage again at the end
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int kk = ks * 32 + 8 * (lane >> 4);
-      half8 bfr[4];
-      float sc[4];
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
-        bfr[nt] = *reinterpret_cast<const half8*>(&s_b[(nt * 16 + (lane & 15)) * kEncLd + kk]);
-        sc[nt] = WQ8 ? s_sc[nt * 16 + (lane & 15)][ks] : 1.f;
-      }
+        const half8 bfr = *reinterpret_cast<const half8*>(&s_b[(nt * 16 + (lane & 15)) * kEncLd + kk]);
+        const float sc = WQ8 ? s_sc[nt * 16 + (lane & 15)][ks] : 1.f;
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int r = wv * 32 + mt * 16 + (lane & 15);
-        const half8 ah = *reinterpret_cast<const half8*>(&s_ah[r * kEncLd + kk]);
-        const half8 al = *reinterpret_cast<const half8*>(&s_al[r * kEncLd + kk]);
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
+        for (int mt = 0; mt < MT; ++mt) {
           if (!WQ8) {
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bfr[nt], acc[mt][nt], 0, 0, 0);
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bfr[nt], acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt][ks], bfr, acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt][ks], bfr, acc[mt][nt], 0, 0, 0);
           } else {
-            floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bfr[nt], floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bfr[nt], t, 0, 0, 0);
+            floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt][ks], bfr, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt][ks], bfr, t, 0, 0, 0);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[mt][nt][e] = fmaf(sc[nt], t[e], acc[mt][nt][e]);
+            for (int e = 0; e < 4; ++e) acc[mt][nt][e] = fmaf(sc, t[e], acc[mt][nt][e]);
           }
         }
       }
     }
   }
 
-  // Epilogue: lane holds rows wv * 32 + mt * 16 + 4 * (lane >> 4) + e of column nt * 16 + (lane & 15).
+  // Epilogue: lane holds rows wv * 16 MT + 16 mt + 4 * (lane >> 4) + e of column nt * 16 + (lane & 15).
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
     const int n = n0 + nt * 16 + (lane & 15);
     if (n >= N) continue;
     const float b = g.bias ? g.bias[n] : 0.f;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = m0 + wv * 32 + mt * 16 + 4 * (lane >> 4) + e;
-        if (m >= M) continue;
-        const float c = acc[mt][nt][e] + b;
-        if constexpr (EPI == kEpiStore) {
-          g.out[(size_t)m * g.ldo + n] = c;
-        } else if constexpr (EPI == kEpiGelu) {
-          g.out[(size_t)m * g.ldo + n] = gelu_f16(c);
-        } else if constexpr (EPI == kEpiResid) {
-          g.out[(size_t)m * g.ldo + n] = g.add[(size_t)m * g.ldo + n] + c;
-        } else if constexpr (EPI == kEpiGeluPos) {
-          g.out[(size_t)m * g.ldo + n] = gelu_f16(c) + g.add[(size_t)m * N + n];
-        } else {  // kEpiQkv
-          const int d = N / 3, part = n / d, h = (n - part * d) >> 6, ei = n & 63;
-          const float v = part == 0 ? c * 0.125f : c;
-          const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
-          const size_t plane = (size_t)(d >> 6) * g.Tp * kHeadDim;  // halves per (part, hi|lo) plane
-          const size_t idx = part == 2 ? ((size_t)h * kHeadDim + ei) * g.Tp + m : ((size_t)h * g.Tp + m) * kHeadDim + ei;
-          _Float16* q16 = reinterpret_cast<_Float16*>(g.qkv);
-          q16[(size_t)(part * 2) * plane + idx] = hi;
-          q16[(size_t)(part * 2 + 1) * plane + idx] = lo;
-        }
+    for (int me = 0; me < 4 * MT; ++me) {
+      const int mt = me >> 2, e = me & 3;
+      const int m = m0 + wv * 16 * MT + 16 * mt + 4 * (lane >> 4) + e;
+      if (m >= M) continue;
+      const float c = acc[mt][nt][e] + b;
+      if constexpr (EPI == kEpiStore) {
+        g.out[(size_t)m * g.ldo + n] = c;
+      } else if constexpr (EPI == kEpiGelu) {
+        g.out[(size_t)m * g.ldo + n] = gelu_f16(c);
+      } else if constexpr (EPI == kEpiResid) {
+        g.out[(size_t)m * g.ldo + n] = g.add[(size_t)m * g.ldo + n] + c;
+      } else if constexpr (EPI == kEpiGeluPos) {
+        g.out[(size_t)m * g.ldo + n] = gelu_f16(c) + g.add[(size_t)m * N + n];
+      } else {  // kEpiQkv
+        const int d = N / 3, part = n / d, h = (n - part * d) >> 6, ei = n & 63;
+        const float v = part == 0 ? c * 0.125f : c;
+        const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
+        const size_t plane = (size_t)(d >> 6) * g.Tp * kHeadDim;  // halves per (part, hi|lo) plane
+        const size_t idx = part == 2 ? ((size_t)h * kHeadDim + ei) * g.Tp + m : ((size_t)h * g.Tp + m) * kHeadDim + ei;
+        _Float16* q16 = reinterpret_cast<_Float16*>(g.qkv);
+        q16[(size_t)(part * 2) * plane + idx] = hi;
+        q16[(size_t)(part * 2 + 1) * plane + idx] = lo;
       }
+    }
   }
 }
 
@@ -379,7 +389,8 @@ __global__ void k_enc_mel_t(const float* __restrict__ mel, int n_mels, int frame
 
 template <int EPI>
 static hipError_t gemm_t(const EncGemm& g, hipStream_t st) {
-  const dim3 grid((g.M + kEncBM - 1) / kEncBM, (g.N + kEncBN - 1) / kEncBN);
+  const int ntiles = ((g.M + 63) / 64) * ((g.N + kEncBN - 1) / kEncBN);
+  const dim3 grid(((ntiles + kXcds - 1) / kXcds) * kXcds);
   if (g.ws)
     hipLaunchKernelGGL((k_enc_gemm<EPI, 1>), grid, dim3(256), 0, st, g);
   else
