@@ -46,6 +46,7 @@ extern "C" {
 #define W4H_ERR_CAPACITY -8  /* KV context full */
 #define W4H_ERR_TIMEOUT -9   /* a bounded device-side wait expired (the step is aborted, never hangs) */
 #define W4H_ERR_IO -10       /* file could not be read */
+#define W4H_ERR_CANCELLED -11 /* the session was cancelled (w4h_session_cancel) */
 
 /* ---- GGML tensor types accepted by model creation (GgmlLoader type ids) ---- */
 #define W4H_TYPE_F32 0
@@ -164,6 +165,14 @@ int w4h_session_set_suppress(w4h_session* s, const int32_t* ids, int32_t n);
  * workload whose selection is made deterministic by a seeded logit bias.  step_out, logits and the
  * decode drivers all see the biased logits. */
 int w4h_session_set_logit_bias(w4h_session* s, const float* bias);
+/* Cancel the session's work (TranscriptionHandle.cancel, main/WhisperModel.java:620-633; the reference
+ * checks it between segments): on = 1 may be called from ANY thread, also while another thread is
+ * inside a call on this session.  The call in flight returns W4H_ERR_CANCELLED: a one-launch greedy
+ * decode stops at its next step, a sampled decode at its next launch, other launches when they end;
+ * every later call returns W4H_ERR_CANCELLED too.  on = 0 (from the session's own thread, with no call
+ * in flight) clears it; the self-KV is then undefined until w4h_session_reset (the decode drivers
+ * reset it themselves). */
+int w4h_session_cancel(w4h_session* s, int32_t on);
 /* Token whose raw logit is reported in w4h_step_out.probe_logit (e.g. <|nospeech|>), -1 for none. */
 int w4h_session_set_probe(w4h_session* s, int32_t token);
 

@@ -137,3 +137,49 @@ def test_persistent_kernel_size_guard(gpu, monkeypatch):
     s = m.session(n_rows=4, n_encoders=4, max_ctx=64)
     s.close()
     m.close()
+
+
+@pytest.mark.parametrize("mode", ["greedy", "sampled", "beam"])
+def test_cancel_from_another_thread(gpu, mode):
+    """w4h_session_cancel (TranscriptionHandle.cancel, main/WhisperModel.java:620-633) from another
+    thread while the owner thread is inside a long decode: a greedy decode running as one launch
+    (decode rules on the device), a sampled decode (T = 0.5, a chain of launches) and a beam-5 search
+    on the batched engine each return W4H_ERR_CANCELLED well before the uncancelled decode's time;
+    calls on the cancelled session return W4H_ERR_CANCELLED at once; once cleared, the same decode on
+    the same session gives the uncancelled result again."""
+    import time
+
+    dims = synth.Dims(n_vocab=2000, n_text_ctx=1024, n_text_state=256, n_text_head=4, n_text_layer=4, n_audio_ctx=64)
+    T = synth.make_decoder(dims, seed=31)
+    xa = synth.encoder_output(dims, 31)
+    beam = 5 if mode == "beam" else 1
+    prompt, eot, n = [1, 2, 3], 1999, 900 if mode != "beam" else 600
+    kw = dict(temperature=0.5, seed=4) if mode == "sampled" else {}
+    with gpu.Model.from_tensors(dims, T) as m:
+        dec = gpu.WhisperDecoder(m, beam_size=beam, max_ctx=1024)
+        run = (lambda: dec.decode_beam(xa, prompt, eot, n, [eot], beam_size=5)) if mode == "beam" else \
+              (lambda: dec.decode(xa, prompt, eot, n, [eot], **kw))
+        run()  # warm-up
+        t0 = time.perf_counter()
+        full = run()
+        t_full = time.perf_counter() - t0
+        assert len(full.tokens) >= n - 2
+        delay = 0.2 * t_full
+        th = threading.Timer(delay, lambda: dec.session.cancel(True))
+        t0 = time.perf_counter()
+        th.start()
+        with pytest.raises(gpu.W4HError) as ei:
+            run()
+        t_cancel = time.perf_counter() - t0
+        th.join()
+        say(f"{mode}: uncancelled {t_full * 1e3:.1f} ms, cancel after {delay * 1e3:.1f} ms returned after {t_cancel * 1e3:.1f} ms")
+        assert ei.value.code == -11
+        assert t_cancel < 0.6 * t_full
+        with pytest.raises(gpu.W4HError) as ei:
+            run()
+        assert ei.value.code == -11
+        dec.session.cancel(False)
+        again = run()
+        assert again.tokens == full.tokens
+        assert again.avg_logprob == full.avg_logprob
+        dec.close()

@@ -23,6 +23,7 @@ W4H_ERR_CLOSED = -7
 W4H_ERR_CAPACITY = -8
 W4H_ERR_TIMEOUT = -9
 W4H_ERR_IO = -10
+W4H_ERR_CANCELLED = -11
 TOPK_MAX = 8
 
 TYPE_F32, TYPE_F16, TYPE_Q8_0 = 0, 1, 8
@@ -33,7 +34,7 @@ EXPORTS = (
     "w4h_model_destroy", "w4h_encoder_create", "w4h_encoder_load_ggml", "w4h_encoder_get_dims",
     "w4h_encoder_forward", "w4h_encoder_forward_device", "w4h_encoder_destroy", "w4h_ggml_inspect", "w4h_ggml_read_tensor", "w4h_session_create", "w4h_session_destroy",
     "w4h_session_set_encoder", "w4h_session_set_encoder_device", "w4h_session_reset", "w4h_session_kv_len", "w4h_session_set_suppress",
-    "w4h_session_set_probe", "w4h_session_set_logit_bias", "w4h_session_step", "w4h_session_run", "w4h_session_reorder", "w4h_session_time_run",
+    "w4h_session_set_probe", "w4h_session_set_logit_bias", "w4h_session_cancel", "w4h_session_step", "w4h_session_run", "w4h_session_reorder", "w4h_session_time_run",
     "w4h_session_trace_run",
     "w4h_decode", "w4h_decode_beam", "w4h_decode_with_fallback", "w4h_compression_ratio", "w4h_op_linear",
     "w4h_op_layernorm", "w4h_op_gelu", "w4h_op_attention", "w4h_op_select", "w4h_op_sample",
@@ -123,6 +124,7 @@ def lib():
         "w4h_session_set_suppress": (i32, [vp, i32p, i32]),
         "w4h_session_set_probe": (i32, [vp, i32]),
         "w4h_session_set_logit_bias": (i32, [vp, f32p]),
+        "w4h_session_cancel": (i32, [vp, i32]),
         "w4h_session_step": (i32, [vp, i32p, u32p, i32, ctypes.POINTER(StepOut), f32p]),
         "w4h_session_run": (i32, [vp, i32p, i32p, i32, i32, ctypes.POINTER(StepOut)]),
         "w4h_session_reorder": (i32, [vp, i32p]),

@@ -422,6 +422,10 @@ int w4h_model_destroy(w4h_model* m) {
 // ---------------------------------------------------------------------------------------------
 // sessions
 
+// Input area of a session: the device cancel word at offset 0, the error word at kErrOff (the kernels'
+// abort check reads both with one 8-byte load), per-step inputs from offset 256.
+constexpr size_t kErrOff = 4;
+
 struct w4h_session {
   w4h_model* m = nullptr;
   int S = 1, X = 1, max_ctx = 0, grid = 0, ngroups = 2, ncs_max = 0, ncc = 0, chc = 0, rpw = 0, mw = 0;
@@ -460,6 +464,11 @@ struct w4h_session {
   bool use_graph = true;
   // device-sampled decodes (T > 0): sampler state, the step's logits rows, the static suppress mask
   DevBuf samp, samp_row, samp_sup;
+  // cancellation (w4h_session_cancel, callable from any thread): the host flag, and the device cancel
+  // word (input area offset 0, before the error word) written on a stream of its own
+  std::atomic<int> cancel{0};
+  std::mutex cancel_mu;
+  hipStream_t ctl = nullptr;
 };
 
 namespace w4h {
@@ -504,7 +513,7 @@ static StepParams base_params(w4h_session* s) {
   p.mask = s->has_mask ? s->mask.as<uint32_t>() : nullptr;
   p.mw = s->mw;
   p.probe = s->probe;
-  p.err = s->in_at<unsigned>(0);
+  p.err = s->in_at<unsigned>(kErrOff);
   p.rows_per_wg = s->rpw;
   p.ngroups = s->ngroups;
   p.rep_stride = s->rep_stride;
@@ -580,7 +589,7 @@ static int copy_back(w4h_session* s, int n_steps, w4h_step_out* out, float* logi
   int rc;
   if ((rc = s->h_out.ensure(b_err + b_out + b_lg))) return rc;
   char* hp = static_cast<char*>(s->h_out.p);
-  if (herr) HIPCHK(hipMemcpyAsync(hp, s->in.p, sizeof(unsigned), hipMemcpyDeviceToHost, s->stream));
+  if (herr) HIPCHK(hipMemcpyAsync(hp, s->in_at<char>(kErrOff), sizeof(unsigned), hipMemcpyDeviceToHost, s->stream));
   if (b_out) HIPCHK(hipMemcpyAsync(hp + b_err, s->out.p, b_out, hipMemcpyDeviceToHost, s->stream));
   if (b_lg) HIPCHK(hipMemcpyAsync(hp + b_err + b_out, s->logits.p, b_lg, hipMemcpyDeviceToHost, s->stream));
   HIPCHK(hipStreamSynchronize(s->stream));
@@ -622,6 +631,7 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
               int topk, w4h_step_out* out, float* logits, float* ms, uint64_t* trace = nullptr,
               const RulesRun* rules = nullptr, int* steps_done = nullptr) {
   if (s->closed) return fail(W4H_ERR_CLOSED, "session destroyed");
+  if (s->cancel.load()) return fail(W4H_ERR_CANCELLED, "session cancelled");
   if (!tokens || n_steps <= 0) return fail(W4H_ERR_INVALID, "tokens and n_steps > 0 required");
   if (topk < 0 || topk > W4H_TOPK_MAX) return fail(W4H_ERR_INVALID, "topk %d outside [0, %d]", topk, W4H_TOPK_MAX);
   if (s->kv_len + n_steps > s->max_ctx)
@@ -637,12 +647,12 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
   int rc;
   // per-step inputs: one asynchronous copy of the leading part of the input area that changed
   char* hp = static_cast<char*>(s->h_in.p);
-  *reinterpret_cast<unsigned*>(hp) = 0u;  // error word
+  *reinterpret_cast<unsigned*>(hp + kErrOff) = 0u;  // error word (the cancel word before it is not copied)
   memcpy(hp + s->o_toks, tokens, sizeof(int32_t) * s->S);
   if (extra_mask) memcpy(hp + s->o_mask2, extra_mask, sizeof(uint32_t) * (size_t)s->S * s->mw);
   if (s->slots_dirty) memcpy(hp + s->o_slots, s->slots_host.data(), sizeof(int32_t) * s->slots_host.size());
   const size_t in_len = s->slots_dirty ? s->in_bytes : (extra_mask ? s->o_slots : s->o_mask2);
-  HIPCHK(hipMemcpyAsync(s->in.p, hp, in_len, hipMemcpyHostToDevice, s->stream));
+  HIPCHK(hipMemcpyAsync(s->in_at<char>(kErrOff), hp + kErrOff, in_len - kErrOff, hipMemcpyHostToDevice, s->stream));
   s->slots_dirty = false;
   if (rules && (s->wide || s->S != 1 || forced || !out || trace || !steps_done || rules->nhist < 0 ||
                 (rules->nhist > 0 && !rules->hist)))
@@ -690,6 +700,7 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
       (void)hipEventDestroy(e1);
     }
     s->kv_len += n_steps;
+    if (s->cancel.load()) return fail(W4H_ERR_CANCELLED, "session cancelled");
     return W4H_OK;
   }
   StepParams p = base_params(s);
@@ -732,6 +743,7 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
   }
+  if (s->cancel.load()) return fail(W4H_ERR_CANCELLED, "session cancelled during the launch");
   if (herr) return fail(W4H_ERR_TIMEOUT, "a device-side wait expired during the step (code %u); step aborted", herr);
   int done = n_steps;
   if (rules)
@@ -823,6 +835,10 @@ int create_wide(std::unique_ptr<w4h_session>& s, const hipDeviceProp_t& prop, w4
   if (const char* e = getenv("W4H_GRAPH")) s->use_graph = atoi(e) != 0;
   if ((rc = s->mask.alloc(sizeof(uint32_t) * (size_t)s->S * s->mw))) return rc;
   if ((rc = s->bias.alloc(sizeof(float) * (size_t)V))) return rc;
+  // sampled-decode state, allocated up front: w4h_session_cancel writes its stop word from any thread
+  if ((rc = s->samp.alloc(sizeof(SampleDev)))) return rc;
+  HIPCHK(hipMemsetAsync(s->samp.p, 0, sizeof(SampleDev), s->stream));
+  HIPCHK(hipStreamCreateWithFlags(&s->ctl, hipStreamNonBlocking));
   HIPCHK(hipStreamSynchronize(s->stream));
   m->refs.fetch_add(1);
   *out = s.release();
@@ -953,6 +969,10 @@ int w4h_session_create(w4h_model* m, const w4h_session_desc* desc, w4h_session**
   HIPCHK(launch_fill_u64(s->ll.as<u64>(), total * kRep, s->stream));
   if ((rc = s->mask.alloc(sizeof(uint32_t) * (size_t)s->S * s->mw))) return rc;
   if ((rc = s->bias.alloc(sizeof(float) * (size_t)V))) return rc;
+  // sampled-decode state, allocated up front: w4h_session_cancel writes its stop word from any thread
+  if ((rc = s->samp.alloc(sizeof(SampleDev)))) return rc;
+  HIPCHK(hipMemsetAsync(s->samp.p, 0, sizeof(SampleDev), s->stream));
+  HIPCHK(hipStreamCreateWithFlags(&s->ctl, hipStreamNonBlocking));
   HIPCHK(hipStreamSynchronize(s->stream));
   m->refs.fetch_add(1);
   *out = s.release();
@@ -969,8 +989,24 @@ int w4h_session_destroy(w4h_session* s) {
     wide_graph_release(&s->wgraph_beam);
     (void)hipStreamDestroy(s->stream);
   }
+  if (s->ctl) (void)hipStreamDestroy(s->ctl);
   delete s;
   model_release(m);
+  return W4H_OK;
+}
+
+int w4h_session_cancel(w4h_session* s, int32_t on) {
+  if (!s) return fail(W4H_ERR_INVALID, "null argument");
+  std::lock_guard<std::mutex> lk(s->cancel_mu);
+  HIPCHK(hipSetDevice(s->m->device));
+  s->cancel.store(on ? 1 : 0);
+  // The device words are written by the command processor of the control stream's queue (a stream
+  // write, no copy kernel), so the write lands while the persistent kernel holds every compute unit:
+  // the cancel word (read by the step kernel's waits and, with decode rules, once per step), and a
+  // sampled decode's stop word, which makes every later launch of its chain return at once.
+  HIPCHK(hipStreamWriteValue32(s->ctl, s->in.p, on ? 1u : 0u, 0));
+  if (on && !s->wide) HIPCHK(hipStreamWriteValue32(s->ctl, &s->samp.as<SampleDev>()->stop, 1u, 0));
+  HIPCHK(hipStreamSynchronize(s->ctl));
   return W4H_OK;
 }
 
@@ -1303,6 +1339,7 @@ bool session_device_sample(const w4h_session* s) {
 // synchronises once per run.
 int device_sampled_run(w4h_session* s, const SampleRun& r, int n_steps, const uint32_t* sup, SampleRunOut* out) {
   if (!session_device_sample(s)) return fail(W4H_ERR_INVALID, "device sampling needs a persistent session");
+  if (s->cancel.load()) return fail(W4H_ERR_CANCELLED, "session cancelled");
   if (r.nhist < 1 || !r.hist || r.nhist >= kSampleHist) return fail(W4H_ERR_INVALID, "device sampling needs the generated tokens");
   if (!(r.temperature > 0.0f)) return fail(W4H_ERR_INVALID, "device sampling needs a temperature above 0");
   if (n_steps < 1 || n_steps > kSampleHist) return fail(W4H_ERR_INVALID, "n_steps outside [1, %d]", kSampleHist);
@@ -1312,8 +1349,7 @@ int device_sampled_run(w4h_session* s, const SampleRun& r, int n_steps, const ui
   const int V = s->m->dims.n_vocab;
   int rc;
   HIPCHK(hipSetDevice(s->m->device));
-  if ((rc = ensure(s->samp, sizeof(SampleDev))) || (rc = ensure(s->samp_row, sizeof(float) * (size_t)s->S * V)) ||
-      (rc = ensure(s->samp_sup, sizeof(uint32_t) * (size_t)s->mw)))
+  if ((rc = ensure(s->samp_row, sizeof(float) * (size_t)s->S * V)) || (rc = ensure(s->samp_sup, sizeof(uint32_t) * (size_t)s->mw)))
     return rc;
   std::vector<char> hb(sizeof(SampleDev), 0);
   SampleDev* h = reinterpret_cast<SampleDev*>(hb.data());
@@ -1322,12 +1358,16 @@ int device_sampled_run(w4h_session* s, const SampleRun& r, int n_steps, const ui
   for (int q = 0; q < s->S; q++) h->tok[q] = r.hist[r.nhist - 1];
   // error word (and the slot table, when a reorder changed it) as run_steps stages them
   char* hp = static_cast<char*>(s->h_in.p);
-  *reinterpret_cast<unsigned*>(hp) = 0u;
+  *reinterpret_cast<unsigned*>(hp + kErrOff) = 0u;
   if (s->slots_dirty) memcpy(hp + s->o_slots, s->slots_host.data(), sizeof(int32_t) * s->slots_host.size());
-  HIPCHK(hipMemcpyAsync(s->in.p, hp, s->slots_dirty ? s->in_bytes : sizeof(unsigned), hipMemcpyHostToDevice, s->stream));
+  HIPCHK(hipMemcpyAsync(s->in_at<char>(kErrOff), hp + kErrOff, (s->slots_dirty ? s->in_bytes : kErrOff + sizeof(unsigned)) - kErrOff,
+                        hipMemcpyHostToDevice, s->stream));
   s->slots_dirty = false;
   HIPCHK(hipMemcpyAsync(s->samp.p, hb.data(), offsetof(SampleDev, out_tok), hipMemcpyHostToDevice, s->stream));
   if (sup) HIPCHK(hipMemcpyAsync(s->samp_sup.p, sup, sizeof(uint32_t) * (size_t)s->mw, hipMemcpyHostToDevice, s->stream));
+  // the state is in place before the chain starts, so a cancel's stop word cannot be overwritten by it
+  HIPCHK(hipStreamSynchronize(s->stream));
+  if (s->cancel.load()) return fail(W4H_ERR_CANCELLED, "session cancelled");
   SampleDev* dst = s->samp.as<SampleDev>();
   SampleParams sp{};
   sp.logits = s->samp_row.as<float>();
@@ -1354,19 +1394,32 @@ int device_sampled_run(w4h_session* s, const SampleRun& r, int n_steps, const ui
   p.nres = 0;  // one step per launch: loading resident vocabulary rows would not pay
   p.stop = &dst->stop;
   {
+    // Enqueued kSampleChunk steps at a time; between chunks the host reads the stop word (end token,
+    // last step or cancel), so a decode that ends early leaves no launches to drain.
+    constexpr int kSampleChunk = 32;
     std::unique_lock<std::mutex> coop(coop_lock(s->m->device));
-    for (int i = 0; i < n_steps; i++) {
-      p.kv_len0 = s->kv_len + i;
-      p.tag0 = s->next_tag++;
-      hipError_t le = launch_step(p, s->grid, s->lds, s->stream);
-      if (le != hipSuccess) return fail(W4H_ERR_DEVICE, "decoder step launch failed: %s", hipGetErrorString(le));
-      if ((le = launch_sample_mask(sp, s->stream)) != hipSuccess || (le = launch_sample(sp, s->stream)) != hipSuccess)
-        return fail(W4H_ERR_DEVICE, "sampling launch failed: %s", hipGetErrorString(le));
+    int i = 0;
+    while (i < n_steps) {
+      const int nc = std::min(kSampleChunk, n_steps - i);
+      for (int j = 0; j < nc; j++, i++) {
+        p.kv_len0 = s->kv_len + i;
+        p.tag0 = s->next_tag++;
+        hipError_t le = launch_step(p, s->grid, s->lds, s->stream);
+        if (le != hipSuccess) return fail(W4H_ERR_DEVICE, "decoder step launch failed: %s", hipGetErrorString(le));
+        if ((le = launch_sample_mask(sp, s->stream)) != hipSuccess || (le = launch_sample(sp, s->stream)) != hipSuccess)
+          return fail(W4H_ERR_DEVICE, "sampling launch failed: %s", hipGetErrorString(le));
+      }
+      if (i >= n_steps) break;
+      int32_t hdr[4];
+      HIPCHK(hipMemcpyAsync(hdr, s->samp.p, sizeof(hdr), hipMemcpyDeviceToHost, s->stream));
+      HIPCHK(hipStreamSynchronize(s->stream));
+      if (hdr[2] || s->cancel.load()) break;  // SampleDev::stop
     }
     HIPCHK(hipMemcpyAsync(hb.data(), s->samp.p, sizeof(SampleDev), hipMemcpyDeviceToHost, s->stream));
     unsigned herr = 0;
-    HIPCHK(hipMemcpyAsync(&herr, s->in.p, sizeof(unsigned), hipMemcpyDeviceToHost, s->stream));
+    HIPCHK(hipMemcpyAsync(&herr, s->in_at<char>(kErrOff), sizeof(unsigned), hipMemcpyDeviceToHost, s->stream));
     HIPCHK(hipStreamSynchronize(s->stream));
+    if (s->cancel.load()) return fail(W4H_ERR_CANCELLED, "session cancelled during the sampled decode");
     if (herr) return fail(W4H_ERR_TIMEOUT, "a device-side wait expired during the step (code %u); step aborted", herr);
   }
   s->kv_len += h->steps;  // one step-kernel launch ran per sampled step
@@ -1398,11 +1451,11 @@ int device_beam_search(w4h_session* s, const BeamSearchIn& in, BeamSearchOut* ou
     HIPCHK(hipMemcpy(s->wbsup.p, in.suppress, sizeof(int32_t) * in.n_suppress, hipMemcpyHostToDevice));
   // first run's inputs (tokens, mask, slot table) through the staging area
   char* hp = static_cast<char*>(s->h_in.p);
-  *reinterpret_cast<unsigned*>(hp) = 0u;
+  *reinterpret_cast<unsigned*>(hp + kErrOff) = 0u;
   memcpy(hp + s->o_toks, in.first_tokens, sizeof(int32_t) * B);
   memcpy(hp + s->o_mask2, in.first_mask, sizeof(uint32_t) * (size_t)B * s->mw);
   memcpy(hp + s->o_slots, s->slots_host.data(), sizeof(int32_t) * s->slots_host.size());
-  HIPCHK(hipMemcpyAsync(s->in.p, hp, s->in_bytes, hipMemcpyHostToDevice, s->stream));
+  HIPCHK(hipMemcpyAsync(s->in_at<char>(kErrOff), hp + kErrOff, s->in_bytes - kErrOff, hipMemcpyHostToDevice, s->stream));
   s->slots_dirty = false;
   constexpr int kChunk = 32;  // steps per launch; the host checks for the end of the search between launches
   if ((rc = ensure(s->out, sizeof(w4h_step_out) * (size_t)kChunk * B))) return rc;
@@ -1439,6 +1492,7 @@ int device_beam_search(w4h_session* s, const BeamSearchIn& in, BeamSearchOut* ou
     s->kv_len += c.i;  // steps that ran (each appended its KV row)
     remaining -= n;
     first = false;
+    if (s->cancel.load()) return fail(W4H_ERR_CANCELLED, "session cancelled during the beam search");
     if (c.stop) break;
   }
   // results, and the slot table the device left behind

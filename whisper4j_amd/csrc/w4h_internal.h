@@ -57,7 +57,7 @@ struct StepParams {
   int mw, probe, topk;
   w4h_step_out* out;            // [nsteps][S] or null
   float* logits_out;            // [nsteps][S][V] or null
-  unsigned* err;
+  unsigned* err;                // error word; the cancel word is the 4 bytes before it (8-byte aligned)
   int rows_per_wg;              // vocab rows one workgroup keeps in LDS in the logits phase
   int ngroups;                  // phase groups: 1, 2 (halves) or 4 (quarters); see phase_group
   size_t rep_stride;            // words between replicas of the exchange buffers

@@ -78,8 +78,11 @@ DEV void ll_st(u64* p, float v, uint32_t tag, size_t rs) {
 #pragma unroll
   for (int r = 0; r < kRep; ++r) __hip_atomic_store(p + r * rs, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// The error word and, just before it (8-byte aligned), the session's cancel word, which the host
+// may set while a launch runs: one 8-byte load covers both.
 DEV bool aborted(const unsigned* err) {
-  return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+  return __hip_atomic_load(reinterpret_cast<const unsigned long long*>(err - 1), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT) != 0ull;
 }
 DEV void raise_err(unsigned* err, unsigned code) {
   __hip_atomic_fetch_or(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2549,11 +2552,15 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
     }
     STAMP(3);
     ++c.ph;
+    // a decode with the rules on runs to its end token in this launch: it also ends on a cancel
+    // (the word is read before the selection wait, which hides its latency); workgroups that leave
+    // a step early make the others' next waits see the cancel word and leave as well
+    const bool cancel = p.rules && aborted(p.err);
     if (!phase_reduce(p, m, c)) return;
     STAMP(3);
     ++c.ph;
     // every workgroup saw the same token (all reduce the same pairs): the run ends together
-    if (p.rules && st + 1 < p.nsteps && m.toks[0] == p.eot) break;
+    if (p.rules && st + 1 < p.nsteps && (m.toks[0] == p.eot || cancel)) break;
   }
   kv_drain();
 }

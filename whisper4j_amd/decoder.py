@@ -214,6 +214,10 @@ class Session:
     def reset(self, kv_len: int = 0) -> None:
         check(lib().w4h_session_reset(self._h, kv_len))
 
+    def cancel(self, on: bool = True) -> None:
+        """Request (on) or clear (off) cancellation; on may come from any thread (see w4h.h)."""
+        check(lib().w4h_session_cancel(self._h, 1 if on else 0))
+
     @property
     def kv_len(self) -> int:
         n = ctypes.c_int32()
