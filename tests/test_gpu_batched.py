@@ -24,15 +24,21 @@ def say(*a):
 # (chunks of at most 128 keys), whose (max, sum, value) partials k_w_cmerge merges: 10 rows on one
 # encoder (two row groups of 8 and 2) and 4 rows with their own encoders.  Sessions of fewer than 5
 # rows at d < 768 would run on the persistent kernel, so the 4-row case sets W4H_ENGINE=wide.
-@pytest.mark.parametrize("d,heads,n_rows,n_enc,wtype,a_ctx", [(384, 6, 12, 12, "f16", 80), (512, 8, 20, 20, "f16", 80),
-                                                              (1280, 20, 32, 32, "f16", 80), (1024, 16, 16, 16, "q8_0", 80),
-                                                              (768, 12, 10, 1, "f16", 80), (384, 6, 10, 1, "f16", 300),
-                                                              (384, 6, 4, 4, "f16", 300)])
-def test_batched_streams_forced(gpu, orc, monkeypatch, d, heads, n_rows, n_enc, wtype, a_ctx):
+# Sessions of at most 16 rows at d in {384, 512, 768, 1024} run whole-K GEMMs with the residual,
+# LayerNorm and GELU inside them; split=True runs two of those cases on the split-K GEMMs and
+# separate kernels instead (W4H_WIDE_FUSE=0), which 20 and 32 rows and d = 1280 always use.
+@pytest.mark.parametrize("d,heads,n_rows,n_enc,wtype,a_ctx,split", [(384, 6, 12, 12, "f16", 80, False), (512, 8, 20, 20, "f16", 80, False),
+                                                                    (1280, 20, 32, 32, "f16", 80, False), (1024, 16, 16, 16, "q8_0", 80, False),
+                                                                    (768, 12, 10, 1, "f16", 80, False), (384, 6, 10, 1, "f16", 300, False),
+                                                                    (384, 6, 4, 4, "f16", 300, False), (768, 12, 10, 1, "f16", 80, True),
+                                                                    (1024, 16, 16, 16, "q8_0", 80, True)])
+def test_batched_streams_forced(gpu, orc, monkeypatch, d, heads, n_rows, n_enc, wtype, a_ctx, split):
     dims = synth.Dims(n_vocab=1200, n_text_ctx=48, n_text_state=d, n_text_head=heads, n_text_layer=2, n_audio_ctx=a_ctx)
     if n_rows < 5:
         monkeypatch.setenv("W4H_ENGINE", "wide")
-    say(f"d={d} heads={heads} rows={n_rows} encoders={n_enc} {wtype} frames={a_ctx}")
+    if split:
+        monkeypatch.setenv("W4H_WIDE_FUSE", "0")
+    say(f"d={d} heads={heads} rows={n_rows} encoders={n_enc} {wtype} frames={a_ctx} split-K={split}")
     T = synth.make_decoder(dims, seed=41, wtype=wtype, ln_random=True)
     xas = [synth.encoder_output(dims, 41, stream=e) for e in range(n_enc)]
     n_forced = 10

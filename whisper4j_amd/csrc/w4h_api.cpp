@@ -462,6 +462,7 @@ struct w4h_session {
   WideGraph wgraph, wgraph_beam;
   DevBuf wbeam, wbsup;
   bool use_graph = true;
+  bool no_fuse = false;  // whole-K GEMM step switched off (W4H_WIDE_FUSE=0)
   // device-sampled decodes (T > 0): sampler state, the step's logits rows, the static suppress mask
   DevBuf samp, samp_row, samp_sup;
   // cancellation (w4h_session_cancel, callable from any thread): the host flag, and the device cancel
@@ -557,6 +558,7 @@ static WideParams wide_params(w4h_session* s) {
   p.next_tok = s->wnext.as<int32_t>();
   p.ctl = s->wctl.as<WideCtl>();
   p.graph = s->use_graph ? &s->wgraph : nullptr;
+  p.no_fuse = s->no_fuse ? 1 : 0;
   p.nch = s->nch;
   p.chlen = s->chlen;
   p.nsel = s->nsel;
@@ -833,6 +835,9 @@ int create_wide(std::unique_ptr<w4h_session>& s, const hipDeviceProp_t& prop, w4
   HIPCHK(wide_prepare(s->Rp, m->wq8));
   // One step is captured as a HIP graph and replayed per step; W4H_GRAPH=0 launches every kernel.
   if (const char* e = getenv("W4H_GRAPH")) s->use_graph = atoi(e) != 0;
+  // Sessions of at most 16 rows run whole-K GEMMs with the residual, LayerNorm and GELU steps
+  // inside them; W4H_WIDE_FUSE=0 keeps the split-K GEMMs and separate kernels.
+  if (const char* e = getenv("W4H_WIDE_FUSE")) s->no_fuse = atoi(e) == 0;
   if ((rc = s->mask.alloc(sizeof(uint32_t) * (size_t)s->S * s->mw))) return rc;
   if ((rc = s->bias.alloc(sizeof(float) * (size_t)V))) return rc;
   // sampled-decode state, allocated up front: w4h_session_cancel writes its stop word from any thread

@@ -231,6 +231,7 @@ struct WideParams {
   float* logits_out;        // [nsteps][S][V] or null
   const float* bias;        // [V] fixed logit bias (session buffer, always present)
   int bias_on;
+  int no_fuse;              // split-K GEMMs even where the whole-K step applies
 };
 
 // Enqueue p.nsteps wide steps on st.
@@ -240,6 +241,9 @@ hipError_t wide_prepare(int Rp, int wq8);
 void wide_graph_release(WideGraph* g);
 // Slicing of one wide GEMM for a device with n_cu compute units.
 WideGemm wide_plan(const void* w, const uint16_t* ws, int N, int K, int n_cu);
+// Whether a step of Rp padded rows at width d runs whole-K GEMMs (residual, LayerNorm and GELU
+// inside them) rather than split-K GEMMs and separate kernels.
+bool wide_fused_ok(int d, int Rp);
 
 // Launchers (return the HIP error of the launch).
 hipError_t launch_step(const StepParams& p, int grid, size_t lds_bytes, hipStream_t st);

@@ -198,9 +198,10 @@ __global__ __launch_bounds__(256) void k_w_gemm(GemmArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Residual update + LayerNorm, one workgroup per row.  EMB: x = token embedding + positional row
-// (layer 0).  Otherwise x += bias + the slices of the last GEMM (out-projection, cross-out or MLP2).
-// Then act[row] = LN(x[row]), two passes, eps 1e-5, as nn/LayerNorm.java:5-31.
+// Residual update + LayerNorm, one workgroup per row.  EMB = 1: x = token embedding + positional
+// row (layer 0).  EMB = 2: x as it is (the whole-K GEMMs updated it).  EMB = 0: x += bias + the
+// slices of the last GEMM (out-projection, cross-out or MLP2).  Then act[row] = LN(x[row]), two
+// passes, eps 1e-5, as nn/LayerNorm.java:5-31.
 
 constexpr int kWideVec = 8;  // d <= 8 * 256
 
@@ -218,7 +219,7 @@ __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl
   const int stopped = ctl->stop;  // ended beam search: read with the other loads, checked before storing
   const int s = blockIdx.x, tid = threadIdx.x;
   float v[NV];
-  if (EMB) {
+  if (EMB == 1) {
     // token of this step: the run's first tokens, the forced row, or the last step's argmax;
     // positional row clamped as the reference
     const int i0 = ctl->i, t = ctl->kv_len0 + i0;
@@ -234,6 +235,13 @@ __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl
       else e = (float)static_cast<const int8_t*>(emb)[(size_t)tk * d + j] * h2f(emb_s[(size_t)tk * (d >> 5) + (j >> 5)]);
       const float pv = pos[(size_t)pe * d + j];
       v[i] = tid + 256 * i < d ? e + pv : 0.f;
+    }
+  } else if (EMB == 2) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int j = min(tid + 256 * i, d - 1);
+      const float xr = x[(size_t)s * d + j];
+      v[i] = tid + 256 * i < d ? xr : 0.f;
     }
   } else {
     float xr[NV], bs[NV];
@@ -265,9 +273,10 @@ __global__ __launch_bounds__(256) void k_w_resid(const WideCtl* __restrict__ ctl
     for (int i = 0; i < NV; ++i) v[i] = tid + 256 * i < d ? xr[i] + (bs[i] + acc[i]) : 0.f;
   }
   if (stopped) return;
+  if (EMB != 2)
 #pragma unroll
-  for (int i = 0; i < NV; ++i)
-    if (tid + 256 * i < d) x[(size_t)s * d + tid + 256 * i] = v[i];
+    for (int i = 0; i < NV; ++i)
+      if (tid + 256 * i < d) x[(size_t)s * d + tid + 256 * i] = v[i];
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) sum += v[i];
@@ -299,6 +308,179 @@ __global__ __launch_bounds__(256) void k_w_gelu(const WideCtl* __restrict__ ctl,
   const int r = i / n, k = i - r * n;
   const float v = gelu_f16(bias[k] + slice_sum<kWideMaxSlices>(P, ks, ss, (size_t)r * n + k));
   if (!stopped) act[(size_t)r * lda + k] = v;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Whole-K GEMM for sessions of at most 16 rows (one MFMA row tile).  A workgroup owns 16 output
+// columns and all of K, split over its W waves (KS MFMA steps of 32 k per wave), so it ends with
+// finished sums and applies the step that consumes them itself; no split-K partials, and no
+// separate residual+LayerNorm or GELU kernel:
+//   PRO = kProLn   input rows are the residual stream x; the workgroup forms each row's LayerNorm
+//                  (two passes, eps 1e-5, nn/LayerNorm.java:5-31) from the fragments its waves hold,
+//                  which cover every element of every row, and normalises them before the MFMA.
+//   PRO = kProRaw  input rows enter as they are (attention outputs, MLP hidden rows).
+//   EPI = kFEpiRaw    out[r][n] = sum (the attention kernels add the bias as they read q, k, v)
+//   EPI = kFEpiResid  out[r][n] = out[r][n] + (bias[n] + sum)   (the residual update of x)
+//   EPI = kFEpiGelu   out[r][n] = GELU(bias[n] + sum)            (MLP hidden row, f16 table value)
+// Every lane loads its A fragments (row lane % 16, 8 consecutive k per step) from memory straight
+// into registers, then its weight fragments: one memory round trip, the activation loads first so
+// that the statistics wait only for them.  Lanes of padding rows (>= S) load through a buffer
+// descriptor at an offset past its end, which returns zeros without touching memory.  The LayerNorm
+// gain and bias pass through LDS (one copy per workgroup).  The waves' sums are added in wave
+// order through LDS, and wave j applies the epilogue to component j of every lane's 4 rows.
+
+enum { kProRaw = 0, kProLn = 1 };
+enum { kFEpiRaw = 0, kFEpiResid = 1, kFEpiGelu = 2 };
+
+struct FusedArgs {
+  const void* w;          // [N][K] f16, or int8 with f16 scales [N][K/32] in ws
+  const uint16_t* ws;
+  int N, K;
+  const float* in;        // [S][lda] input rows
+  int lda, S;
+  const float *g, *b;     // LayerNorm gain and bias [K] (kProLn)
+  const float* bias;      // [N] (kFEpiResid, kFEpiGelu)
+  float* out;             // [S][ldo]
+  int ldo;
+  const WideCtl* ctl;     // a stopped run (ended beam search) stores nothing
+};
+
+template <int WQ8, int W, int KS, int PRO, int EPI>
+__global__ __launch_bounds__(64 * W) void k_w_fgemm(FusedArgs a) {
+  static_assert(W >= 4, "the epilogue takes one row component per wave");
+  constexpr int KL = PRO == kProLn ? W * KS * 32 : 4;  // LayerNorm gain / bias entries in LDS
+  __shared__ float s_st[2][W][16];
+  __shared__ __attribute__((aligned(16))) float s_g[KL], s_b[KL];
+  __shared__ floatx4 s_acc[W][64];
+  const int stopped = a.ctl->stop;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g4 = lane >> 4, c16 = lane & 15;
+  const int n = blockIdx.x * 16 + c16;
+  const int kw0 = wv * KS * 32 + 8 * g4;  // the lane's first k
+  const int S = a.S;
+  const bool live = c16 < S;
+
+  // 1. loads: A fragments, then weights, then the LayerNorm gain / bias (into LDS) and the
+  //    epilogue's bias and residual values
+  const __amdgpu_buffer_rsrc_t rin = brsrc(a.in, ((size_t)(S - 1) * a.lda + a.K) * sizeof(float));
+  const uint32_t aoff = live ? (uint32_t)(((size_t)c16 * a.lda + kw0) * sizeof(float)) : kOOB;
+  u32x4 av[KS][2];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    av[s][0] = __builtin_amdgcn_raw_buffer_load_b128(rin, (int)(aoff + 128 * s), 0, 0);
+    av[s][1] = __builtin_amdgcn_raw_buffer_load_b128(rin, (int)(aoff + 128 * s + 16), 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  uint4 bf[KS];
+  uint2 bq[KS];
+  float sc[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const int k = kw0 + 32 * s;
+    if (!WQ8) {
+      bf[s] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.w) + (size_t)n * a.K + k);
+    } else {
+      bq[s] = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(a.w) + (size_t)n * a.K + k);
+      sc[s] = h2f(a.ws[(size_t)n * (a.K >> 5) + (k >> 5)]);
+    }
+  }
+  if constexpr (PRO == kProLn) {
+    for (int i = tid; i < KL / 4; i += 64 * W) {
+      reinterpret_cast<float4*>(s_g)[i] = reinterpret_cast<const float4*>(a.g)[i];
+      reinterpret_cast<float4*>(s_b)[i] = reinterpret_cast<const float4*>(a.b)[i];
+    }
+  }
+  const int er = 4 * g4 + (wv & 3);  // epilogue row of this lane (waves 0-3)
+  float bb = 0.f, xo = 0.f;
+  if constexpr (EPI != kFEpiRaw) bb = a.bias[n];
+  if constexpr (EPI == kFEpiResid) {
+    if (wv < 4) xo = a.out[(size_t)min(er, S - 1) * a.ldo + n];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  float v[KS][8];
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[s][4 * h + e] = __uint_as_float(av[s][h][e]);
+
+  // 2. LayerNorm of the fragments: row sums over the lane's values, the 4 lanes of the row in the
+  //    wave, then the waves in wave order
+  if constexpr (PRO == kProLn) {
+    float s1 = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s1 += v[s][e];
+    s1 += __shfl_xor(s1, 16);
+    s1 += __shfl_xor(s1, 32);
+    if (lane < 16) s_st[0][wv][lane] = s1;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) tot += s_st[0][w][c16];
+    const float mean = tot / (float)a.K;
+    float s2 = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s2 = fmaf(v[s][e] - mean, v[s][e] - mean, s2);
+    s2 += __shfl_xor(s2, 16);
+    s2 += __shfl_xor(s2, 32);
+    if (lane < 16) s_st[1][wv][lane] = s2;
+    __syncthreads();
+    float tq = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) tq += s_st[1][w][c16];
+    const float inv = 1.0f / sqrtf(tq / (float)a.K + 1e-5f);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int k = kw0 + 32 * s;
+      const float4 g0 = *reinterpret_cast<const float4*>(&s_g[k]), g1 = *reinterpret_cast<const float4*>(&s_g[k + 4]);
+      const float4 b0 = *reinterpret_cast<const float4*>(&s_b[k]), b1 = *reinterpret_cast<const float4*>(&s_b[k + 4]);
+      const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+      const float be[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[s][e] = live ? (v[s][e] - mean) * inv * gg[e] + be[e] : 0.f;
+    }
+  }
+
+  // 3. MFMA over the wave's k range, each step as (hi, lo) f16 parts against one weight fragment
+  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    half8 ah, al;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ah[e] = (_Float16)v[s][e];
+      al[e] = (_Float16)(v[s][e] - (float)ah[e]);
+    }
+    const half8 B = WQ8 ? i8x8_to_h8(bq[s]) : as_half8(bf[s]);
+    if (!WQ8) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, B, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, B, acc, 0, 0, 0);
+    } else {
+      floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, B, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, B, t, 0, 0, 0);
+      acc += t * sc[s];
+    }
+  }
+
+  // 4. waves' sums in wave order; wave j (< 4) finishes component j of every lane: row
+  //    4 (lane / 16) + j, column n
+  s_acc[wv][lane] = acc;
+  __syncthreads();
+  if (wv >= 4 || stopped || er >= S) return;
+  const float* sa = reinterpret_cast<const float*>(&s_acc[0][0]);
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < W; ++w) t += sa[(w * 64 + lane) * 4 + wv];
+  float o;
+  if constexpr (EPI == kFEpiRaw) o = t;
+  else if constexpr (EPI == kFEpiResid) o = xo + (bb + t);
+  else o = gelu_f16(bb + t);
+  a.out[(size_t)er * a.ldo + n] = o;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1016,12 +1198,15 @@ static hipError_t gemm(const WideParams& p, const WideGemm& g, const void* w, co
 static size_t sstride(const WideParams& p, const WideGemm& g) { return (size_t)p.Rp * g.N; }
 
 template <int WQ8, int NV>
-static hipError_t resid_nv(const WideParams& p, bool emb, int ks, size_t ss, const float* bias, const float* lg, const float* lb,
+static hipError_t resid_nv(const WideParams& p, int mode, int ks, size_t ss, const float* bias, const float* lg, const float* lb,
                            hipStream_t st) {
   const int lda = 4 * p.d;
   const dim3 grid(p.S), blk(256);
-  if (emb)
+  if (mode == 1)
     hipLaunchKernelGGL((k_w_resid<WQ8, 1, NV>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos,
+                       p.part, ks, ss, bias, p.x, p.d, lg, lb, p.act, lda);
+  else if (mode == 2)
+    hipLaunchKernelGGL((k_w_resid<WQ8, 2, NV>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos,
                        p.part, ks, ss, bias, p.x, p.d, lg, lb, p.act, lda);
   else
     hipLaunchKernelGGL((k_w_resid<WQ8, 0, NV>), grid, blk, 0, st, p.ctl, p.tokens0, p.forced, p.next_tok, p.S, p.C, p.emb, p.emb_s, p.pos,
@@ -1030,15 +1215,15 @@ static hipError_t resid_nv(const WideParams& p, bool emb, int ks, size_t ss, con
 }
 
 template <int WQ8>
-static hipError_t resid_wq(const WideParams& p, bool emb, int ks, size_t ss, const float* bias, const float* lg, const float* lb,
+static hipError_t resid_wq(const WideParams& p, int mode, int ks, size_t ss, const float* bias, const float* lg, const float* lb,
                            hipStream_t st) {
   switch ((p.d + 255) / 256) {
     case 1:
-    case 2: return resid_nv<WQ8, 2>(p, emb, ks, ss, bias, lg, lb, st);
-    case 3: return resid_nv<WQ8, 3>(p, emb, ks, ss, bias, lg, lb, st);
-    case 4: return resid_nv<WQ8, 4>(p, emb, ks, ss, bias, lg, lb, st);
-    case 5: return resid_nv<WQ8, 5>(p, emb, ks, ss, bias, lg, lb, st);
-    default: return resid_nv<WQ8, kWideVec>(p, emb, ks, ss, bias, lg, lb, st);
+    case 2: return resid_nv<WQ8, 2>(p, mode, ks, ss, bias, lg, lb, st);
+    case 3: return resid_nv<WQ8, 3>(p, mode, ks, ss, bias, lg, lb, st);
+    case 4: return resid_nv<WQ8, 4>(p, mode, ks, ss, bias, lg, lb, st);
+    case 5: return resid_nv<WQ8, 5>(p, mode, ks, ss, bias, lg, lb, st);
+    default: return resid_nv<WQ8, kWideVec>(p, mode, ks, ss, bias, lg, lb, st);
   }
 }
 
@@ -1047,7 +1232,70 @@ static hipError_t resid(const WideParams& p, const WideGemm* g_prev, const float
                         hipStream_t st) {
   const int ks = g_prev ? g_prev->ks : 0;
   const size_t ss = g_prev ? sstride(p, *g_prev) : 0;
-  return p.wq8 ? resid_wq<1>(p, !g_prev, ks, ss, bias, lg, lb, st) : resid_wq<0>(p, !g_prev, ks, ss, bias, lg, lb, st);
+  return p.wq8 ? resid_wq<1>(p, g_prev ? 0 : 1, ks, ss, bias, lg, lb, st) : resid_wq<0>(p, g_prev ? 0 : 1, ks, ss, bias, lg, lb, st);
+}
+
+// LayerNorm (lg, lb) of x as it is -> act.
+static hipError_t ln_only(const WideParams& p, const float* lg, const float* lb, hipStream_t st) {
+  return p.wq8 ? resid_wq<1>(p, 2, 0, 0, nullptr, lg, lb, st) : resid_wq<0>(p, 2, 0, 0, nullptr, lg, lb, st);
+}
+
+// Whole-K GEMMs (sessions of at most 16 rows).  Four waves over K = d (KS = d / 128 steps each),
+// eight over K = 4d (MLP2, KS = d / 64).
+bool wide_fused_ok(int d, int Rp) { return Rp == 16 && (d == 384 || d == 512 || d == 768 || d == 1024); }
+
+template <int WQ8, int W, int KS, int PRO, int EPI>
+static hipError_t fgemm_launch(const FusedArgs& a, hipStream_t st) {
+  if (a.K != W * KS * 32 || a.N % 16 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((k_w_fgemm<WQ8, W, KS, PRO, EPI>), dim3(a.N / 16), dim3(64 * W), 0, st, a);
+  return hipGetLastError();
+}
+
+template <int WQ8, int PRO, int EPI>
+static hipError_t fgemm_d(const FusedArgs& a, hipStream_t st) {
+  switch (a.K) {
+    case 384: return fgemm_launch<WQ8, 4, 3, PRO, EPI>(a, st);
+    case 512: return fgemm_launch<WQ8, 4, 4, PRO, EPI>(a, st);
+    case 768: return fgemm_launch<WQ8, 4, 6, PRO, EPI>(a, st);
+    case 1024: return fgemm_launch<WQ8, 4, 8, PRO, EPI>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int WQ8>
+static hipError_t fgemm_4d(const FusedArgs& a, hipStream_t st) {
+  switch (a.K) {
+    case 4 * 384: return fgemm_launch<WQ8, 8, 6, kProRaw, kFEpiResid>(a, st);
+    case 4 * 512: return fgemm_launch<WQ8, 8, 8, kProRaw, kFEpiResid>(a, st);
+    case 4 * 768: return fgemm_launch<WQ8, 8, 12, kProRaw, kFEpiResid>(a, st);
+    case 4 * 1024: return fgemm_launch<WQ8, 8, 16, kProRaw, kFEpiResid>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// One whole-K GEMM of the step: in rows [S][lda] (LayerNorm lg/lb first when given) times the
+// weights [N][K] -> out [S][ldo] through the epilogue.
+static hipError_t fgemm(const WideParams& p, const void* w, const uint16_t* ws, int N, int K, const float* in, int lda,
+                        const float* lg, const float* lb, int epi, const float* bias, float* out, int ldo, hipStream_t st) {
+  FusedArgs a{};
+  a.w = w;
+  a.ws = ws;
+  a.N = N;
+  a.K = K;
+  a.in = in;
+  a.lda = lda;
+  a.S = p.S;
+  a.g = lg;
+  a.b = lb;
+  a.bias = bias;
+  a.out = out;
+  a.ldo = ldo;
+  a.ctl = p.ctl;
+  if (K == 4 * p.d) return epi == kFEpiResid && !lg ? (p.wq8 ? fgemm_4d<1>(a, st) : fgemm_4d<0>(a, st)) : hipErrorInvalidValue;
+  if (lg && epi == kFEpiRaw) return p.wq8 ? fgemm_d<1, kProLn, kFEpiRaw>(a, st) : fgemm_d<0, kProLn, kFEpiRaw>(a, st);
+  if (lg && epi == kFEpiGelu) return p.wq8 ? fgemm_d<1, kProLn, kFEpiGelu>(a, st) : fgemm_d<0, kProLn, kFEpiGelu>(a, st);
+  if (!lg && epi == kFEpiResid) return p.wq8 ? fgemm_d<1, kProRaw, kFEpiResid>(a, st) : fgemm_d<0, kProRaw, kFEpiResid>(a, st);
+  return hipErrorInvalidValue;
 }
 
 #define WCHK(x)                          \
@@ -1071,44 +1319,30 @@ hipError_t wide_prepare(int Rp, int wq8) {
   return wq8 ? prepare_mt<2, 1>() : prepare_mt<2, 0>();
 }
 
-// The kernels of one step; every per-step value comes from the control block.
-static hipError_t enqueue_step(const WideParams& p, hipStream_t st) {
+// Cross-attention of layer l (chunk partials, then their merge when there is more than one chunk)
+// reading the query from q (ks slices of stride ss).
+static hipError_t cross(const WideParams& p, int l, const float* q, int ks, size_t ss, hipStream_t st) {
+  const LayerDev& lw = p.layers[l];
   const int d = p.d, H = p.H, lda = 4 * d;
   const int rg_rows = (p.X == p.S) ? 1 : 8;
   const int ngroups = (p.X == p.S) ? 1 : (p.S + 7) / 8;
   const size_t cross_lds = (size_t)rg_rows * p.chlen * sizeof(float);
-  const size_t self_lds = (size_t)(p.max_ctx + 1) * sizeof(float);
-  for (int l = 0; l < p.L; ++l) {
-    const LayerDev& lw = p.layers[l];
-    if (l == 0) WCHK(resid(p, nullptr, nullptr, lw.ln1_g, lw.ln1_b, st));
-    else WCHK(resid(p, &p.g_2, p.layers[l - 1].b_2, lw.ln1_g, lw.ln1_b, st));
-    WCHK(gemm(p, p.g_qkv, lw.w_qkv, lw.s_qkv, p.act, st));
-    hipLaunchKernelGGL(k_w_self, dim3(p.S, H), dim3(256), self_lds, st, p.ctl, p.part, p.g_qkv.ks, sstride(p, p.g_qkv), lw.b_qkv, d, H,
-                       l, p.S, p.max_ctx, p.kv_k, p.kv_v, p.slots, p.act, lda);
+  if (rg_rows == 1)
+    hipLaunchKernelGGL(k_w_cross<1>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.ctl, q, ks, ss,
+                       lw.b_cq, d, H, p.A, l, p.L, p.S, p.X, p.chlen, p.nch, p.xk, p.xv, p.cpart, p.act, lda);
+  else
+    hipLaunchKernelGGL(k_w_cross<8>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.ctl, q, ks, ss,
+                       lw.b_cq, d, H, p.A, l, p.L, p.S, p.X, p.chlen, p.nch, p.xk, p.xv, p.cpart, p.act, lda);
+  WCHK(hipGetLastError());
+  if (p.nch > 1) {
+    hipLaunchKernelGGL(k_w_cmerge, dim3(p.S, H), dim3(64), 0, st, p.ctl, p.cpart, H, p.nch, p.act, lda);
     WCHK(hipGetLastError());
-    WCHK(gemm(p, p.g_o, lw.w_o, lw.s_o, p.act, st));
-    WCHK(resid(p, &p.g_o, lw.b_o, lw.ln2_g, lw.ln2_b, st));
-    WCHK(gemm(p, p.g_cq, lw.w_cq, lw.s_cq, p.act, st));
-    if (rg_rows == 1)
-      hipLaunchKernelGGL(k_w_cross<1>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.ctl, p.part, p.g_cq.ks, sstride(p, p.g_cq),
-                         lw.b_cq, d, H, p.A, l, p.L, p.S, p.X, p.chlen, p.nch, p.xk, p.xv, p.cpart, p.act, lda);
-    else
-      hipLaunchKernelGGL(k_w_cross<8>, dim3(p.X, H, p.nch * ngroups), dim3(256), cross_lds, st, p.ctl, p.part, p.g_cq.ks, sstride(p, p.g_cq),
-                         lw.b_cq, d, H, p.A, l, p.L, p.S, p.X, p.chlen, p.nch, p.xk, p.xv, p.cpart, p.act, lda);
-    WCHK(hipGetLastError());
-    if (p.nch > 1) {
-      hipLaunchKernelGGL(k_w_cmerge, dim3(p.S, H), dim3(64), 0, st, p.ctl, p.cpart, H, p.nch, p.act, lda);
-      WCHK(hipGetLastError());
-    }
-    WCHK(gemm(p, p.g_co, lw.w_co, lw.s_co, p.act, st));
-    WCHK(resid(p, &p.g_co, lw.b_co, lw.ln3_g, lw.ln3_b, st));
-    WCHK(gemm(p, p.g_1, lw.w_1, lw.s_1, p.act, st));
-    hipLaunchKernelGGL(k_w_gelu, dim3((p.S * 4 * d + 255) / 256), dim3(256), 0, st, p.ctl, p.part, p.g_1.ks, sstride(p, p.g_1), lw.b_1, p.S,
-                       4 * d, p.hid, lda);
-    WCHK(hipGetLastError());
-    WCHK(gemm(p, p.g_2, lw.w_2, lw.s_2, p.hid, st));
   }
-  WCHK(resid(p, &p.g_2, p.layers[p.L - 1].b_2, p.lnf_g, p.lnf_b, st));
+  return hipSuccess;
+}
+
+// Logits GEMM, selection and (device beam search) the beam step, after the final LayerNorm.
+static hipError_t enqueue_head(const WideParams& p, hipStream_t st) {
   WCHK(gemm(p, p.g_v, p.emb, p.emb_s, p.act, st));
   const int nblk = (p.nsel + 3) / 4;
   hipLaunchKernelGGL(k_w_select, dim3(p.S, nblk), dim3(256), 0, st, p.ctl, p.part, p.g_v.ks, sstride(p, p.g_v), p.S, p.V, p.mask,
@@ -1122,6 +1356,60 @@ static hipError_t enqueue_step(const WideParams& p, hipStream_t st) {
                        p.beam_nsup, p.V, p.mw, const_cast<uint32_t*>(p.mask2), const_cast<int32_t*>(p.slots), p.max_ctx, p.next_tok);
     WCHK(hipGetLastError());
   }
+  return hipSuccess;
+}
+
+// The kernels of one step with whole-K GEMMs (at most 16 rows): 8 or 9 per layer, the residual
+// updates, LayerNorms and GELU inside the GEMMs.
+static hipError_t enqueue_step_fused(const WideParams& p, hipStream_t st) {
+  const int d = p.d, H = p.H, lda = 4 * d;
+  const size_t self_lds = (size_t)(p.max_ctx + 1) * sizeof(float);
+  WCHK(resid(p, nullptr, nullptr, p.layers[0].ln1_g, p.layers[0].ln1_b, st));  // x = embedding + position
+  for (int l = 0; l < p.L; ++l) {
+    const LayerDev& lw = p.layers[l];
+    WCHK(fgemm(p, lw.w_qkv, lw.s_qkv, 3 * d, d, p.x, d, lw.ln1_g, lw.ln1_b, kFEpiRaw, nullptr, p.part, 3 * d, st));
+    hipLaunchKernelGGL(k_w_self, dim3(p.S, H), dim3(256), self_lds, st, p.ctl, p.part, 1, (size_t)0, lw.b_qkv, d, H,
+                       l, p.S, p.max_ctx, p.kv_k, p.kv_v, p.slots, p.act, lda);
+    WCHK(hipGetLastError());
+    WCHK(fgemm(p, lw.w_o, lw.s_o, d, d, p.act, lda, nullptr, nullptr, kFEpiResid, lw.b_o, p.x, d, st));
+    WCHK(fgemm(p, lw.w_cq, lw.s_cq, d, d, p.x, d, lw.ln2_g, lw.ln2_b, kFEpiRaw, nullptr, p.part, d, st));
+    WCHK(cross(p, l, p.part, 1, 0, st));
+    WCHK(fgemm(p, lw.w_co, lw.s_co, d, d, p.act, lda, nullptr, nullptr, kFEpiResid, lw.b_co, p.x, d, st));
+    WCHK(fgemm(p, lw.w_1, lw.s_1, 4 * d, d, p.x, d, lw.ln3_g, lw.ln3_b, kFEpiGelu, lw.b_1, p.hid, lda, st));
+    WCHK(fgemm(p, lw.w_2, lw.s_2, d, 4 * d, p.hid, lda, nullptr, nullptr, kFEpiResid, lw.b_2, p.x, d, st));
+  }
+  WCHK(ln_only(p, p.lnf_g, p.lnf_b, st));
+  WCHK(enqueue_head(p, st));
+  return hipGetLastError();
+}
+
+// The kernels of one step; every per-step value comes from the control block.
+static hipError_t enqueue_step(const WideParams& p, hipStream_t st) {
+  if (wide_fused_ok(p.d, p.Rp) && !p.no_fuse) return enqueue_step_fused(p, st);
+  const int d = p.d, H = p.H, lda = 4 * d;
+  const size_t self_lds = (size_t)(p.max_ctx + 1) * sizeof(float);
+  for (int l = 0; l < p.L; ++l) {
+    const LayerDev& lw = p.layers[l];
+    if (l == 0) WCHK(resid(p, nullptr, nullptr, lw.ln1_g, lw.ln1_b, st));
+    else WCHK(resid(p, &p.g_2, p.layers[l - 1].b_2, lw.ln1_g, lw.ln1_b, st));
+    WCHK(gemm(p, p.g_qkv, lw.w_qkv, lw.s_qkv, p.act, st));
+    hipLaunchKernelGGL(k_w_self, dim3(p.S, H), dim3(256), self_lds, st, p.ctl, p.part, p.g_qkv.ks, sstride(p, p.g_qkv), lw.b_qkv, d, H,
+                       l, p.S, p.max_ctx, p.kv_k, p.kv_v, p.slots, p.act, lda);
+    WCHK(hipGetLastError());
+    WCHK(gemm(p, p.g_o, lw.w_o, lw.s_o, p.act, st));
+    WCHK(resid(p, &p.g_o, lw.b_o, lw.ln2_g, lw.ln2_b, st));
+    WCHK(gemm(p, p.g_cq, lw.w_cq, lw.s_cq, p.act, st));
+    WCHK(cross(p, l, p.part, p.g_cq.ks, sstride(p, p.g_cq), st));
+    WCHK(gemm(p, p.g_co, lw.w_co, lw.s_co, p.act, st));
+    WCHK(resid(p, &p.g_co, lw.b_co, lw.ln3_g, lw.ln3_b, st));
+    WCHK(gemm(p, p.g_1, lw.w_1, lw.s_1, p.act, st));
+    hipLaunchKernelGGL(k_w_gelu, dim3((p.S * 4 * d + 255) / 256), dim3(256), 0, st, p.ctl, p.part, p.g_1.ks, sstride(p, p.g_1), lw.b_1, p.S,
+                       4 * d, p.hid, lda);
+    WCHK(hipGetLastError());
+    WCHK(gemm(p, p.g_2, lw.w_2, lw.s_2, p.hid, st));
+  }
+  WCHK(resid(p, &p.g_2, p.layers[p.L - 1].b_2, p.lnf_g, p.lnf_b, st));
+  WCHK(enqueue_head(p, st));
   return hipGetLastError();
 }
 
