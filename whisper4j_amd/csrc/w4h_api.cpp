@@ -463,6 +463,8 @@ struct w4h_session {
   DevBuf wbeam, wbsup;
   bool use_graph = true;
   bool no_fuse = false;  // whole-K GEMM step switched off (W4H_WIDE_FUSE=0)
+  DevBuf xvt;            // V transposed [L][H][64][Ap] for the matrix-core cross-attention, or empty
+  int Ap = 0;
   // device-sampled decodes (T > 0): sampler state, the step's logits rows, the static suppress mask
   DevBuf samp, samp_row, samp_sup;
   // cancellation (w4h_session_cancel, callable from any thread): the host flag, and the device cancel
@@ -548,6 +550,8 @@ static WideParams wide_params(w4h_session* s) {
   p.kv_v = s->kvv.as<uint16_t>();
   p.xk = s->xk.as<uint16_t>();
   p.xv = s->xv.as<uint16_t>();
+  p.xvt = s->xvt.p ? s->xvt.as<uint16_t>() : nullptr;
+  p.Ap = s->Ap;
   p.slots = s->slots_identity ? nullptr : s->in_at<int32_t>(s->o_slots);
   p.x = s->wx.as<float>();
   p.act = s->wact.as<float>();
@@ -785,6 +789,12 @@ int create_wide(std::unique_ptr<w4h_session>& s, const hipDeviceProp_t& prop, w4
     return fail(W4H_ERR_INVALID, "batched engine needs n_text_state a multiple of %d (<= 2048) and head size %d", kWideKBlock, kHeadDim);
   const int ncu = prop.multiProcessorCount;
   s->Rp = s->S <= 16 ? 16 : 32;
+  // Sessions of at most 16 rows run whole-K GEMMs with the residual, LayerNorm and GELU steps
+  // inside them; W4H_WIDE_FUSE=0 keeps the split-K GEMMs and separate kernels.
+  if (const char* e = getenv("W4H_WIDE_FUSE")) s->no_fuse = atoi(e) == 0;
+  // With those, rows sharing one encoder output run cross-attention on the matrix cores (scores
+  // and values of up to 16 rows per key chunk as MFMA tiles), reading V transposed.
+  const bool xattn = !s->no_fuse && wide_fused_ok(d, s->Rp) && s->X == 1;
   s->g_qkv = wide_plan(nullptr, nullptr, 3 * d, d, ncu);
   s->g_o = wide_plan(nullptr, nullptr, d, d, ncu);
   s->g_cq = s->g_o;
@@ -799,12 +809,15 @@ int create_wide(std::unique_ptr<w4h_session>& s, const hipDeviceProp_t& prop, w4
   // no more than ceil(A / kWideKeysPerPass), the fewest that keep every chunk within one pass of the
   // kernel's key loop: more, shorter chunks only add partials to merge (small, 5 rows: 751 us per
   // step with 23 chunks of 66 keys, 731 with 12 of 125)
-  const int ngroups = s->X == s->S ? 1 : (s->S + 7) / 8;
+  const int ngroups = (s->X == s->S || xattn) ? 1 : (s->S + 7) / 8;
   int per_cu = 2;  // W4H_XWG overrides the cross-attention workgroups per compute unit (tuning)
   if (const char* e = getenv("W4H_XWG")) per_cu = std::max(1, std::min(16, atoi(e)));
   int nch = (per_cu * ncu + s->X * H * ngroups - 1) / (s->X * H * ngroups);
   nch = std::max(1, std::min(std::min(nch, (A + kWideKeysPerPass - 1) / kWideKeysPerPass), 64));  // k_w_cmerge: <= 64
+  if (xattn) nch = std::max(nch, (A + kXattnKeys - 1) / kXattnKeys);  // its chunks hold at most kXattnKeys keys
+  if (nch > 64) return fail(W4H_ERR_INVALID, "n_audio_ctx %d needs more than 64 cross-attention chunks", A);
   s->chlen = (A + nch - 1) / nch;
+  if (xattn) s->chlen = (s->chlen + 31) / 32 * 32;  // whole 32-key wave slices (<= kXattnKeys)
   s->nch = (A + s->chlen - 1) / s->chlen;
   s->nsel = (V + kWideSelChunk - 1) / kWideSelChunk;
   int rc;
@@ -817,6 +830,14 @@ int create_wide(std::unique_ptr<w4h_session>& s, const hipDeviceProp_t& prop, w4
   HIPCHK(hipStreamCreate(&s->stream));
   HIPCHK(hipMemsetAsync(s->xk.p, 0, x_elems * 2, s->stream));
   HIPCHK(hipMemsetAsync(s->xv.p, 0, x_elems * 2, s->stream));
+  if (xattn) {
+    // frames padded past the last 128-frame tile by one more chunk, all zero, so that a wave's
+    // 32-key slice of the last chunk reads inside the rows
+    s->Ap = (A + 127) / 128 * 128 + kXattnKeys;
+    const size_t t_elems = (size_t)L * H * kHeadDim * s->Ap;
+    if ((rc = s->xvt.alloc(t_elems * 2))) return rc;
+    HIPCHK(hipMemsetAsync(s->xvt.p, 0, t_elems * 2, s->stream));
+  }
   s->slots_host.resize((size_t)s->S * s->max_ctx);
   for (int r = 0; r < s->S; r++)
     for (int q = 0; q < s->max_ctx; q++) s->slots_host[(size_t)r * s->max_ctx + q] = r;
@@ -835,9 +856,6 @@ int create_wide(std::unique_ptr<w4h_session>& s, const hipDeviceProp_t& prop, w4
   HIPCHK(wide_prepare(s->Rp, m->wq8));
   // One step is captured as a HIP graph and replayed per step; W4H_GRAPH=0 launches every kernel.
   if (const char* e = getenv("W4H_GRAPH")) s->use_graph = atoi(e) != 0;
-  // Sessions of at most 16 rows run whole-K GEMMs with the residual, LayerNorm and GELU steps
-  // inside them; W4H_WIDE_FUSE=0 keeps the split-K GEMMs and separate kernels.
-  if (const char* e = getenv("W4H_WIDE_FUSE")) s->no_fuse = atoi(e) == 0;
   if ((rc = s->mask.alloc(sizeof(uint32_t) * (size_t)s->S * s->mw))) return rc;
   if ((rc = s->bias.alloc(sizeof(float) * (size_t)V))) return rc;
   // sampled-decode state, allocated up front: w4h_session_cancel writes its stop word from any thread
@@ -1018,8 +1036,10 @@ int w4h_session_cancel(w4h_session* s, int32_t on) {
 static int project_encoder(w4h_session* s, int32_t enc, const float* xa_dev) {
   const w4h_dims& D = s->m->dims;
   const size_t off = (size_t)enc * D.n_text_layer * D.n_text_head * D.n_audio_ctx * kHeadDim;
+  // the transposed V copy exists only for one shared encoder (enc 0)
   HIPCHK(launch_cross_kv(s->m->layers_dev.as<LayerDev>(), D.n_text_layer, D.n_text_state, D.n_text_head, D.n_audio_ctx,
-                         s->m->wq8, xa_dev, s->xk.as<uint16_t>() + off, s->xv.as<uint16_t>() + off, s->stream));
+                         s->m->wq8, xa_dev, s->xk.as<uint16_t>() + off, s->xv.as<uint16_t>() + off,
+                         s->xvt.p ? s->xvt.as<uint16_t>() : nullptr, s->Ap, s->stream));
   HIPCHK(hipStreamSynchronize(s->stream));
   return W4H_OK;
 }

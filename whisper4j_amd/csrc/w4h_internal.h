@@ -143,6 +143,7 @@ inline int step_rounds(int d, int wq8) { return wq8 ? 2 : (d <= 512 ? 2 : 3); }
 // GEMM over all rows.  Row counts are padded to Rp = 16 or 32 (one or two 16-row MFMA tiles).
 constexpr int kWideMaxRows = 32;
 constexpr int kWideKeysPerPass = 128;  // keys one pass of the batched cross-attention key loop covers
+constexpr int kXattnKeys = 128;        // keys per chunk of the matrix-core cross-attention (4 waves x 32)
 constexpr int kWideCols = 64;        // output columns per GEMM workgroup (16 per wave)
 constexpr int kWideKBlock = 128;     // k per block: four 16x16x32 MFMA steps
 constexpr int kWideSelChunk = 512;   // vocabulary entries per selection partial (one wave)
@@ -204,6 +205,8 @@ struct WideParams {
   int S, X, max_ctx, Rp;
   uint16_t *kv_k, *kv_v;    // [L][S][H][max_ctx][64]
   const uint16_t *xk, *xv;  // [X][L][H][A][64]
+  const uint16_t* xvt;      // [L][H][64][Ap] V transposed (one shared encoder, at most 16 rows) or null
+  int Ap;
   const int32_t* slots;     // [S][max_ctx] or null
   float* x;                 // [S][d] residual stream
   float* act;               // [Rp][4d] GEMM input rows: LN outputs, attention outputs
@@ -249,8 +252,9 @@ bool wide_fused_ok(int d, int Rp);
 hipError_t launch_step(const StepParams& p, int grid, size_t lds_bytes, hipStream_t st);
 size_t step_lds_bytes(const StepParams& p, int grid);
 int step_max_grid(size_t lds_bytes);
+// xvt (or null): V also transposed per (layer, head), [L][H][64][Ap], frames past A zero.
 hipError_t launch_cross_kv(const LayerDev* layers_host, int L, int d, int H, int A, int wq8, const float* xa,
-                           uint16_t* xk, uint16_t* xv, hipStream_t st);
+                           uint16_t* xk, uint16_t* xv, uint16_t* xvt, int Ap, hipStream_t st);
 hipError_t launch_fill_u64(u64* p, size_t n, hipStream_t st);
 
 // Standalone op launchers (device pointers).

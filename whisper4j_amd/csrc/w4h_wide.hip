@@ -39,6 +39,7 @@ struct GemmArgs {
 // values per lane, takes four at a time.
 template <int B>
 DEV float slice_sum(const float* p, int ks, size_t ss, size_t idx) {
+  if (ks == 1) return p[idx];  // whole-K GEMM output (uniform branch)
   float v = 0.f;
   for (int j = 0; j < ks; j += B) {
     float t[B];
@@ -324,8 +325,8 @@ __global__ __launch_bounds__(256) void k_w_gelu(const WideCtl* __restrict__ ctl,
 //   EPI = kFEpiGelu   out[r][n] = GELU(bias[n] + sum)            (MLP hidden row, f16 table value)
 // Every lane loads its A fragments (row lane % 16, 8 consecutive k per step) from memory straight
 // into registers, then its weight fragments: one memory round trip, the activation loads first so
-// that the statistics wait only for them.  Lanes of padding rows (>= S) load through a buffer
-// descriptor at an offset past its end, which returns zeros without touching memory.  The LayerNorm
+// that the statistics wait only for them.  Lanes of padding rows (>= S) load nothing (their
+// fragments are zero; the loads sit in a branch those lanes skip).  The LayerNorm
 // gain and bias pass through LDS (one copy per workgroup).  The waves' sums are added in wave
 // order through LDS, and wave j applies the epilogue to component j of every lane's 4 rows.
 
@@ -359,15 +360,31 @@ __global__ __launch_bounds__(64 * W) void k_w_fgemm(FusedArgs a) {
   const int S = a.S;
   const bool live = c16 < S;
 
-  // 1. loads: A fragments, then weights, then the LayerNorm gain / bias (into LDS) and the
-  //    epilogue's bias and residual values
-  const __amdgpu_buffer_rsrc_t rin = brsrc(a.in, ((size_t)(S - 1) * a.lda + a.K) * sizeof(float));
-  const uint32_t aoff = live ? (uint32_t)(((size_t)c16 * a.lda + kw0) * sizeof(float)) : kOOB;
-  u32x4 av[KS][2];
+  // 1. loads: LayerNorm gain / bias (bound for LDS), A fragments, weights, then the epilogue's
+  //    bias and residual values.  Every load is unconditional, so that each consumer waits only
+  //    for the loads issued before its own.
+  constexpr int NG = PRO == kProLn ? (KL / 4 + 64 * W - 1) / (64 * W) : 1;
+  float4 gq[NG], bq4[NG];
+  if constexpr (PRO == kProLn) {
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    av[s][0] = __builtin_amdgcn_raw_buffer_load_b128(rin, (int)(aoff + 128 * s), 0, 0);
-    av[s][1] = __builtin_amdgcn_raw_buffer_load_b128(rin, (int)(aoff + 128 * s + 16), 0, 0);
+    for (int j = 0; j < NG; ++j) {
+      const int i = min(tid + 64 * W * j, KL / 4 - 1);
+      gq[j] = reinterpret_cast<const float4*>(a.g)[i];
+      bq4[j] = reinterpret_cast<const float4*>(a.b)[i];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float4 av[KS][2];
+  if (live) {
+    const float* src = a.in + (size_t)c16 * a.lda + kw0;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      av[s][0] = *reinterpret_cast<const float4*>(src + 32 * s);
+      av[s][1] = *reinterpret_cast<const float4*>(src + 32 * s + 4);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) av[s][0] = av[s][1] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   __builtin_amdgcn_sched_barrier(0);
   uint4 bf[KS];
@@ -383,12 +400,6 @@ __global__ __launch_bounds__(64 * W) void k_w_fgemm(FusedArgs a) {
       sc[s] = h2f(a.ws[(size_t)n * (a.K >> 5) + (k >> 5)]);
     }
   }
-  if constexpr (PRO == kProLn) {
-    for (int i = tid; i < KL / 4; i += 64 * W) {
-      reinterpret_cast<float4*>(s_g)[i] = reinterpret_cast<const float4*>(a.g)[i];
-      reinterpret_cast<float4*>(s_b)[i] = reinterpret_cast<const float4*>(a.b)[i];
-    }
-  }
   const int er = 4 * g4 + (wv & 3);  // epilogue row of this lane (waves 0-3)
   float bb = 0.f, xo = 0.f;
   if constexpr (EPI != kFEpiRaw) bb = a.bias[n];
@@ -396,14 +407,24 @@ __global__ __launch_bounds__(64 * W) void k_w_fgemm(FusedArgs a) {
     if (wv < 4) xo = a.out[(size_t)min(er, S - 1) * a.ldo + n];
   }
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (PRO == kProLn) {
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      const int i = tid + 64 * W * j;
+      if (i < KL / 4) {
+        reinterpret_cast<float4*>(s_g)[i] = gq[j];
+        reinterpret_cast<float4*>(s_b)[i] = bq4[j];
+      }
+    }
+  }
 
   float v[KS][8];
 #pragma unroll
-  for (int s = 0; s < KS; ++s)
+  for (int s = 0; s < KS; ++s) {
+    const float t[8] = {av[s][0].x, av[s][0].y, av[s][0].z, av[s][0].w, av[s][1].x, av[s][1].y, av[s][1].z, av[s][1].w};
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[s][4 * h + e] = __uint_as_float(av[s][h][e]);
+    for (int e = 0; e < 8; ++e) v[s][e] = t[e];
+  }
 
   // 2. LayerNorm of the fragments: row sums over the lane's values, the 4 lanes of the row in the
   //    wave, then the waves in wave order
@@ -565,6 +586,7 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
   for (int e = 0; e < 8; ++e) qd[e] = q[dc * 8 + e];
 #pragma unroll
   for (int f = 0; f < kSelfKF; ++f) {
+    if (32 * f >= t) break;  // uniform: the first block's key groups that hold positions
     const int j = 32 * f + kg;
     const float dot = sum8(dot8h(qd, kr[f]));
     if (dc == 0 && j < t) sc[j] = dot * 0.125f;
@@ -610,6 +632,7 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
   for (int e = 0; e < 8; ++e) o[e] = 0.f;
 #pragma unroll
   for (int f = 0; f < kSelfKF; ++f) {
+    if (32 * f >= t) break;
     const int j = 32 * f + kg;
     axpy8h(j < t ? sc[j] : 0.f, vr[f], o);
   }
@@ -831,6 +854,145 @@ __global__ __launch_bounds__(64) void k_w_cmerge(const WideCtl* __restrict__ ctl
     for (int u = 0; u < 8; ++u) o = fmaf(__shfl(f, c0 + u), t[u], o);
   }
   if (!stopped) act[(size_t)s * lda + h * kHeadDim + k] = o / Lsum;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Cross-attention on the matrix cores for rows that share one encoder output (beam hypotheses; at
+// most 16 rows).  Workgroup (h, c): head h, key chunk c of at most kXattnKeys keys; wave w takes
+// 32 keys of it.  Scores are computed transposed, S^T = K . q^T (A = key rows, f16; B = the rows'
+// queries as (hi, lo) f16 parts), so a lane ends with 8 keys of one row: {g4 + [0, 4)} of each
+// 16-key tile (g4 = 4 (lane / 16)), row lane % 16.  After the chunk's row maximum (waves combined
+// through LDS) the probabilities stay in registers as the B operand of O^T = V^T . P^T, with the
+// keys of one 32-key MFMA step taken in that order; A = V^T rows (one head dimension over the same
+// keys) read from the transposed V copy.  The waves' O^T tiles are added through LDS.  Output:
+// the chunk partial (max, sum, acc[64]) per row for k_w_cmerge, or, with one chunk, the
+// normalised row straight into act.
+
+__global__ __launch_bounds__(256) void k_w_xattn(const WideCtl* __restrict__ ctl, const float* __restrict__ P, int ks, size_t ss,
+                                                 const float* __restrict__ bcq, int d, int H, int A, int Ap, int l, int S,
+                                                 int chlen, int nch, const uint16_t* __restrict__ xk,
+                                                 const uint16_t* __restrict__ xvt, float* __restrict__ cpart,
+                                                 float* __restrict__ act, int lda) {
+  __shared__ float s_m[4][16], s_l[4][16];
+  __shared__ floatx4 s_o[4][4][64];
+  const int stopped = ctl->stop;  // checked before the stores
+  const int h = blockIdx.x, c = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, g4 = 4 * g, c16 = lane & 15;
+  const int j0 = c * chlen, j1 = min(A, j0 + chlen);
+  const int kw = j0 + 32 * wv;  // the wave's first key
+  const uint16_t* kb = xk + ((size_t)l * H + h) * A * kHeadDim;
+  const uint16_t* vt = xvt + ((size_t)l * H + h) * kHeadDim * Ap;
+
+  // loads: key fragments (A of S^T: key kw + 16 t + c16, clamped to the last frame; dims
+  // 8 g + 32 q), V^T fragments (A of O^T: dim 16 nd + c16, keys kw + g4 + [0, 4) and
+  // kw + 16 + g4 + [0, 4); the copy is zero past A and long enough for every chunk's 128 keys),
+  // then the query of row c16 (bias + slices, dims 8 g + 32 q + [0, 8)) scaled by 1/8
+  uint4 kf[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      kf[t][q] = *reinterpret_cast<const uint4*>(kb + (size_t)min(kw + 16 * t + c16, A - 1) * kHeadDim + 8 * g + 32 * q);
+  uint2 vf[4][2];
+#pragma unroll
+  for (int nd = 0; nd < 4; ++nd)
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      vf[nd][u] = *reinterpret_cast<const uint2*>(vt + (size_t)(16 * nd + c16) * Ap + kw + 16 * u + g4);
+  const int row = min(c16, S - 1);
+  half8 qh[2], ql[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int col = h * kHeadDim + 8 * g + 32 * q;
+    float qv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[e] = bcq[col + e];
+    for (int z = 0; z < ks; ++z) {
+      const float4 a0 = *reinterpret_cast<const float4*>(P + z * ss + (size_t)row * d + col);
+      const float4 a1 = *reinterpret_cast<const float4*>(P + z * ss + (size_t)row * d + col + 4);
+      const float t8[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[e] += t8[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = c16 < S ? qv[e] * 0.125f : 0.f;
+      qh[q][e] = (_Float16)v;
+      ql[q][e] = (_Float16)(v - (float)qh[q][e]);
+    }
+  }
+
+  // S^T tiles: keys kw + 16 t + g4 + e of row c16
+  floatx4 sc[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    sc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const half8 K = as_half8(kf[t][q]);
+      sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(K, qh[q], sc[t], 0, 0, 0);
+      sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(K, ql[q], sc[t], 0, 0, 0);
+    }
+  }
+  // chunk maximum of row c16: the lane's 8 keys, lanes ^16 and ^32, then the waves
+  float mx = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (kw + 16 * t + g4 + e >= j1) sc[t][e] = -INFINITY;
+      mx = fmaxf(mx, sc[t][e]);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  if (lane < 16) s_m[wv][lane] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(s_m[0][c16], s_m[1][c16]), fmaxf(s_m[2][c16], s_m[3][c16]));
+  float ls = 0.f;
+  half8 ph, pl;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float pv = __expf(sc[t][e] - M);
+      ls += pv;
+      const _Float16 hi = (_Float16)pv;
+      ph[4 * t + e] = hi;
+      pl[4 * t + e] = (_Float16)(pv - (float)hi);
+    }
+  ls += __shfl_xor(ls, 16);
+  ls += __shfl_xor(ls, 32);
+  if (lane < 16) s_l[wv][lane] = ls;
+  // O^T tiles over the wave's 32 keys: dims 16 nd + g4 + e of row c16
+#pragma unroll
+  for (int nd = 0; nd < 4; ++nd) {
+    half8 V;
+    __builtin_memcpy(&V, &vf[nd][0], 8);
+    __builtin_memcpy(reinterpret_cast<char*>(&V) + 8, &vf[nd][1], 8);
+    floatx4 o = __builtin_amdgcn_mfma_f32_16x16x32_f16(V, ph, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    o = __builtin_amdgcn_mfma_f32_16x16x32_f16(V, pl, o, 0, 0, 0);
+    s_o[wv][nd][lane] = o;
+  }
+  __syncthreads();
+  // wave w adds dim tile w over the waves (wave order) and stores rows < S
+  if (stopped || c16 >= S) return;
+  const float L = (s_l[0][c16] + s_l[1][c16]) + (s_l[2][c16] + s_l[3][c16]);
+  floatx4 o = s_o[0][wv][lane];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) o += s_o[w][wv][lane];
+  const int dim = 16 * wv + g4;
+  if (nch == 1) {
+    const float inv = 1.f / L;
+    *reinterpret_cast<float4*>(act + (size_t)c16 * lda + h * kHeadDim + dim) = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+    return;
+  }
+  float* dst = cpart + (((size_t)c16 * H + h) * nch + c) * kPartWords;  // 8-byte aligned
+#pragma unroll
+  for (int e = 0; e < 4; ++e) dst[2 + dim + e] = o[e];
+  if (wv == 0 && g == 0) {
+    dst[0] = M;
+    dst[1] = L;
+  }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1241,7 +1403,7 @@ static hipError_t ln_only(const WideParams& p, const float* lg, const float* lb,
 }
 
 // Whole-K GEMMs (sessions of at most 16 rows).  Four waves over K = d (KS = d / 128 steps each),
-// eight over K = 4d (MLP2, KS = d / 64).
+// sixteen over K = 4d (MLP2, KS = d / 128).
 bool wide_fused_ok(int d, int Rp) { return Rp == 16 && (d == 384 || d == 512 || d == 768 || d == 1024); }
 
 template <int WQ8, int W, int KS, int PRO, int EPI>
@@ -1265,10 +1427,10 @@ static hipError_t fgemm_d(const FusedArgs& a, hipStream_t st) {
 template <int WQ8>
 static hipError_t fgemm_4d(const FusedArgs& a, hipStream_t st) {
   switch (a.K) {
-    case 4 * 384: return fgemm_launch<WQ8, 8, 6, kProRaw, kFEpiResid>(a, st);
-    case 4 * 512: return fgemm_launch<WQ8, 8, 8, kProRaw, kFEpiResid>(a, st);
-    case 4 * 768: return fgemm_launch<WQ8, 8, 12, kProRaw, kFEpiResid>(a, st);
-    case 4 * 1024: return fgemm_launch<WQ8, 8, 16, kProRaw, kFEpiResid>(a, st);
+    case 4 * 384: return fgemm_launch<WQ8, 16, 3, kProRaw, kFEpiResid>(a, st);
+    case 4 * 512: return fgemm_launch<WQ8, 16, 4, kProRaw, kFEpiResid>(a, st);
+    case 4 * 768: return fgemm_launch<WQ8, 16, 6, kProRaw, kFEpiResid>(a, st);
+    case 4 * 1024: return fgemm_launch<WQ8, 16, 8, kProRaw, kFEpiResid>(a, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1324,6 +1486,21 @@ hipError_t wide_prepare(int Rp, int wq8) {
 static hipError_t cross(const WideParams& p, int l, const float* q, int ks, size_t ss, hipStream_t st) {
   const LayerDev& lw = p.layers[l];
   const int d = p.d, H = p.H, lda = 4 * d;
+  if (p.xvt) {
+    // one shared encoder, one row tile, chunks of whole 32-key wave slices (8-byte aligned V^T
+    // reads) within the transposed copy's rows
+    if (p.X != 1 || p.S > 16 || p.chlen > kXattnKeys || p.chlen % 32 != 0 || (p.nch - 1) * p.chlen + kXattnKeys > p.Ap ||
+        p.Ap % 128 != 0)
+      return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_w_xattn, dim3(H, p.nch), dim3(256), 0, st, p.ctl, q, ks, ss, lw.b_cq, d, H, p.A, p.Ap, l, p.S,
+                       p.chlen, p.nch, p.xk, p.xvt, p.cpart, p.act, lda);
+    WCHK(hipGetLastError());
+    if (p.nch > 1) {
+      hipLaunchKernelGGL(k_w_cmerge, dim3(p.S, H), dim3(64), 0, st, p.ctl, p.cpart, H, p.nch, p.act, lda);
+      WCHK(hipGetLastError());
+    }
+    return hipSuccess;
+  }
   const int rg_rows = (p.X == p.S) ? 1 : 8;
   const int ngroups = (p.X == p.S) ? 1 : (p.S + 7) / 8;
   const size_t cross_lds = (size_t)rg_rows * p.chlen * sizeof(float);

@@ -10,6 +10,8 @@
 // values, one 32-element block per MFMA step, and the block's f16 scale multiplies that step's
 // fp32 result.  Each stage is loaded into registers while the previous one runs on the matrix
 // cores, then split into hi/lo and written to LDS; results leave through LDS as 16-byte rows.
+// Sessions whose rows share one encoder output also get V transposed, [layer][head][64][Ap]
+// (frames past A zero), the layout their matrix-core cross-attention reads.
 
 #include "w4h_mfma.h"
 
@@ -24,7 +26,7 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 template <int WQ8>
 __global__ __launch_bounds__(256) void k_cross_kv(const LayerDev* __restrict__ layers, int d, int H, int A,
                                                  const float* __restrict__ xa, uint16_t* __restrict__ xk,
-                                                 uint16_t* __restrict__ xv) {
+                                                 uint16_t* __restrict__ xv, uint16_t* __restrict__ xvt, int Ap) {
   __shared__ __attribute__((aligned(16))) _Float16 s_ah[kXkvBM * kXkvLd];
   __shared__ __attribute__((aligned(16))) _Float16 s_al[kXkvBM * kXkvLd];
   __shared__ __attribute__((aligned(16))) _Float16 s_b[64 * kXkvLd];
@@ -161,16 +163,36 @@ __global__ __launch_bounds__(256) void k_cross_kv(const LayerDev* __restrict__ l
       *reinterpret_cast<uint4*>(out + (size_t)(t0 + r) * kHeadDim + 8 * (c & 7)) =
           *reinterpret_cast<const uint4*>(&s_ah[r * kXkvLd + 8 * (c & 7)]);
   }
+  if (isv && xvt) {
+    // transposed: task c = (dim c >> 4, frames 8 (c & 15) + [0, 8)), one 16-byte row piece each
+    uint16_t* ot = xvt + ((size_t)l * H + h) * kHeadDim * Ap;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = j * 256 + tid;
+      const int dm = c >> 4, f0 = 8 * (c & 15);
+      uint16_t e[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const _Float16 v = s_ah[(f0 + q) * kXkvLd + dm];
+        e[q] = t0 + f0 + q < A ? __builtin_bit_cast(uint16_t, v) : (uint16_t)0;
+      }
+      *reinterpret_cast<uint4*>(ot + (size_t)dm * Ap + t0 + f0) =
+          make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16, e[4] | (uint32_t)e[5] << 16,
+                     e[6] | (uint32_t)e[7] << 16);
+    }
+  }
 }
 
 hipError_t launch_cross_kv(const LayerDev* layers_dev, int L, int d, int H, int A, int wq8, const float* xa,
-                           uint16_t* xk, uint16_t* xv, hipStream_t st) {
+                           uint16_t* xk, uint16_t* xv, uint16_t* xvt, int Ap, hipStream_t st) {
   if (d != H * kHeadDim || d % kXkvBK != 0 || A < 1 || L < 1) return hipErrorInvalidValue;
+  // every frame tile of the transposed copy lies inside its rows
+  if (xvt && (Ap % 8 != 0 || Ap < (A + kXkvBM - 1) / kXkvBM * kXkvBM)) return hipErrorInvalidValue;
   const dim3 grid((A + kXkvBM - 1) / kXkvBM, H, 2 * L);
   if (wq8)
-    hipLaunchKernelGGL(k_cross_kv<1>, grid, dim3(256), 0, st, layers_dev, d, H, A, xa, xk, xv);
+    hipLaunchKernelGGL(k_cross_kv<1>, grid, dim3(256), 0, st, layers_dev, d, H, A, xa, xk, xv, xvt, Ap);
   else
-    hipLaunchKernelGGL(k_cross_kv<0>, grid, dim3(256), 0, st, layers_dev, d, H, A, xa, xk, xv);
+    hipLaunchKernelGGL(k_cross_kv<0>, grid, dim3(256), 0, st, layers_dev, d, H, A, xa, xk, xv, xvt, Ap);
   return hipGetLastError();
 }
 
