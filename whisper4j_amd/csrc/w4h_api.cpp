@@ -435,6 +435,7 @@ struct w4h_session {
   size_t lds = 0;
   hipStream_t stream = nullptr;
   DevBuf kvk, kvv, xk, xv, ll, out, forced, mask, logits, xa_tmp, trace, bias;
+  DevBuf xa_hl;  // f16 (hi, lo) planes of an encoder output for the all-layer cross-K/V GEMM
   // Per-step inputs in one device area (error word, tokens, extra mask, slot table) filled by one
   // copy from its page-locked staging twin; forced rows and results are staged separately.
   DevBuf in;
@@ -1036,10 +1037,17 @@ int w4h_session_cancel(w4h_session* s, int32_t on) {
 static int project_encoder(w4h_session* s, int32_t enc, const float* xa_dev) {
   const w4h_dims& D = s->m->dims;
   const size_t off = (size_t)enc * D.n_text_layer * D.n_text_head * D.n_audio_ctx * kHeadDim;
+  const size_t sb = cross_kv_scratch_bytes(D.n_audio_ctx, D.n_text_state);
+  void* scratch = nullptr;
+  if (sb && !getenv("W4H_XKV_LAYERWISE")) {  // W4H_XKV_LAYERWISE: one GEMM per layer instead (comparison)
+    const int rc = ensure(s->xa_hl, sb);
+    if (rc) return rc;
+    scratch = s->xa_hl.p;
+  }
   // the transposed V copy exists only for one shared encoder (enc 0)
   HIPCHK(launch_cross_kv(s->m->layers_dev.as<LayerDev>(), D.n_text_layer, D.n_text_state, D.n_text_head, D.n_audio_ctx,
                          s->m->wq8, xa_dev, s->xk.as<uint16_t>() + off, s->xv.as<uint16_t>() + off,
-                         s->xvt.p ? s->xvt.as<uint16_t>() : nullptr, s->Ap, s->stream));
+                         s->xvt.p ? s->xvt.as<uint16_t>() : nullptr, s->Ap, scratch, s->stream));
   HIPCHK(hipStreamSynchronize(s->stream));
   return W4H_OK;
 }

@@ -253,8 +253,11 @@ hipError_t launch_step(const StepParams& p, int grid, size_t lds_bytes, hipStrea
 size_t step_lds_bytes(const StepParams& p, int grid);
 int step_max_grid(size_t lds_bytes);
 // xvt (or null): V also transposed per (layer, head), [L][H][64][Ap], frames past A zero.
+// scratch (or null): cross_kv_scratch_bytes(A, d) bytes of device memory for the f16 (hi, lo)
+// planes of xa; with it (and d a multiple of 128) all layers run as one GEMM.
 hipError_t launch_cross_kv(const LayerDev* layers_host, int L, int d, int H, int A, int wq8, const float* xa,
-                           uint16_t* xk, uint16_t* xv, uint16_t* xvt, int Ap, hipStream_t st);
+                           uint16_t* xk, uint16_t* xv, uint16_t* xvt, int Ap, void* scratch, hipStream_t st);
+size_t cross_kv_scratch_bytes(int A, int d);
 hipError_t launch_fill_u64(u64* p, size_t n, hipStream_t st);
 
 // Standalone op launchers (device pointers).
