@@ -453,8 +453,8 @@ def main():
                     help="timed oracle forwards per other workload for its CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the tiny/small/turbo/medium lines")
-    ap.add_argument("--only", choices=["turbo", "small-beam-rows", "greedy-driver", "sampled-driver", "medium", "tiny",
-                                       "encoder"],
+    ap.add_argument("--only", choices=["turbo", "small-beam-rows", "small-beam", "greedy-driver", "sampled-driver", "medium",
+                                       "tiny", "encoder"],
                     help="run only this other workload (one JSON line; for profiling it alone)")
     ap.add_argument("--only-steps", type=int, default=224, help="forced steps of the --only workload")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -483,6 +483,12 @@ def main():
         if args.only == "encoder":
             print(json.dumps({"workload": "audio encoder forward", **{k: measure_encoder(w4h, synth, k)
                                                                        for k in ("tiny.en", "base.en", "large-v3-turbo")}}))
+            return
+        if args.only == "small-beam":
+            sps, hps, us, steps, frac = measure_beam(w4h, synth, "small", n, 5)
+            print(json.dumps({"workload": f"small beam 5 through the library beam driver, {n} steps",
+                              "steps_per_s": round(sps, 1), "hypothesis_tokens_per_s": round(hps, 1), "us_per_step": round(us, 2),
+                              "steps": steps, "roofline_frac": round(frac, 4)}))
             return
         if args.only == "sampled-driver":
             drv = measure_sampled_driver(w4h, synth, "base.en", n)
