@@ -25,20 +25,26 @@ def say(*a):
 # encoder (two row groups of 8 and 2) and 4 rows with their own encoders.  Sessions of fewer than 5
 # rows at d < 768 would run on the persistent kernel, so the 4-row case sets W4H_ENGINE=wide.
 # Sessions of at most 16 rows at d in {384, 512, 768, 1024} run whole-K GEMMs with the residual,
-# LayerNorm and GELU inside them; split=True runs two of those cases on the split-K GEMMs and
-# separate kernels instead (W4H_WIDE_FUSE=0), which 20 and 32 rows and d = 1280 always use.
-@pytest.mark.parametrize("d,heads,n_rows,n_enc,wtype,a_ctx,split", [(384, 6, 12, 12, "f16", 80, False), (512, 8, 20, 20, "f16", 80, False),
-                                                                    (1280, 20, 32, 32, "f16", 80, False), (1024, 16, 16, 16, "q8_0", 80, False),
-                                                                    (768, 12, 10, 1, "f16", 80, False), (384, 6, 10, 1, "f16", 300, False),
-                                                                    (384, 6, 4, 4, "f16", 300, False), (768, 12, 10, 1, "f16", 80, True),
-                                                                    (1024, 16, 16, 16, "q8_0", 80, True)])
-def test_batched_streams_forced(gpu, orc, monkeypatch, d, heads, n_rows, n_enc, wtype, a_ctx, split):
+# LayerNorm and GELU inside them, and rows sharing one encoder there run the matrix-core
+# cross-attention on the transposed V copy.  mode "split" runs a case on the split-K GEMMs and
+# separate kernels instead (W4H_WIDE_FUSE=0), which 20 and 32 rows and d = 1280 always use; mode
+# "layerwise" projects the cross K/V (and the transposed V) with the per-layer kernel
+# (W4H_XKV_LAYERWISE=1) instead of the all-layer GEMM.
+@pytest.mark.parametrize("d,heads,n_rows,n_enc,wtype,a_ctx,mode", [(384, 6, 12, 12, "f16", 80, ""), (512, 8, 20, 20, "f16", 80, ""),
+                                                                   (1280, 20, 32, 32, "f16", 80, ""), (1024, 16, 16, 16, "q8_0", 80, ""),
+                                                                   (768, 12, 10, 1, "f16", 80, ""), (384, 6, 10, 1, "f16", 300, ""),
+                                                                   (384, 6, 4, 4, "f16", 300, ""), (512, 8, 6, 1, "f16", 300, ""),
+                                                                   (1024, 16, 5, 1, "q8_0", 300, ""), (768, 12, 10, 1, "f16", 80, "split"),
+                                                                   (1024, 16, 16, 16, "q8_0", 80, "split"), (512, 8, 6, 1, "f16", 300, "layerwise")])
+def test_batched_streams_forced(gpu, orc, monkeypatch, d, heads, n_rows, n_enc, wtype, a_ctx, mode):
     dims = synth.Dims(n_vocab=1200, n_text_ctx=48, n_text_state=d, n_text_head=heads, n_text_layer=2, n_audio_ctx=a_ctx)
     if n_rows < 5:
         monkeypatch.setenv("W4H_ENGINE", "wide")
-    if split:
+    if mode == "split":
         monkeypatch.setenv("W4H_WIDE_FUSE", "0")
-    say(f"d={d} heads={heads} rows={n_rows} encoders={n_enc} {wtype} frames={a_ctx} split-K={split}")
+    if mode == "layerwise":
+        monkeypatch.setenv("W4H_XKV_LAYERWISE", "1")
+    say(f"d={d} heads={heads} rows={n_rows} encoders={n_enc} {wtype} frames={a_ctx} {mode}")
     T = synth.make_decoder(dims, seed=41, wtype=wtype, ln_random=True)
     xas = [synth.encoder_output(dims, 41, stream=e) for e in range(n_enc)]
     n_forced = 10
