@@ -188,6 +188,188 @@ __global__ __launch_bounds__(256) void k_enc_gemm(EncGemm g) {
   }
 }
 
+// The per-layer GEMMs, with activation rows that their producers (LayerNorm, attention, the MLP1
+// epilogue) wrote as f16 (hi, lo) planes: no conversion in the GEMM, and BM x BN workgroup tiles
+// (4 waves of BM/2 x BN/2: BM/32 x BN/32 MFMA tiles each) staged through LDS, k in stages of 64, the next
+// stage in registers while the current one runs on the matrix cores.  Workgroups are ordered so
+// that an XCD takes a contiguous run of the column-major tile order: its weight tiles stay in its
+// L2 across the row blocks.  Two f16 products per (hi, lo) pair, fp32 accumulation; q8_0 weights
+// as exact int8 with the block scale per 32-k step.
+constexpr int kE2BK = 64;
+constexpr int kE2Ld = kE2BK + kPadH;
+
+template <int EPI, int WQ8, int BM, int BN>
+__global__ __launch_bounds__(256) void k_enc_gemm2(EncGemm2 g) {
+  constexpr int NT = BN / 32;  // MFMA column tiles per wave
+  constexpr int MT = BM / 32;  // MFMA row tiles per wave
+  __shared__ __attribute__((aligned(16))) _Float16 s_a[2 * BM * kE2Ld];  // hi plane, then lo plane
+  __shared__ __attribute__((aligned(16))) _Float16 s_b[BN * kE2Ld];
+  __shared__ float s_sc[BN][2];
+  _Float16* s_ah = s_a;
+  _Float16* s_al = s_a + BM * kE2Ld;
+  const int M = g.M, N = g.N, K = g.K;
+  const int Mt = (M + BM - 1) / BM, Nt = N / BN, total = Mt * Nt, per = (total + kXcds - 1) / kXcds;
+  const int T = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  if (T >= total) return;
+  const int m0 = (T % Mt) * BM, n0 = (T / Mt) * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, gq = lane >> 4, c16 = lane & 15;
+  const int wm = wv >> 1, wn = wv & 1;
+
+  // stage registers: A planes 128 x 64 halves (4 x 16 bytes per thread and plane: rows ar + 32 j,
+  // k ak); f16 weights BN x 64 (BN / 32 per thread, rows ar + 32 j); q8_0 BN x 64 bytes (BN / 64 per
+  // thread: rows qr + 64 j, k qk) and the scales of (row tid >> 1, block tid & 1), tid < 2 BN
+  const int ar = tid >> 3, ak = 8 * (tid & 7), qr = tid >> 2, qk = 16 * (tid & 3);
+  const _Float16* ahp = reinterpret_cast<const _Float16*>(g.ah) + (size_t)(m0 + ar) * g.lda + ak;
+  const _Float16* alp = reinterpret_cast<const _Float16*>(g.al) + (size_t)(m0 + ar) * g.lda + ak;
+  const size_t astep = (size_t)32 * g.lda;
+  uint4 a0_0, a1_0, a2_0, a3_0, l0_0, l1_0, l2_0, l3_0, b0_0, b1_0, b2_0, b3_0;
+  uint16_t rs_0 = 0;
+#define E2_LOAD(X, K0)                                                                                                \
+  do {                                                                                                              \
+    a0_##X = *reinterpret_cast<const uint4*>(ahp + (K0));                                                           \
+    a1_##X = *reinterpret_cast<const uint4*>(ahp + astep + (K0));                                                   \
+    if (BM == 128) {                                                                                                \
+      a2_##X = *reinterpret_cast<const uint4*>(ahp + 2 * astep + (K0));                                             \
+      a3_##X = *reinterpret_cast<const uint4*>(ahp + 3 * astep + (K0));                                             \
+    }                                                                                                               \
+    l0_##X = *reinterpret_cast<const uint4*>(alp + (K0));                                                           \
+    l1_##X = *reinterpret_cast<const uint4*>(alp + astep + (K0));                                                   \
+    if (BM == 128) {                                                                                                \
+      l2_##X = *reinterpret_cast<const uint4*>(alp + 2 * astep + (K0));                                             \
+      l3_##X = *reinterpret_cast<const uint4*>(alp + 3 * astep + (K0));                                             \
+    }                                                                                                               \
+    if (!WQ8) {                                                                                                     \
+      const uint16_t* wp = static_cast<const uint16_t*>(g.w) + (size_t)(n0 + ar) * K + ak + (K0);                    \
+      b0_##X = *reinterpret_cast<const uint4*>(wp);                                                                 \
+      b1_##X = *reinterpret_cast<const uint4*>(wp + (size_t)32 * K);                                                \
+      if (BN == 128) {                                                                                              \
+        b2_##X = *reinterpret_cast<const uint4*>(wp + (size_t)64 * K);                                              \
+        b3_##X = *reinterpret_cast<const uint4*>(wp + (size_t)96 * K);                                              \
+      }                                                                                                             \
+    } else {                                                                                                        \
+      const int8_t* wp = static_cast<const int8_t*>(g.w) + (size_t)(n0 + qr) * K + qk + (K0);                        \
+      b0_##X = *reinterpret_cast<const uint4*>(wp);                                                                 \
+      if (BN == 128) b1_##X = *reinterpret_cast<const uint4*>(wp + (size_t)64 * K);                                 \
+      if (tid < 2 * BN) rs_##X = g.ws[(size_t)(n0 + (tid >> 1)) * (K >> 5) + ((K0) >> 5) + (tid & 1)];              \
+    }                                                                                                               \
+  } while (0)
+  const int ao = ar * kE2Ld + ak, ls = 32 * kE2Ld;
+#define E2_STASH(X)                                                                                                   \
+  do {                                                                                                              \
+    *reinterpret_cast<uint4*>(&s_ah[ao]) = a0_##X;                                                                  \
+    *reinterpret_cast<uint4*>(&s_ah[ao + ls]) = a1_##X;                                                             \
+    if (BM == 128) {                                                                                                \
+      *reinterpret_cast<uint4*>(&s_ah[ao + 2 * ls]) = a2_##X;                                                       \
+      *reinterpret_cast<uint4*>(&s_ah[ao + 3 * ls]) = a3_##X;                                                       \
+    }                                                                                                               \
+    *reinterpret_cast<uint4*>(&s_al[ao]) = l0_##X;                                                                  \
+    *reinterpret_cast<uint4*>(&s_al[ao + ls]) = l1_##X;                                                             \
+    if (BM == 128) {                                                                                                \
+      *reinterpret_cast<uint4*>(&s_al[ao + 2 * ls]) = l2_##X;                                                       \
+      *reinterpret_cast<uint4*>(&s_al[ao + 3 * ls]) = l3_##X;                                                       \
+    }                                                                                                               \
+    if (!WQ8) {                                                                                                     \
+      *reinterpret_cast<uint4*>(&s_b[ao]) = b0_##X;                                                                 \
+      *reinterpret_cast<uint4*>(&s_b[ao + ls]) = b1_##X;                                                            \
+      if (BN == 128) {                                                                                              \
+        *reinterpret_cast<uint4*>(&s_b[ao + 2 * ls]) = b2_##X;                                                      \
+        *reinterpret_cast<uint4*>(&s_b[ao + 3 * ls]) = b3_##X;                                                      \
+      }                                                                                                             \
+    } else {                                                                                                        \
+      const int o = qr * kE2Ld + qk;                                                                                \
+      *reinterpret_cast<half8*>(&s_b[o]) = i8x8_to_h8(make_uint2(b0_##X.x, b0_##X.y));                              \
+      *reinterpret_cast<half8*>(&s_b[o + 8]) = i8x8_to_h8(make_uint2(b0_##X.z, b0_##X.w));                          \
+      if (BN == 128) {                                                                                              \
+        *reinterpret_cast<half8*>(&s_b[o + 64 * kE2Ld]) = i8x8_to_h8(make_uint2(b1_##X.x, b1_##X.y));               \
+        *reinterpret_cast<half8*>(&s_b[o + 64 * kE2Ld + 8]) = i8x8_to_h8(make_uint2(b1_##X.z, b1_##X.w));           \
+      }                                                                                                             \
+      if (tid < 2 * BN) s_sc[tid >> 1][tid & 1] = h2f(rs_##X);                                                      \
+    }                                                                                                               \
+  } while (0)
+
+  floatx4 acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&]() {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int kk = ks * 32 + 8 * gq;
+      half8 bfr[NT];
+      float sc[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int col = wn * (BN / 2) + j * 16 + c16;
+        bfr[j] = *reinterpret_cast<const half8*>(&s_b[col * kE2Ld + kk]);
+        sc[j] = WQ8 ? s_sc[col][ks] : 1.f;
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int r = wm * (BM / 2) + i * 16 + c16;
+        const half8 ah = *reinterpret_cast<const half8*>(&s_ah[r * kE2Ld + kk]);
+        const half8 al = *reinterpret_cast<const half8*>(&s_al[r * kE2Ld + kk]);
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          if (!WQ8) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bfr[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bfr[j], acc[i][j], 0, 0, 0);
+          } else {
+            floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bfr[j], floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bfr[j], t, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(sc[j], t[e], acc[i][j][e]);
+          }
+        }
+      }
+    }
+  };
+  // the next stage's loads are issued while the current one runs
+  E2_LOAD(0, 0);
+  for (int k0 = 0; k0 < K; k0 += kE2BK) {
+    lds_barrier();  // every wave has read the previous stage
+    E2_STASH(0);
+    lds_barrier();
+    if (k0 + kE2BK < K) E2_LOAD(0, k0 + kE2BK);
+    compute();
+  }
+#undef E2_LOAD
+#undef E2_STASH
+
+  // epilogue: lane holds rows wm * BM / 2 + 16 i + 4 gq + e of column wn * BN / 2 + 16 j + c16
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int n = n0 + wn * (BN / 2) + j * 16 + c16;
+    const float b = g.bias ? g.bias[n] : 0.f;
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + wm * (BM / 2) + 16 * i + 4 * gq + e;
+        if (m >= M) continue;
+        const float c = acc[i][j][e] + b;
+        if constexpr (EPI == kEpiResid) {
+          g.out[(size_t)m * g.ldo + n] += c;
+        } else if constexpr (EPI == kEpiGeluPlanes) {
+          const float v = gelu_f16(c);
+          const _Float16 hi = (_Float16)v;
+          reinterpret_cast<_Float16*>(g.oh)[(size_t)m * g.ldo + n] = hi;
+          reinterpret_cast<_Float16*>(g.ol)[(size_t)m * g.ldo + n] = (_Float16)(v - (float)hi);
+        } else {  // kEpiQkv
+          const int d = N / 3, part = n / d, h = (n - part * d) >> 6, ei = n & 63;
+          const float v = part == 0 ? c * 0.125f : c;
+          const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
+          const size_t plane = (size_t)(d >> 6) * g.Tp * kHeadDim;
+          const size_t idx = part == 2 ? ((size_t)h * kHeadDim + ei) * g.Tp + m : ((size_t)h * g.Tp + m) * kHeadDim + ei;
+          _Float16* q16 = reinterpret_cast<_Float16*>(g.qkv);
+          q16[(size_t)(part * 2) * plane + idx] = hi;
+          q16[(size_t)(part * 2 + 1) * plane + idx] = lo;
+        }
+      }
+  }
+}
+
 // Attention of every frame over every frame for one head (no mask), flash style: a workgroup owns
 // 64 query rows (16 per wave) and walks the keys in blocks of 64 (K and V staged in LDS, double
 // buffered), with an online softmax in fp32.  Products are taken transposed, S^T = K . Q^T and
@@ -200,7 +382,8 @@ __global__ __launch_bounds__(256) void k_enc_gemm(EncGemm g) {
 // out[t][h * 64 + e].
 constexpr int kAttBQ = 64, kAttBK = 64, kAttLd = 64 + kPadH;
 
-__global__ __launch_bounds__(256) void k_enc_attn(const _Float16* __restrict__ qkv, int T, int Tp, int H, float* __restrict__ out) {
+__global__ __launch_bounds__(256) void k_enc_attn(const _Float16* __restrict__ qkv, int T, int Tp, int H, _Float16* __restrict__ oh,
+                                                  _Float16* __restrict__ ol) {
   __shared__ __attribute__((aligned(16))) _Float16 s_k[2][2][kAttBK * kAttLd];    // [buffer][hi|lo][key][dim]
   __shared__ __attribute__((aligned(16))) _Float16 s_v[2][2][kHeadDim * kAttLd];  // [buffer][hi|lo][dim][key]
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g4 = 4 * (lane >> 4), c16 = lane & 15;
@@ -339,17 +522,26 @@ __global__ __launch_bounds__(256) void k_enc_attn(const _Float16* __restrict__ q
   const int t = q0 + wv * 16 + c16;
   if (t < T) {
     const float inv = 1.f / lrow;
-    float* dst = out + (size_t)t * H * kHeadDim + h * kHeadDim;
+    const size_t base = (size_t)t * H * kHeadDim + h * kHeadDim;
 #pragma unroll
-    for (int nd = 0; nd < 4; ++nd)
-      *reinterpret_cast<float4*>(dst + nd * 16 + g4) =
-          make_float4(o[nd][0] * inv, o[nd][1] * inv, o[nd][2] * inv, o[nd][3] * inv);
+    for (int nd = 0; nd < 4; ++nd) {
+      half4 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = o[nd][e] * inv;
+        hi[e] = (_Float16)v;
+        lo[e] = (_Float16)(v - (float)hi[e]);
+      }
+      *reinterpret_cast<half4*>(oh + base + nd * 16 + g4) = hi;
+      *reinterpret_cast<half4*>(ol + base + nd * 16 + g4) = lo;
+    }
   }
 }
 
 // LayerNorm of rows of n (eps 1e-5), one wave per row, two passes in fp32 (main/tensor/Tensor.java:592-619).
 __global__ __launch_bounds__(256) void k_enc_ln(const float* __restrict__ x, int rows, int n, const float* __restrict__ gam,
-                                                const float* __restrict__ bet, float* __restrict__ y) {
+                                                const float* __restrict__ bet, float* __restrict__ y, _Float16* __restrict__ yh,
+                                                _Float16* __restrict__ yl) {
   const int lane = threadIdx.x & 63, r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
   const float* xr = x + (size_t)r * n;
@@ -375,7 +567,15 @@ __global__ __launch_bounds__(256) void k_enc_ln(const float* __restrict__ x, int
 #pragma unroll
   for (int i = 0; i < kEncLnPer; ++i) {
     const int j = lane + 64 * i;
-    if (j < n) y[(size_t)r * n + j] = (v[i] - mean) * inv * gam[j] + bet[j];
+    if (j >= n) continue;
+    const float o = (v[i] - mean) * inv * gam[j] + bet[j];
+    if (y) {
+      y[(size_t)r * n + j] = o;
+    } else {
+      const _Float16 hi = (_Float16)o;
+      yh[(size_t)r * n + j] = hi;
+      yl[(size_t)r * n + j] = (_Float16)(o - (float)hi);
+    }
   }
 }
 
@@ -411,16 +611,55 @@ hipError_t launch_enc_gemm(int epi, const EncGemm& g, hipStream_t st) {
   }
 }
 
-hipError_t launch_enc_attn(const uint16_t* qkv, int T, int Tp, int H, float* out, hipStream_t st) {
-  if (T < 1 || Tp < T || Tp % kEncPad) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_enc_attn, dim3((T + kAttBQ - 1) / kAttBQ, H), dim3(256), 0, st,
-                     reinterpret_cast<const _Float16*>(qkv), T, Tp, H, out);
+template <int EPI, int BM, int BN>
+static hipError_t gemm2_t(const EncGemm2& g, hipStream_t st) {
+  const int total = ((g.M + BM - 1) / BM) * (g.N / BN);
+  const dim3 grid(((total + kXcds - 1) / kXcds) * kXcds);
+  if (g.ws)
+    hipLaunchKernelGGL((k_enc_gemm2<EPI, 1, BM, BN>), grid, dim3(256), 0, st, g);
+  else
+    hipLaunchKernelGGL((k_enc_gemm2<EPI, 0, BM, BN>), grid, dim3(256), 0, st, g);
   return hipGetLastError();
 }
 
-hipError_t launch_enc_ln(const float* x, int rows, int n, const float* g, const float* b, float* y, hipStream_t st) {
-  if (n > 64 * kEncLnPer) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_enc_ln, dim3((rows + 3) / 4), dim3(256), 0, st, x, rows, n, g, b, y);
+// Workgroup tile: the largest of 128 x 128, 128 x 64 and 64 x 64 that gives at least min_wg
+// workgroups (default 512, two per compute unit), else 64 x 64.  W4H_ENC_MINWG overrides it.
+template <int EPI>
+static hipError_t gemm2_bn(const EncGemm2& g, hipStream_t st) {
+  static const int min_wg = [] {
+    const char* e = getenv("W4H_ENC_MINWG");
+    return e ? atoi(e) : 512;
+  }();
+  const int m128 = (g.M + 127) / 128, m64 = (g.M + 63) / 64;
+  if (g.N % 128 == 0 && m128 * (g.N / 128) >= min_wg) return gemm2_t<EPI, 128, 128>(g, st);
+  if (m128 * (g.N / 64) >= min_wg) return gemm2_t<EPI, 128, 64>(g, st);
+  (void)m64;
+  return gemm2_t<EPI, 64, 64>(g, st);
+}
+
+hipError_t launch_enc_gemm2(int epi, const EncGemm2& g, hipStream_t st) {
+  if (g.M < 1 || g.N % 64 || g.K % kE2BK || g.lda % 8 || g.K > g.lda) return hipErrorInvalidValue;
+  if (epi == kEpiQkv && (g.N % 192 || g.Tp < g.M || g.Tp % kEncPad)) return hipErrorInvalidValue;
+  switch (epi) {
+    case kEpiResid: return gemm2_bn<kEpiResid>(g, st);
+    case kEpiQkv: return gemm2_bn<kEpiQkv>(g, st);
+    case kEpiGeluPlanes: return gemm2_bn<kEpiGeluPlanes>(g, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_enc_attn(const uint16_t* qkv, int T, int Tp, int H, uint16_t* oh, uint16_t* ol, hipStream_t st) {
+  if (T < 1 || Tp < T || Tp % kEncPad) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_enc_attn, dim3((T + kAttBQ - 1) / kAttBQ, H), dim3(256), 0, st,
+                     reinterpret_cast<const _Float16*>(qkv), T, Tp, H, reinterpret_cast<_Float16*>(oh), reinterpret_cast<_Float16*>(ol));
+  return hipGetLastError();
+}
+
+hipError_t launch_enc_ln(const float* x, int rows, int n, const float* g, const float* b, float* y, uint16_t* yh, uint16_t* yl,
+                         hipStream_t st) {
+  if (n > 64 * kEncLnPer || (!y && (!yh || !yl))) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_enc_ln, dim3((rows + 3) / 4), dim3(256), 0, st, x, rows, n, g, b, y, reinterpret_cast<_Float16*>(yh),
+                     reinterpret_cast<_Float16*>(yl));
   return hipGetLastError();
 }
 

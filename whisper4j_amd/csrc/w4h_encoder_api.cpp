@@ -58,7 +58,9 @@ struct w4h_encoder {
   const float *c1b = nullptr, *c2b = nullptr, *pos = nullptr, *lnp_g = nullptr, *lnp_b = nullptr;
   std::vector<EncLayer> layers;
   // working buffers
-  float *melt = nullptr, *x1p = nullptr, *x = nullptr, *xn = nullptr, *att = nullptr, *hid = nullptr;
+  float *melt = nullptr, *x1p = nullptr, *x = nullptr;
+  // (hi, lo) f16 planes of the layer GEMMs' activation rows, [Mp][n] (rows past T stay zero)
+  uint16_t *xnh = nullptr, *xnl = nullptr, *atth = nullptr, *attl = nullptr, *hidh = nullptr, *hidl = nullptr;
   float *mel_in = nullptr, *out = nullptr;  // staging for the host-memory entry point
   uint16_t* qkv = nullptr;
   int Tp = 0;
@@ -280,9 +282,10 @@ int build(w4h_encoder* e, const w4h_tensor* tensors, int n) {
   if (!(e->melt = static_cast<float*>(dev_alloc(e, (F + 2) * nm * 4, &rc)))) return rc;
   if (!(e->x1p = static_cast<float*>(dev_alloc(e, (F + 2) * d * 4, &rc)))) return rc;
   if (!(e->x = static_cast<float*>(dev_alloc(e, (size_t)T * d * 4, &rc)))) return rc;
-  if (!(e->xn = static_cast<float*>(dev_alloc(e, (size_t)T * d * 4, &rc)))) return rc;
-  if (!(e->att = static_cast<float*>(dev_alloc(e, (size_t)T * d * 4, &rc)))) return rc;
-  if (!(e->hid = static_cast<float*>(dev_alloc(e, (size_t)T * 4 * d * 4, &rc)))) return rc;
+  const size_t Mp = (size_t)(T + kEncRowTile - 1) / kEncRowTile * kEncRowTile;
+  uint16_t** planes[6] = {&e->xnh, &e->xnl, &e->atth, &e->attl, &e->hidh, &e->hidl};
+  for (int i = 0; i < 6; ++i)
+    if (!(*planes[i] = static_cast<uint16_t*>(dev_alloc(e, Mp * (i < 4 ? d : 4 * d) * 2, &rc)))) return rc;
   if (!(e->qkv = static_cast<uint16_t*>(dev_alloc(e, (size_t)6 * e->Tp * d * 2, &rc)))) return rc;
   if (!(e->mel_in = static_cast<float*>(dev_alloc(e, F * nm * 4, &rc)))) return rc;
   if (!(e->out = static_cast<float*>(dev_alloc(e, (size_t)T * d * 4, &rc)))) return rc;
@@ -310,6 +313,28 @@ int gemm(int epi, const float* a, int lda, int M, int N, int K, const void* w, c
   return W4H_OK;
 }
 
+int gemm2(int epi, const uint16_t* ah, const uint16_t* al, int lda, int M, int N, int K, const void* w, const uint16_t* ws,
+          const float* bias, float* out, uint16_t* oh, uint16_t* ol, int ldo, uint16_t* qkv, int Tp, hipStream_t st) {
+  EncGemm2 g{};
+  g.ah = ah;
+  g.al = al;
+  g.lda = lda;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.w = w;
+  g.ws = ws;
+  g.bias = bias;
+  g.out = out;
+  g.oh = oh;
+  g.ol = ol;
+  g.ldo = ldo;
+  g.qkv = qkv;
+  g.Tp = Tp;
+  HIPCHK(launch_enc_gemm2(epi, g, st));
+  return W4H_OK;
+}
+
 // The encoder forward on stream st: mel [n_mels][2T] (device) -> out [T][d] (device).
 int forward(w4h_encoder* e, const float* mel, float* out, hipStream_t st) {
   const w4h_encoder_dims& D = e->dims;
@@ -322,18 +347,22 @@ int forward(w4h_encoder* e, const float* mel, float* out, hipStream_t st) {
   if ((rc = gemm(kEpiGeluPos, e->x1p, 2 * d, T, d, 3 * d, e->c2w, nullptr, e->c2b, e->x, d, e->pos, nullptr, 0, st)))
     return rc;
   for (const EncLayer& L : e->layers) {
-    HIPCHK(launch_enc_ln(e->x, T, d, L.ln1_g, L.ln1_b, e->xn, st));
-    if ((rc = gemm(kEpiQkv, e->xn, d, T, 3 * d, d, L.w_qkv, L.s_qkv, L.b_qkv, nullptr, 0, nullptr, e->qkv, e->Tp, st)))
+    HIPCHK(launch_enc_ln(e->x, T, d, L.ln1_g, L.ln1_b, nullptr, e->xnh, e->xnl, st));
+    if ((rc = gemm2(kEpiQkv, e->xnh, e->xnl, d, T, 3 * d, d, L.w_qkv, L.s_qkv, L.b_qkv, nullptr, nullptr, nullptr, 0, e->qkv,
+                    e->Tp, st)))
       return rc;
-    HIPCHK(launch_enc_attn(e->qkv, T, e->Tp, H, e->att, st));
-    if ((rc = gemm(kEpiResid, e->att, d, T, d, d, L.w_o, L.s_o, L.b_o, e->x, d, e->x, nullptr, 0, st))) return rc;
-    HIPCHK(launch_enc_ln(e->x, T, d, L.ln2_g, L.ln2_b, e->xn, st));
-    if ((rc = gemm(kEpiGelu, e->xn, d, T, 4 * d, d, L.w_1, L.s_1, L.b_1, e->hid, 4 * d, nullptr, nullptr, 0, st)))
+    HIPCHK(launch_enc_attn(e->qkv, T, e->Tp, H, e->atth, e->attl, st));
+    if ((rc = gemm2(kEpiResid, e->atth, e->attl, d, T, d, d, L.w_o, L.s_o, L.b_o, e->x, nullptr, nullptr, d, nullptr, 0, st)))
       return rc;
-    if ((rc = gemm(kEpiResid, e->hid, 4 * d, T, d, 4 * d, L.w_2, L.s_2, L.b_2, e->x, d, e->x, nullptr, 0, st)))
+    HIPCHK(launch_enc_ln(e->x, T, d, L.ln2_g, L.ln2_b, nullptr, e->xnh, e->xnl, st));
+    if ((rc = gemm2(kEpiGeluPlanes, e->xnh, e->xnl, d, T, 4 * d, d, L.w_1, L.s_1, L.b_1, nullptr, e->hidh, e->hidl, 4 * d,
+                    nullptr, 0, st)))
+      return rc;
+    if ((rc = gemm2(kEpiResid, e->hidh, e->hidl, 4 * d, T, d, 4 * d, L.w_2, L.s_2, L.b_2, e->x, nullptr, nullptr, d, nullptr, 0,
+                    st)))
       return rc;
   }
-  HIPCHK(launch_enc_ln(e->x, T, d, e->lnp_g, e->lnp_b, out, st));
+  HIPCHK(launch_enc_ln(e->x, T, d, e->lnp_g, e->lnp_b, out, nullptr, nullptr, st));
   return W4H_OK;
 }
 
