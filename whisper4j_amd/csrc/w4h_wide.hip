@@ -544,12 +544,17 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
                                                 const int32_t* __restrict__ slot_table, float* __restrict__ act, int lda) {
   extern __shared__ float sc[];  // [t + 1] scores, then probabilities
   __shared__ float q[64], kc[64], vc[64], red[4 * 64], stat[8];
-  if (ctl->stop) return;
   const int s = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int kg = tid >> 3, dc = tid & 7;
+  // the slot-table entries of the first block, loaded with the control block (not after it)
+  int slot0[kSelfKF];
+  if (slot_table)
+#pragma unroll
+    for (int f = 0; f < kSelfKF; ++f) slot0[f] = slot_table[(size_t)s * max_ctx + min(32 * f + kg, max_ctx - 1)];
+  if (ctl->stop) return;
   const int t = ctl->kv_len0 + ctl->i;  // position of the current token
   const int32_t* srow = ctl->slots_on ? slot_table + (size_t)s * max_ctx : nullptr;
   const size_t head_base = ((size_t)l * S * H) * max_ctx * kHeadDim;  // layer l
-  const int kg = tid >> 3, dc = tid & 7;
   auto kv_off = [&](int j) -> size_t {
     const int slot = srow ? srow[j] : s;
     return head_base + (((size_t)slot * H + h) * max_ctx + j) * kHeadDim + dc * 8;
@@ -560,7 +565,8 @@ __global__ __launch_bounds__(256) void k_w_self(const WideCtl* __restrict__ ctl,
   for (int f = 0; f < kSelfKF; ++f) {
     const int j = 32 * f + kg;
     if (j < t) {
-      const size_t o = kv_off(j);
+      const int slot = srow ? slot0[f] : s;
+      const size_t o = head_base + (((size_t)slot * H + h) * max_ctx + j) * kHeadDim + dc * 8;
       kr[f] = *reinterpret_cast<const uint4*>(kvk + o);
       vr[f] = *reinterpret_cast<const uint4*>(kvv + o);
     } else {
