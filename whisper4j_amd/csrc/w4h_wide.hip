@@ -1024,17 +1024,106 @@ __global__ __launch_bounds__(256) void k_w_select(const WideCtl* __restrict__ ct
   const int part = blockIdx.y * 4 + wv;
   const int v0 = part * kWideSelChunk;
   const int nl = max(0, min(kWideSelChunk, V - v0));
-  for (int j = lane; j < nl; j += 64) {
-    const int v = v0 + j;
-    const float x = slice_sum<4>(P, ks, ss, (size_t)s * V + v) + (bias ? bias[v] : 0.f);
-    rw[wv][j] = x;
-    lg[wv][j] = (masked(mask, mw, s, v) || masked(mask2, mw, s, v)) ? -INFINITY : x;
-    idx[wv][j] = v;
-    if (logits_out) logits_out[(size_t)s * V + v] = x;
+  if (nl > 0 && ks <= 4) {
+    // every load of the lane's kSelPer entries (slices, bias, mask words) issued before any is used;
+    // indices clamped to the chunk's last entry, the stores guarded
+    constexpr int kSelPer = kWideSelChunk / 64;
+    float t[kSelPer][4], bv[kSelPer];
+    uint32_t m1[kSelPer], m2[kSelPer];
+#pragma unroll
+    for (int u = 0; u < kSelPer; ++u) {
+      const int v = v0 + min(lane + 64 * u, nl - 1);
+#pragma unroll
+      for (int z = 0; z < 4; ++z) t[u][z] = P[(size_t)min(z, ks - 1) * ss + (size_t)s * V + v];
+      bv[u] = bias ? bias[v] : 0.f;
+      m1[u] = mask ? mask[(size_t)s * mw + (v >> 5)] : 0u;
+      m2[u] = mask2 ? mask2[(size_t)s * mw + (v >> 5)] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < kSelPer; ++u) {
+      const int j = lane + 64 * u;
+      if (j >= nl) continue;
+      const int v = v0 + j;
+      float acc = 0.f;
+#pragma unroll
+      for (int z = 0; z < 4; ++z) acc += z < ks ? t[u][z] : 0.f;
+      const float x = acc + bv[u];
+      rw[wv][j] = x;
+      lg[wv][j] = (((m1[u] | m2[u]) >> (v & 31)) & 1u) ? -INFINITY : x;
+      idx[wv][j] = v;
+      if (logits_out) logits_out[(size_t)s * V + v] = x;
+    }
+  } else {
+    for (int j = lane; j < nl; j += 64) {
+      const int v = v0 + j;
+      const float x = slice_sum<4>(P, ks, ss, (size_t)s * V + v) + (bias ? bias[v] : 0.f);
+      rw[wv][j] = x;
+      lg[wv][j] = (masked(mask, mw, s, v) || masked(mask2, mw, s, v)) ? -INFINITY : x;
+      idx[wv][j] = v;
+      if (logits_out) logits_out[(size_t)s * V + v] = x;
+    }
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront", "local");
   if (part < nsel) sel_partial(lg[wv], rw[wv], idx[wv], nl, probe, topk, selp + ((size_t)s * nsel + part) * kSelWords);
+}
+
+// sel_merge for at most 128 partials: a lane's two records are loaded whole before any is used
+// (the same operations in the same order, so the same result).
+DEV void sel_merge_128(const float* recs, int n, int topk, float* out_rec) {
+  const int lane = threadIdx.x & 63;
+  float r[2][kSelWords];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float* src = recs + (size_t)min(lane + 64 * h, n - 1) * kSelWords;
+#pragma unroll
+    for (int w = 0; w < kSelWords; ++w) r[h][w] = src[w];
+  }
+  float bv = -INFINITY, rv = -INFINITY, pv = -INFINITY;
+  int bi = 0x7fffffff;
+  TopList tl;
+  top_init(tl);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (lane + 64 * h >= n) continue;
+    const int id = __float_as_int(r[h][1]);
+    if (r[h][0] > bv || (r[h][0] == bv && id < bi)) {
+      bv = r[h][0];
+      bi = id;
+    }
+    rv = fmaxf(rv, r[h][3]);
+    pv = fmaxf(pv, r[h][5]);
+#pragma unroll
+    for (int q = 0; q < W4H_TOPK_MAX; ++q)
+      if (q < topk) top_insert(tl, r[h][6 + q], __float_as_int(r[h][6 + W4H_TOPK_MAX + q]));
+  }
+  wave_argmax(bv, bi);
+  rv = wave_max(rv);
+  pv = wave_max(pv);
+  float se = 0.f, re = 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (lane + 64 * h >= n) continue;
+    if (r[h][0] > -INFINITY) se += r[h][2] * __expf(r[h][0] - bv);
+    if (r[h][3] > -INFINITY) re += r[h][4] * __expf(r[h][3] - rv);
+  }
+  se = wave_sum(se);
+  re = wave_sum(re);
+  float tv[W4H_TOPK_MAX];
+  int ti[W4H_TOPK_MAX];
+  top_pop(tl, topk, tv, ti);
+  if (lane == 0) {
+    out_rec[0] = bv;
+    out_rec[1] = __int_as_float(bi);
+    out_rec[2] = se;
+    out_rec[3] = rv;
+    out_rec[4] = re;
+    out_rec[5] = pv;
+    for (int k = 0; k < W4H_TOPK_MAX; ++k) {
+      out_rec[6 + k] = tv[k];
+      out_rec[6 + W4H_TOPK_MAX + k] = __int_as_float(ti[k]);
+    }
+  }
 }
 
 __global__ __launch_bounds__(64) void k_w_selmerge(WideCtl* __restrict__ ctl, const float* __restrict__ selp, int S, int nsel,
@@ -1043,7 +1132,8 @@ __global__ __launch_bounds__(64) void k_w_selmerge(WideCtl* __restrict__ ctl, co
   if (ctl->stop) return;
   const int s = blockIdx.x;
   const int topk = ctl->topk, i = ctl->i;
-  sel_merge(selp + (size_t)s * nsel * kSelWords, nsel, kSelWords, topk, rec);
+  if (nsel <= 128) sel_merge_128(selp + (size_t)s * nsel * kSelWords, nsel, topk, rec);
+  else sel_merge(selp + (size_t)s * nsel * kSelWords, nsel, kSelWords, topk, rec);
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront", "local");
   if (threadIdx.x == 0) {
