@@ -1238,32 +1238,49 @@ __global__ __launch_bounds__(256) void k_w_beam(WideCtl* __restrict__ ctl, BeamD
     order[rank] = tid;
   }
   __syncthreads();
-  if (tid == 0) {
-    int nlive = 0;
-    for (int c = 0; c < nc; ++c) nlive += clive[c];
-    int nf = s_nf0, saved = 0;
-    for (int q = 0; q < nlive; ++q) {
-      const int c = order[q], b = c / (B + 1);
-      if (sti[c] == eot) {
-        fsrc[nf] = b;
-        fsc[nf] = csc[c];
-        ++nf;
-        if (nf >= B) break;
-        continue;
-      }
-      if (saved >= B) continue;
-      psrc[saved] = b;
-      ptok[saved] = sti[c];
-      plp[saved] = csc[c];
-      ++saved;
+  // The walk over the sorted candidates (end tokens to the finished list until it holds B, stopping
+  // there; the first B others become the new beams), done by wave 0 at once, lane q taking sorted
+  // position q (nc <= 56 < 64): the counts of end tokens and of others before each position come
+  // from ballots.
+  if (tid < 64) {
+    const int q = tid;
+    const u64 lt = (1ull << q) - 1ull;
+    const int nlive = __popcll(__ballot(q < nc && clive[q]));
+    const bool act = q < nlive;
+    const int c = act ? order[q] : 0, b = c / (B + 1);
+    const bool is_eot = act && sti[c] == eot;
+    const u64 eotm = __ballot(is_eot);
+    const int e_before = __popcll(eotm & lt);
+    // the walk stops at the first end token that fills the finished list (inclusive)
+    const u64 brk = __ballot(is_eot && s_nf0 + e_before + 1 >= B);
+    const int qstop = brk ? __ffsll((long long)brk) - 1 : 64;
+    const bool proc = act && q <= qstop;
+    if (proc && is_eot) {
+      fsrc[s_nf0 + e_before] = b;
+      fsc[s_nf0 + e_before] = csc[c];
     }
-    for (int j = saved; j < B && saved > 0; ++j) {  // leftover beams continue from the first
-      psrc[j] = psrc[0];
-      ptok[j] = ptok[0];
-      plp[j] = plp[0];
+    const u64 keep = __ballot(proc && !is_eot);
+    const int n_before = __popcll(keep & lt);
+    if (proc && !is_eot && n_before < B) {
+      psrc[n_before] = b;
+      ptok[n_before] = sti[c];
+      plp[n_before] = csc[c];
     }
-    s_nf = nf;
-    s_done = (nlive == 0 || saved == 0 || nf >= B) ? 1 : 0;
+    const int saved = min(B, __popcll(keep));
+    const int nf = s_nf0 + __popcll(eotm & __ballot(proc));
+    // leftover beams continue from the first saved one (the lane at n_before == 0)
+    const int first = keep ? __ffsll((long long)keep) - 1 : 0;
+    const int f_b = __shfl(b, first), f_tok = __shfl(act ? sti[c] : 0, first);
+    const double f_lp = __shfl(act ? csc[c] : 0.0, first);
+    if (saved > 0 && q >= saved && q < B) {
+      psrc[q] = f_b;
+      ptok[q] = f_tok;
+      plp[q] = f_lp;
+    }
+    if (q == 0) {
+      s_nf = nf;
+      s_done = (nlive == 0 || saved == 0 || nf >= B) ? 1 : 0;
+    }
   }
   __syncthreads();
   // 3. finished entries of this step: the source beam's tokens (without the end token)
