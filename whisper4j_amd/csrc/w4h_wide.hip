@@ -1162,6 +1162,7 @@ __global__ __launch_bounds__(64) void k_w_selmerge(WideCtl* __restrict__ ctl, co
 
 constexpr int kBeamCand = kBeamMax * (kBeamMax + 1);
 constexpr int kSlotChunk = 1024;
+constexpr int kBeamSupLds = 512;  // suppress-list entries held in LDS
 
 // Dynamic LDS of k_w_beam: the slot-table chunk, then reused for the next step's masks.
 inline size_t beam_lds_bytes(int B, int mw) {
@@ -1184,8 +1185,10 @@ __global__ __launch_bounds__(256) void k_w_beam(WideCtl* __restrict__ ctl, BeamD
   __shared__ int psrc[kBeamMax], ptok[kBeamMax], fsrc[kBeamMax];
   __shared__ double plp[kBeamMax], fsc[kBeamMax];
   __shared__ int s_nf0, s_nf, s_done, s_cur, s_maxlen;
+  __shared__ int ssup[kBeamSupLds];
   if (ctl->stop) return;
   const int tid = threadIdx.x;
+  for (int q = tid; q < min(nsup, kBeamSupLds); q += 256) ssup[q] = sup[q];  // read once, used per row below
   const int step = ctl->i - 1;             // the selection merge of this step has advanced the index
   const int kv = ctl->kv_len0 + step + 1;  // KV length after this step
   const int nc = B * (B + 1);
@@ -1352,7 +1355,7 @@ __global__ __launch_bounds__(256) void k_w_beam(WideCtl* __restrict__ ctl, BeamD
   for (int j = 0; j < B; ++j) {
     const int b = psrc[j], cnt = slen[b] + 1;
     auto g = [&](int q) { return q < cnt - 1 ? stoks[b][q] : ptok[j]; };
-    for (int q = tid; q < nsup; q += 256) set(j, sup[q]);
+    for (int q = tid; q < nsup; q += 256) set(j, q < kBeamSupLds ? ssup[q] : sup[q]);
     for (int nn = 3; nn <= 4; ++nn)
       for (int i = tid; i <= cnt - nn; i += 256) {
         bool match = true;
