@@ -13,7 +13,7 @@ a real single-token decoder step (the next token could be the previous argmax; t
 id is read from device memory instead).  The whole sweep is one launch of the persistent step
 kernel, timed with HIP events on the session stream.
 
-Prints ONE JSON line (see the keys below); ``--gpus N`` with N > 1 exits: this build runs on one GPU.
+Prints ONE JSON line (see the keys below); ``--gpus N`` with N > 1 exits: the decoder runs on one GPU.
 """
 
 from __future__ import annotations
@@ -466,7 +466,7 @@ def main():
         traffic_from(args.traffic_from[0], args.traffic_from[1], args.copy_mib or 256, TRAFFIC_FILE)
         return
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for {args.gpus}); this build has no multi-GPU path.",
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}); the decoder has no multi-GPU path.",
               file=sys.stderr)
         sys.exit(2)
 

@@ -1,7 +1,7 @@
 """ctypes wrapper of the oracle (libwhisper_ref.so, a CPU restatement of whisper4j's decode path).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's CPU-baseline
-leg, always as the checker (or the timed CPU baseline), never by the product package.
+leg, always as the parity reference (or the timed CPU baseline), never by the product package.
 """
 
 from __future__ import annotations

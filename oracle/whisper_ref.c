@@ -1,7 +1,7 @@
 /*
  * whisper_ref.c -- the oracle: CPU restatement of whisper4j's Linux text-decoder path.
  *
- * TEST INFRASTRUCTURE ONLY (see whisper_ref.h).  It is the checker for the HIP product and the
+ * TEST INFRASTRUCTURE ONLY (see whisper_ref.h).  It is the parity reference for the HIP product and the
  * timed CPU baseline ("port"); nothing in whisper4j_amd/ links, loads or calls it.
  *
  * Build: gcc -O3 -march=x86-64-v3 -ffp-contract=off -fPIC -shared whisper_ref.c -lz -lm

@@ -2,7 +2,7 @@
  * whisper_ref.h -- the oracle: a CPU restatement of whisper4j's Linux decode path.
  *
  * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's CPU
- * baseline leg may load this library, and only as the checker (or as the timed CPU
+ * baseline leg may load this library, and only as the parity reference (or as the timed CPU
  * baseline).  The product (whisper4j_amd) never links, loads or calls it.
  *
  * Every function states the reference file:line it restates (paths are relative to the
@@ -135,7 +135,7 @@ int orc_greedy_drive(const orc_ops* ops, int n_vocab, int eot, int max_tokens, c
                      int no_speech, float temperature, int ts_begin, uint64_t seed, orc_result* out);
 /* gaps (nullable, [max_tokens]): gaps[i] for search step i = the score of the last hypothesis kept
  * minus that of the first non-end candidate left out (+inf when none was left out); gaps[0] = the
- * final pick's margin over the runner-up.  Decisions with a gap above the checker's tolerance cannot
+ * final pick's margin over the runner-up.  Decisions with a gap above the parity tolerance cannot
  * flip under a logit error below it (test instrumentation, not part of the reference). */
 int orc_beam_drive(const orc_ops* ops, int n_vocab, int eot, int max_tokens, const int32_t* suppress, int n_suppress,
                    int no_speech, int ts_begin, int beam, orc_result* out, double* gaps);

@@ -1,4 +1,4 @@
-"""Pins the oracle (a CPU restatement of whisper4j's decode path) before it is trusted as the checker.
+"""Pins the oracle (a CPU restatement of whisper4j's decode path) before it is trusted as the parity reference.
 
 Each check is either a known answer held by the reference's own tests (cited file:line, relative to
 src/test/java/com/sparrowlogic/whisper4j/), an exact closed form, a brute-force float64 evaluation,
