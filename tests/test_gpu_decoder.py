@@ -444,6 +444,37 @@ def test_device_sampling_equals_host_sampling(gpu, monkeypatch, temperature, see
     assert len(d.tokens) > 5
 
 
+@pytest.mark.parametrize("d,heads,wtype,temperature,seed,ts_begin", [(128, 2, "f16", 0.6, 7, -1), (128, 2, "f16", 1.0, 21, 500),
+                                                                   (768, 12, "f16", 0.8, 3, -1), (256, 4, "q8_0", 0.7, 5, 500)])
+def test_sampling_in_launch_equals_chain(gpu, monkeypatch, d, heads, wtype, temperature, seed, ts_begin):
+    """A sampled run on a one-row session draws its tokens inside one launch of the step kernel (the
+    grid's phase after the logits: row maximum, per-workgroup weight sums, the crossing range, the
+    token), instead of one-step launches chained with the masking and sampling kernels
+    (W4H_SAMPLE_IN_LAUNCH=0).  Same session, inputs and seed: identical tokens and average
+    log-probability within 1e-9 (the two sum the weights in different orders, which moves only the last
+    bits of a double).  Covers the three sampled instances of the step kernel: f16 with two and three
+    register rounds (d = 128, 768) and q8_0."""
+    dims = synth.Dims(n_vocab=600, n_text_ctx=320, n_text_state=d, n_text_head=heads, n_text_layer=2, n_audio_ctx=50)
+    T = make(dims, 73, wtype=wtype)
+    xa = synth.encoder_output(dims, 73)
+    m = gpu.Model.from_tensors(dims, T)
+    dec = gpu.WhisperDecoder(m, beam_size=1)
+    prompt, eot, sup = [10, 11, 12], 599, [1, 2]
+    res = {}
+    monkeypatch.setenv("W4H_DEVICE_SAMPLE", "1")
+    for mode in ("0", "1"):
+        monkeypatch.setenv("W4H_SAMPLE_IN_LAUNCH", mode)
+        res[mode] = dec.decode(xa, prompt, eot, 120, sup, temperature=temperature, seed=seed, timestamp_begin=ts_begin)
+    dec.close()
+    m.close()
+    c, i = res["0"], res["1"]
+    say(f"d={d} {wtype} T={temperature} seed={seed} ts={ts_begin}: chain {len(c.tokens)} tokens avg {c.avg_logprob:.9f}, "
+        f"in-launch {len(i.tokens)} tokens avg {i.avg_logprob:.9f}")
+    assert i.tokens == c.tokens
+    assert abs(i.avg_logprob - c.avg_logprob) <= 1e-9
+    assert len(i.tokens) > 5
+
+
 @pytest.mark.parametrize("beam", [1, 3])
 def test_decode_with_fallback_matches_oracle(gpu, orc, beam):
     """WhisperDecoder.decodeWithFallback (main/nn/WhisperDecoder.java:119-149) on a model whose greedy

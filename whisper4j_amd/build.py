@@ -22,9 +22,10 @@ DEVICE_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-Wall",
 CLANG = os.environ.get("W4H_HOST_CXX", "/opt/rocm/lib/llvm/bin/clang++")
 # Host-only translation units: plain C++ against the HIP runtime API (no device code).
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include"]
-# Step-kernel instances (rows x weight type x register rounds), one translation unit each so they
+# Step-kernel instances (rows x weight type x register rounds; "_s": sampled runs), one translation unit each so they
 # compile in parallel; the shared device code is w4h_kernels.h.
-STEP_VARIANTS = ["1_f16_r2", "1_f16_r3", "1_q8_r2", "8_f16_r2", "8_f16_r3", "8_q8_r2"]
+STEP_VARIANTS = ["1_f16_r2", "1_f16_r3", "1_q8_r2", "8_f16_r2", "8_f16_r3", "8_q8_r2", "1_f16_r2_s", "1_f16_r3_s",
+                 "1_q8_r2_s"]
 SOURCES = ([("w4h_device.hip", HIPCC, DEVICE_FLAGS), ("w4h_wide.hip", HIPCC, DEVICE_FLAGS),
             ("w4h_xkv.hip", HIPCC, DEVICE_FLAGS), ("w4h_sample.hip", HIPCC, DEVICE_FLAGS), ("w4h_encoder.hip", HIPCC, DEVICE_FLAGS)] + [(f"w4h_step_{v}.hip", HIPCC, DEVICE_FLAGS) for v in STEP_VARIANTS] +
            [("w4h_api.cpp", CLANG, HOST_FLAGS), ("w4h_ggml.cpp", CLANG, HOST_FLAGS), ("w4h_decode.cpp", CLANG, HOST_FLAGS), ("w4h_encoder_api.cpp", CLANG, HOST_FLAGS)])

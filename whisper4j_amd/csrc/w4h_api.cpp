@@ -468,6 +468,7 @@ struct w4h_session {
   int Ap = 0;
   // device-sampled decodes (T > 0): sampler state, the step's logits rows, the static suppress mask
   DevBuf samp, samp_row, samp_sup;
+  DevBuf samp_x, samp_io;  // in-launch sampling: exchange words; drawn tokens and log-probabilities
   // cancellation (w4h_session_cancel, callable from any thread): the host flag, and the device cancel
   // word (input area offset 0, before the error word) written on a stream of its own
   std::atomic<int> cancel{0};
@@ -636,7 +637,8 @@ static std::mutex& coop_lock(int device) {
 // of steps run and the self-KV advances by that many.
 int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int n_steps, const uint32_t* extra_mask,
               int topk, w4h_step_out* out, float* logits, float* ms, uint64_t* trace = nullptr,
-              const RulesRun* rules = nullptr, int* steps_done = nullptr) {
+              const RulesRun* rules = nullptr, int* steps_done = nullptr, const SampleRun* samp = nullptr,
+              SampleRunOut* sout = nullptr) {
   if (s->closed) return fail(W4H_ERR_CLOSED, "session destroyed");
   if (s->cancel.load()) return fail(W4H_ERR_CANCELLED, "session cancelled");
   if (!tokens || n_steps <= 0) return fail(W4H_ERR_INVALID, "tokens and n_steps > 0 required");
@@ -731,6 +733,24 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
     p.hist_cap = rules->nhist + n_steps;
     if (!(lds = rules_layout(s, p.hist_cap, p))) return fail(W4H_ERR_INVALID, "no LDS left for the device decode rules");
   }
+  if (samp) {
+    if (!rules || !sout || !(samp->temperature > 0.0f)) return fail(W4H_ERR_INVALID, "in-launch sampling needs the decode rules");
+    const int V = s->m->dims.n_vocab;
+    if (s->grid > kThreads || (size_t)V > (size_t)s->grid * kThreads * kSampEpt)
+      return fail(W4H_ERR_INVALID, "in-launch sampling needs grid <= %d and V <= grid * %d", kThreads, kThreads * kSampEpt);
+    const size_t xw = (size_t)s->grid * 6 + 2;
+    if ((rc = ensure(s->samp_x, xw * sizeof(u64))) || (rc = ensure(s->samp_row, sizeof(float) * (size_t)V)) ||
+        (rc = ensure(s->samp_io, (sizeof(int32_t) + sizeof(double)) * (size_t)n_steps)))
+      return rc;
+    HIPCHK(hipMemsetAsync(s->samp_x.p, 0, xw * sizeof(u64), s->stream));
+    p.samp_t = samp->temperature;
+    p.samp_rng = samp->rng;
+    p.samp_x = s->samp_x.as<u64>();
+    p.samp_stride = 0;
+    p.samp_row = s->samp_row.as<float>();
+    p.samp_lp = s->samp_io.as<double>();
+    p.samp_tok = reinterpret_cast<int32_t*>(p.samp_lp + n_steps);
+  }
   std::unique_lock<std::mutex> coop(coop_lock(s->m->device));
   hipEvent_t e0 = nullptr, e1 = nullptr;
   if (ms) {
@@ -753,12 +773,28 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
   if (s->cancel.load()) return fail(W4H_ERR_CANCELLED, "session cancelled during the launch");
   if (herr) return fail(W4H_ERR_TIMEOUT, "a device-side wait expired during the step (code %u); step aborted", herr);
   int done = n_steps;
-  if (rules)
+  if (samp) {
+    // the drawn tokens end the run at the end token; the records' argmax does not
+    std::vector<char> io((sizeof(int32_t) + sizeof(double)) * (size_t)n_steps);
+    HIPCHK(hipMemcpy(io.data(), s->samp_io.p, io.size(), hipMemcpyDeviceToHost));
+    const double* lp = reinterpret_cast<const double*>(io.data());
+    const int32_t* tk = reinterpret_cast<const int32_t*>(lp + n_steps);
+    for (int i = 0; i < n_steps; i++)
+      if (tk[i] == rules->eot) {
+        done = i + 1;
+        break;
+      }
+    sout->steps = done;
+    sout->ended = tk[done - 1] == rules->eot;
+    sout->tokens.assign(tk, tk + done);
+    sout->lps.assign(lp, lp + done);
+  } else if (rules) {
     for (int i = 0; i < n_steps; i++)
       if (out[i].argmax == rules->eot) {
         done = i + 1;
         break;
       }
+  }
   if (steps_done) *steps_done = done;
   s->kv_len += done;
   return W4H_OK;
@@ -1357,6 +1393,20 @@ int device_greedy_run(w4h_session* s, const RulesRun& r, int n_steps, const uint
   return run_steps(s, &tok, nullptr, n_steps, mask2, 1, out, nullptr, nullptr, nullptr, &r, steps_done);
 }
 
+// Sampled runs with the draw inside the step kernel (one launch per run) instead of a chain of one-step
+// launches and sampling kernels: one-row persistent sessions (W4H_SAMPLE_IN_LAUNCH=0 selects the chain).
+static bool sample_in_launch(const w4h_session* s) {
+  if (const char* e = getenv("W4H_SAMPLE_IN_LAUNCH"))
+    if (!strcmp(e, "0")) return false;
+  if (!session_device_rules(s) || s->grid > kThreads || (size_t)s->m->dims.n_vocab > (size_t)s->grid * kThreads * kSampEpt)
+    return false;
+  // the draw's scratch (pairs, range sums, scan words) fits the phase region, which ends where the
+  // resident vocabulary rows begin
+  const size_t d = (size_t)s->m->dims.n_text_state;
+  const size_t big0 = 8 + kMaxRows + (size_t)kResItems * kMaxRows * 8 + (size_t)s->S * 4 * d + (size_t)s->S * d;
+  return s->res_off / sizeof(float) >= big0 + (size_t)8 * s->grid + 64;
+}
+
 bool session_device_sample(const w4h_session* s) {
   if (s->wide || s->S > kMaxRows || s->m->dims.n_vocab > kSampleMaxV) return false;
   if (const char* e = getenv("W4H_DEVICE_SAMPLE"))
@@ -1381,6 +1431,14 @@ int device_sampled_run(w4h_session* s, const SampleRun& r, int n_steps, const ui
   if ((uint64_t)s->next_tag + (uint64_t)n_steps >= 0xfffffff0ull) return fail(W4H_ERR_INVALID, "tag space exhausted; recreate the session");
   const int V = s->m->dims.n_vocab;
   int rc;
+  if (sample_in_launch(s)) {
+    // one launch for the whole run: the step kernel draws each token itself (phase_sample)
+    RulesRun rr{r.hist, r.nhist, r.eot, r.tsb};
+    std::vector<w4h_step_out> recs((size_t)n_steps);
+    int done = 0;
+    const int32_t tok = r.hist[r.nhist - 1];
+    return run_steps(s, &tok, nullptr, n_steps, sup, 0, recs.data(), nullptr, nullptr, nullptr, &rr, &done, &r, out);
+  }
   HIPCHK(hipSetDevice(s->m->device));
   if ((rc = ensure(s->samp_row, sizeof(float) * (size_t)s->S * V)) || (rc = ensure(s->samp_sup, sizeof(uint32_t) * (size_t)s->mw)))
     return rc;

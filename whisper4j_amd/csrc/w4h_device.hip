@@ -173,6 +173,9 @@ int step_max_grid(size_t lds_bytes) {
 
 // Step kernel variants live in their own translation units (w4h_step_*.hip), compiled in parallel.
 hipError_t launch_step_1_f16_r2(const StepParams& p, int grid, size_t lds, hipStream_t st);
+hipError_t launch_step_1_f16_r2_s(const StepParams& p, int grid, size_t lds, hipStream_t st);
+hipError_t launch_step_1_f16_r3_s(const StepParams& p, int grid, size_t lds, hipStream_t st);
+hipError_t launch_step_1_q8_r2_s(const StepParams& p, int grid, size_t lds, hipStream_t st);
 hipError_t launch_step_1_f16_r3(const StepParams& p, int grid, size_t lds, hipStream_t st);
 hipError_t launch_step_1_q8_r2(const StepParams& p, int grid, size_t lds, hipStream_t st);
 hipError_t launch_step_8_f16_r2(const StepParams& p, int grid, size_t lds, hipStream_t st);
@@ -181,6 +184,11 @@ hipError_t launch_step_8_q8_r2(const StepParams& p, int grid, size_t lds, hipStr
 
 hipError_t launch_step(const StepParams& p, int grid, size_t lds, hipStream_t st) {
   const int dr = step_rounds(p.d, p.wq8);
+  if (p.S == 1 && p.samp_t > 0.f) {
+    if (p.wq8) return launch_step_1_q8_r2_s(p, grid, lds, st);
+    return dr == 2 ? launch_step_1_f16_r2_s(p, grid, lds, st) : launch_step_1_f16_r3_s(p, grid, lds, st);
+  }
+  if (p.samp_t > 0.f) return hipErrorInvalidValue;  // in-launch sampling draws for one row
   if (p.S == 1) {
     if (p.wq8) return launch_step_1_q8_r2(p, grid, lds, st);
     return dr == 2 ? launch_step_1_f16_r2(p, grid, lds, st) : launch_step_1_f16_r3(p, grid, lds, st);

@@ -15,6 +15,7 @@ constexpr int kMaxRows = 8;    // decoder rows per step handled by the persisten
 constexpr int kSelfChunk = 256;  // self-attention keys per work item
 constexpr int kMaxChunk = 256;   // longest key chunk an attention work item may take
 constexpr int kResItems = 4;     // d-row items (8 rows each) one workgroup may own in a phase
+constexpr int kSampEpt = 4;  // row entries per thread of the in-launch sampler (V <= grid * kThreads * kSampEpt)
 constexpr int kRep = 1;          // replicas of every exchange buffer (consumers poll blockIdx % kRep)
 constexpr int kPartWords = 2 + kHeadDim;            // (m, l, acc[64]) per attention partial
 constexpr int kMergeChunks = 8;                     // attention partials merged from registers
@@ -75,6 +76,15 @@ struct StepParams {
   const float* bias;            // [V] fixed logit bias added before selection, or null
   const int* stop;              // device word: the launch does nothing when it is non-zero (chained
                                 // sampled decodes), or null
+  // Temperature sampling inside the launch (one row, decode rules on): after the logits the
+  // workgroups draw the step's token together instead of taking the argmax.
+  float samp_t;                 // temperature; 0: off
+  uint64_t samp_rng;            // generator state; the run's step i takes draw i + 1 after it
+  u64* samp_x;                  // exchange words, kRep replicas samp_stride apart: [grid][6] sums, then 2
+  size_t samp_stride;
+  float* samp_row;              // [V] the step's masked logits (device-coherent stores and loads)
+  int32_t* samp_tok;            // [nsteps] drawn tokens
+  double* samp_lp;              // [nsteps] their log-probabilities
 };
 
 // Device temperature sampling of one decode row (WhisperDecoder.sample and the log-probability the

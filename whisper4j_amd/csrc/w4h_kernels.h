@@ -152,6 +152,38 @@ DEV void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// The k-th SplitMix64 output after `state` (k >= 1) as a double in [0, 1): the draw the host decode
+// loop's generator returns on its k-th call.
+DEV double splitmix_uniform(uint64_t state, int k) {
+  uint64_t z = state + (uint64_t)k * 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  z ^= z >> 31;
+  return (double)(z >> 11) * (1.0 / 9007199254740992.0);
+}
+
+DEV double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Inclusive scan over the wave's lanes, in lane order.
+DEV double wave_scan_d(double v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const double u = __shfl_up(v, o);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
+
+DEV double ld_agent(const double* p) {
+  return __longlong_as_double((long long)__hip_atomic_load(reinterpret_cast<const unsigned long long*>(p),
+                                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
 // OR of `pred` over the workgroup through LDS (LDS-only barriers); the second barrier keeps the
 // vote words from being rewritten by a later call before every wave has read them.
 DEV bool wg_any(bool pred) {
@@ -1911,6 +1943,196 @@ DEV bool phase_logits(const StepParams& p, const Lds& m, const StepCtx& c) {
 // Selection reduction.  Every workgroup that runs a phase reading the next token reduces the
 // (max, argmax) pairs; one workgroup also merges the full partials (blocks of kRedBlock
 // workgroups) into the step outputs.
+// Exclusive scan over the workgroup's threads (in thread order) of per-thread doubles; *total gets
+// the sum.  red: 4 doubles of LDS.  LDS-only barriers (global loads in flight stay in flight).
+DEV double wg_scan_excl_d(double v, double* red, double* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const double inc = wave_scan_d(v);
+  if (lane == 63) red[wave] = inc;
+  lds_barrier();
+  double pre = __shfl_up(inc, 1);
+  pre = lane == 0 ? 0.0 : pre;
+  double t = 0.0;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) {
+    pre += w < wave ? red[w] : 0.0;
+    t += red[w];
+  }
+  *total = t;
+  lds_barrier();
+  return pre;
+}
+
+DEV void ll_st_d(u64* p, double v, uint32_t tag) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  ll_st(p, __uint_as_float((uint32_t)b), tag, 0);
+  ll_st(p + 1, __uint_as_float((uint32_t)(b >> 32)), tag, 0);
+}
+DEV double words_d(const float* w) {
+  return __longlong_as_double((long long)(((unsigned long long)__float_as_uint(w[1]) << 32) | __float_as_uint(w[0])));
+}
+
+// Temperature sampling of the step's token by the whole grid, inside the launch (one row, decode
+// rules on): WhisperDecoder.sample and the log-probability the decode loop takes of the drawn token
+// (main/nn/WhisperDecoder.java:186-187, 576-598, 614-626).  The logits phase stored the masked row in
+// p.samp_row (device-coherent) before publishing each workgroup's (maximum, index) pair.  Workgroup g
+// owns the contiguous range [g * per, (g + 1) * per) of the row, thread t of it ept consecutive entries:
+//   1. M = the row maximum, from the pairs;
+//   2. p = exp((double)((l - M) / T)) (the float quotient widened), pf = (float) p; the range's sums of
+//      p, pf and exp(pf - 1) in double, published as tagged words;
+//   3. every workgroup: the totals in workgroup order, r = u * sum p (u: draw st + 1 of the SplitMix64
+//      generator after p.samp_rng), and the first range whose cumulative pf sum reaches r (the last
+//      range when none does);
+//   4. that range's workgroup finds, in vocabulary order, the first entry whose cumulative weight
+//      reaches r (continuing into the following ranges when its own sum fell short by rounding; the
+//      last index when none does) and publishes it with its pf;
+//   5. every workgroup takes the token; workgroup 0 records it with (pf - 1) - log(sum exp(pf - 1))
+//      (the reference's logSoftmax over the rewritten row, whose maximum is exactly 1).
+// The sums combine per-thread sequential sums by scans over threads and workgroups: they differ from
+// one sequential loop in the last bits of a double.  Compiled only into the step kernel instances
+// for sampled runs (SAMP = 1), so the greedy instances keep their registers.
+DEV bool phase_sample(const StepParams& p, const Lds& m, const StepCtx& c) {
+  const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, V = p.V;
+  float* pairs = m.big;        // [G][2]
+  float* sums = m.big + 2 * G; // [G][6] (three doubles as 32-bit halves)
+  double* dsc = reinterpret_cast<double*>((reinterpret_cast<uintptr_t>(m.big + 8 * G) + 7) & ~(uintptr_t)7);  // [16]
+  int* isc = reinterpret_cast<int*>(dsc + 16);                                                                // [8]
+  const int per = (V + G - 1) / G, ept = (per + kThreads - 1) / kThreads;
+  const float T = p.samp_t;
+  u64* sx = p.samp_x;
+  // 1. the row maximum
+  if (!ll_poll1<8>(rep(p, p.lpa), G * 2, pairs, c.tag, p.err)) return false;
+  float mx = -INFINITY;
+  for (int k = tid; k < G; k += kThreads) mx = fmaxf(mx, pairs[2 * k]);
+  mx = wave_max(mx);
+  if (lane == 0) dsc[wave] = mx;
+  lds_barrier();
+  const float M = fmaxf(fmaxf((float)dsc[0], (float)dsc[1]), fmaxf((float)dsc[2], (float)dsc[3]));
+  // 2. this workgroup's range: weights and sums
+  const int lo = g * per, hi = min(V, lo + per), j0 = lo + tid * ept;
+  float w[kSampEpt];
+  double sd = 0.0, sf = 0.0, se = 0.0;
+#pragma unroll
+  for (int e = 0; e < kSampEpt; ++e) {
+    const int j = j0 + e;
+    const bool in = e < ept && j < hi;
+    const float v = in ? __hip_atomic_load(p.samp_row + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
+    const double ex = in ? exp((double)((v - M) / T)) : 0.0;
+    w[e] = in ? (float)ex : 0.f;
+    sd += ex;
+    sf += (double)w[e];
+    se += in ? exp((double)(w[e] - 1.0f)) : 0.0;
+  }
+  double tsf;
+  const double pre_t = wg_scan_excl_d(sf, dsc + 4, &tsf);  // this thread's entries' prefix within the range
+  const double tsd = wave_sum_d(sd), tse = wave_sum_d(se);
+  if (lane == 0) {
+    dsc[8 + wave] = tsd;
+    dsc[12 + wave] = tse;
+  }
+  lds_barrier();
+  if (tid == 0) {
+    ll_st_d(sx + (size_t)g * 6, ((dsc[8] + dsc[9]) + dsc[10]) + dsc[11], c.tag);
+    ll_st_d(sx + (size_t)g * 6 + 2, tsf, c.tag);
+    ll_st_d(sx + (size_t)g * 6 + 4, ((dsc[12] + dsc[13]) + dsc[14]) + dsc[15], c.tag);
+  }
+  // 3. every workgroup: totals, the draw, the crossing range (thread k < G takes workgroup k)
+  if (!ll_poll1<8>(sx, G * 6, sums, c.tag, p.err)) return false;
+  const bool gin = tid < G;
+  const double gsd = gin ? words_d(sums + 6 * tid) : 0.0;
+  const double gsf = gin ? words_d(sums + 6 * tid + 2) : 0.0;
+  const double gse = gin ? words_d(sums + 6 * tid + 4) : 0.0;
+  double SD, SF, SE;
+  (void)wg_scan_excl_d(gsd, dsc + 4, &SD);
+  const double gpre = wg_scan_excl_d(gsf, dsc + 4, &SF);
+  (void)wg_scan_excl_d(gse, dsc + 4, &SE);
+  const double r = splitmix_uniform(p.samp_rng, c.st + 1) * SD;
+  const int hitg = gin && gpre + gsf >= r ? tid : 0x7fffffff;
+  const int wh = wave_min_i(hitg);
+  if (lane == 0) isc[wave] = wh;
+  lds_barrier();
+  int gs = min(min(isc[0], isc[1]), min(isc[2], isc[3]));
+  if (gs == 0x7fffffff) gs = G - 1;  // no range reaches r: the last one's scan ends at the last index
+  const double gs_pre = __shfl(gpre, gs & 63);  // the crossing range's prefix (wave gs / 64 holds it)
+  lds_barrier();
+  if (wave == (gs >> 6) && lane == 0) dsc[0] = gs_pre;
+  lds_barrier();
+  // 4. the crossing range's workgroup: the first entry whose cumulative weight reaches r
+  if (g == gs) {
+    double cum = dsc[0];
+    int tok = 0x7fffffff;
+    float tpf = 0.f;
+    for (int rg = gs; rg < G; ++rg) {
+      float q[kSampEpt];
+      double ts = 0.0;
+      const int rlo = rg * per, rhi = min(V, rlo + per), r0 = rlo + tid * ept;
+      if (rg == gs) {
+#pragma unroll
+        for (int e = 0; e < kSampEpt; ++e) q[e] = w[e];
+        ts = sf;
+      } else {
+        // past the crossing range (rounding): its weights again from the row
+#pragma unroll
+        for (int e = 0; e < kSampEpt; ++e) {
+          const int j = r0 + e;
+          const bool in = e < ept && j < rhi;
+          const float v = in ? __hip_atomic_load(p.samp_row + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
+          q[e] = in ? (float)exp((double)((v - M) / T)) : 0.f;
+          ts += (double)q[e];
+        }
+      }
+      double rtot;
+      double cc = cum + (rg == gs ? pre_t : wg_scan_excl_d(ts, dsc + 4, &rtot));
+      if (rg == gs) rtot = tsf;
+      int cand = 0x7fffffff;
+      float cpf = 0.f;
+#pragma unroll
+      for (int e = 0; e < kSampEpt; ++e) {
+        cc += (double)q[e];
+        const bool h = cand == 0x7fffffff && e < ept && r0 + e < rhi && cc >= r;
+        cand = h ? r0 + e : cand;
+        cpf = h ? q[e] : cpf;
+      }
+      const int wc = wave_min_i(cand);
+      if (lane == 0) isc[wave] = wc;
+      lds_barrier();
+      const int best = min(min(isc[0], isc[1]), min(isc[2], isc[3]));
+      lds_barrier();
+      if (best != 0x7fffffff) {
+        tok = best;
+        if (cand == best) dsc[1] = (double)cpf;
+        lds_barrier();
+        tpf = (float)dsc[1];
+        break;
+      }
+      cum += rtot;
+    }
+    if (tok == 0x7fffffff) {  // no cumulative weight reached r: the last index
+      tok = V - 1;
+      tpf = (float)exp((double)((__hip_atomic_load(p.samp_row + V - 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - M) / T));
+    }
+    if (tid == 0) {
+      ll_st(sx + (size_t)G * 6, __int_as_float(tok), c.tag, 0);
+      ll_st(sx + (size_t)G * 6 + 1, tpf, c.tag, 0);
+    }
+  }
+  // 5. every workgroup: the token
+  float* tw = sums;  // [2]
+  if (!ll_poll1<8>(sx + (size_t)G * 6, 2, tw, c.tag, p.err)) return false;
+  const int tok = __float_as_int(tw[0]);
+  if (tid == 0) {
+    m.toks[0] = tok;
+    m.hist[p.nhist0 + c.st] = tok;
+    if (g == 0) {
+      p.samp_tok[c.st] = tok;
+      p.samp_lp[c.st] = (double)(tw[1] - 1.0f) - log(SE);
+    }
+  }
+  lds_barrier();
+  return true;
+}
+
+template <int SAMP>
 DEV bool phase_reduce(const StepParams& p, const Lds& m, const StepCtx& c) {
   const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x, S = p.S, ng = p.ngroups;
   const bool last_step = c.st + 1 == p.nsteps;
@@ -1926,9 +2148,15 @@ DEV bool phase_reduce(const StepParams& p, const Lds& m, const StepCtx& c) {
   // With decode rules every workgroup keeps the token history, so every workgroup needs the token.
   const int kvn = c.kv + 1;
   const int self_items = S * p.H * ((kvn + kSelfChunk - 1) / kSelfChunk + 2), out_items = (p.d + 7) / 8;
-  const bool need_tok = !last_step && (p.rules || (g >= g0.base && g < g0.base + g0.size && g - g0.base < self_items) ||
+  const bool need_tok = !last_step && !SAMP && (p.rules || (g >= g0.base && g < g0.base + g0.size && g - g0.base < self_items) ||
                                        (g >= g1.base && g < g1.base + g1.size && g - g1.base < out_items));
   const bool is_writer = g == writer && p.out != nullptr;
+  if constexpr (SAMP) {
+    // every workgroup takes part in the draw (the last step's token is an output too); the writer
+    // then records the step as usual
+    if (!phase_sample(p, m, c)) return false;
+    if (!is_writer) return true;
+  }
   if (!need_tok && !is_writer) return true;
   float* pairs = m.big;  // [G][S][2]
   STAMP(0);
@@ -2356,7 +2584,7 @@ DEV bool rule_masked(const StepParams& p, const Lds& m, int row, int li) {
   return false;
 }
 
-template <int WQ8, int DR>
+template <int WQ8, int DR, int SAMP>
 DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
   constexpr int R = DR;
   const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x, d = p.d, V = p.V;
@@ -2433,6 +2661,15 @@ DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
     nl = (nmine - 1) * 8 + min(8, V - last_row0);
   }
   if (__builtin_expect(p.bias != nullptr, 0)) add_bias_rows(p, lg, rw, lidx, nl, 1, rpw, c.st);
+  if constexpr (SAMP) {
+    // in-launch sampling: the masked row goes to memory with device-coherent stores, complete in
+    // every wave before the pair that tells the other workgroups it is there
+    lds_barrier();
+    for (int li = tid; li < nl; li += kThreads)
+      if (lidx[li] >= 0) __hip_atomic_store(p.samp_row + lidx[li], lg[li], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    kv_drain();
+    lds_barrier();
+  }
   if (tid < 64) {
     // The (max, argmax) pair goes out first: the next step waits on it, while the full record
     // (log-sum-exp, top-k, probe) only feeds the step outputs.  Same order and ties as sel_partial.
@@ -2457,7 +2694,7 @@ DEV bool phase_logits1(const StepParams& p, const Lds& m, const StepCtx& c) {
   return true;
 }
 
-template <int SM, int WQ8, int DR>
+template <int SM, int WQ8, int DR, int SAMP>
 __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
   extern __shared__ float lds_raw[];
   // a chained sampled decode that has ended: nothing left to compute (uniform across the grid)
@@ -2546,7 +2783,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
       ++c.ph;
     }
     if constexpr (SM == 1) {
-      if (!phase_logits1<WQ8, DR>(p, m, c)) return;
+      if (!phase_logits1<WQ8, DR, SAMP>(p, m, c)) return;
     } else {
       if (!phase_logits<SM, WQ8, DR>(p, m, c)) return;
     }
@@ -2556,7 +2793,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
     // (the word is read before the selection wait, which hides its latency); workgroups that leave
     // a step early make the others' next waits see the cancel word and leave as well
     const bool cancel = p.rules && aborted(p.err);
-    if (!phase_reduce(p, m, c)) return;
+    if (!phase_reduce<SAMP>(p, m, c)) return;
     STAMP(3);
     ++c.ph;
     // every workgroup saw the same token (all reduce the same pairs): the run ends together
@@ -2566,13 +2803,13 @@ __global__ void __launch_bounds__(kThreads, 1) k_step(StepParams p) {
 }
 
 // Cooperative launch of one step-kernel instance (grid = one workgroup per CU).
-template <int SM, int WQ8, int DR>
+template <int SM, int WQ8, int DR, int SAMP = 0>
 static hipError_t launch_step_t(const StepParams& p, int grid, size_t lds, hipStream_t st) {
-  hipError_t e = hipFuncSetAttribute((const void*)k_step<SM, WQ8, DR>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  hipError_t e = hipFuncSetAttribute((const void*)k_step<SM, WQ8, DR, SAMP>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   StepParams pp = p;
   void* args[] = {&pp};
-  return hipLaunchCooperativeKernel((const void*)k_step<SM, WQ8, DR>, dim3(grid), dim3(kThreads), args, (unsigned)lds, st);
+  return hipLaunchCooperativeKernel((const void*)k_step<SM, WQ8, DR, SAMP>, dim3(grid), dim3(kThreads), args, (unsigned)lds, st);
 }
 
 }  // namespace w4h

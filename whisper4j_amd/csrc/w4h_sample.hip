@@ -17,38 +17,6 @@
 
 namespace w4h {
 
-// The k-th SplitMix64 output after `state` (k >= 1) as a double in [0, 1): the draw the host decode
-// loop's generator returns on its k-th call.
-DEV double splitmix_uniform(uint64_t state, int k) {
-  uint64_t z = state + (uint64_t)k * 0x9e3779b97f4a7c15ull;
-  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
-  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
-  z ^= z >> 31;
-  return (double)(z >> 11) * (1.0 / 9007199254740992.0);
-}
-
-DEV double wave_sum_d(double v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
-// Inclusive scan over the wave's lanes, in lane order.
-DEV double wave_scan_d(double v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const double u = __shfl_up(v, o);
-    if (lane >= o) v += u;
-  }
-  return v;
-}
-
-DEV double ld_agent(const double* p) {
-  return __longlong_as_double((long long)__hip_atomic_load(reinterpret_cast<const unsigned long long*>(p),
-                                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-}
-
 // Exclusive scan over the block (256 threads) of per-thread doubles, in thread order; *total gets the
 // block sum.  red: 4 doubles of LDS.
 DEV double block_scan_excl(double v, double* red, double* total) {
