@@ -462,17 +462,45 @@ def test_sampling_in_launch_equals_chain(gpu, monkeypatch, d, heads, wtype, temp
     prompt, eot, sup = [10, 11, 12], 599, [1, 2]
     res = {}
     monkeypatch.setenv("W4H_DEVICE_SAMPLE", "1")
-    for mode in ("0", "1"):
+    for mode in ("0", "2"):  # 2: the in-launch path without falling back to the chain
         monkeypatch.setenv("W4H_SAMPLE_IN_LAUNCH", mode)
         res[mode] = dec.decode(xa, prompt, eot, 120, sup, temperature=temperature, seed=seed, timestamp_begin=ts_begin)
     dec.close()
     m.close()
-    c, i = res["0"], res["1"]
+    c, i = res["0"], res["2"]
     say(f"d={d} {wtype} T={temperature} seed={seed} ts={ts_begin}: chain {len(c.tokens)} tokens avg {c.avg_logprob:.9f}, "
         f"in-launch {len(i.tokens)} tokens avg {i.avg_logprob:.9f}")
     assert i.tokens == c.tokens
     assert abs(i.avg_logprob - c.avg_logprob) <= 1e-9
     assert len(i.tokens) > 5
+
+
+@pytest.mark.parametrize("shape,wtype", [("base.en", "f16"), ("small", "f16"), ("medium", "q8_0")])
+def test_sampling_in_launch_full_vocab(gpu, monkeypatch, shape, wtype):
+    """The in-launch sampler at the real vocabulary (51864-51865 ids, ~203 per workgroup range, one
+    per thread) and full depth, against the launch chain on the same session, inputs and seed:
+    identical tokens, average log-probability within 1e-9.  base.en and small f16 (two and three
+    register rounds), medium q8_0; 1500 encoder frames, the multilingual prompt, 48 tokens at T = 0.7
+    with the end token suppressed so both run to the end."""
+    dims = synth.SHAPES[shape]
+    say(f"in-launch sampler, {shape} {wtype}: building weights")
+    T = synth.make_decoder(dims, seed=3, wtype=wtype)
+    xa = synth.encoder_output(dims, 3)
+    m = gpu.Model.from_tensors(dims, T)
+    dec = gpu.WhisperDecoder(m, beam_size=1)
+    prompt, eot = list(synth.BENCH_PREFIX), synth.EOT_MULTILINGUAL
+    res = {}
+    monkeypatch.setenv("W4H_DEVICE_SAMPLE", "1")
+    for mode in ("0", "2"):  # 2: the in-launch path without falling back to the chain
+        monkeypatch.setenv("W4H_SAMPLE_IN_LAUNCH", mode)
+        res[mode] = dec.decode(xa, prompt, eot, 48, [eot], temperature=0.7, seed=11)
+    dec.close()
+    m.close()
+    c, i = res["0"], res["2"]
+    say(f"{shape}: chain {len(c.tokens)} tokens avg {c.avg_logprob:.9f}, in-launch {len(i.tokens)} tokens avg {i.avg_logprob:.9f}")
+    assert len(i.tokens) == 48
+    assert i.tokens == c.tokens
+    assert abs(i.avg_logprob - c.avg_logprob) <= 1e-9
 
 
 @pytest.mark.parametrize("beam", [1, 3])

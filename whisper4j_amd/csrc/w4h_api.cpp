@@ -631,6 +631,15 @@ static std::mutex& coop_lock(int device) {
   return m[device & 63];
 }
 
+// Whether the in-launch draw's scratch (the pairs, scan words) fits the step kernel's phase region,
+// which ends where the resident vocabulary rows begin (the selection reduce sizes it larger).
+static size_t sample_scratch_room(const w4h_session* s) {
+  const size_t d = (size_t)s->m->dims.n_text_state;
+  const size_t big0 = 8 + kMaxRows + (size_t)kResItems * kMaxRows * 8 + (size_t)s->S * 4 * d + (size_t)s->S * d;
+  return s->res_off / sizeof(float) > big0 ? s->res_off / sizeof(float) - big0 : 0;
+}
+static bool sample_scratch_fits(const w4h_session* s) { return sample_scratch_room(s) >= (size_t)2 * s->grid + 48; }
+
 // Launch n_steps steps; tokens/forced are host arrays.  Results (if out) are copied back.  With
 // `rules` (one-row persistent sessions, greedy feedback, out required) the decode rules run on the
 // device and the run ends after the step that selects rules->eot; *steps_done receives the number
@@ -738,6 +747,7 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
     const int V = s->m->dims.n_vocab;
     if (s->grid > kThreads || (size_t)V > (size_t)s->grid * kThreads * kSampEpt)
       return fail(W4H_ERR_INVALID, "in-launch sampling needs grid <= %d and V <= grid * %d", kThreads, kThreads * kSampEpt);
+    if (!sample_scratch_fits(s)) return fail(W4H_ERR_INVALID, "no LDS left for the in-launch sampler");
     const size_t xw = (size_t)s->grid * 6 + 2;
     if ((rc = ensure(s->samp_x, xw * sizeof(u64))) || (rc = ensure(s->samp_row, sizeof(float) * (size_t)V)) ||
         (rc = ensure(s->samp_io, (sizeof(int32_t) + sizeof(double)) * (size_t)n_steps)))
@@ -746,7 +756,7 @@ int run_steps(w4h_session* s, const int32_t* tokens, const int32_t* forced, int 
     p.samp_t = samp->temperature;
     p.samp_rng = samp->rng;
     p.samp_x = s->samp_x.as<u64>();
-    p.samp_stride = 0;
+    p.samp_lds = sample_scratch_room(s) >= (size_t)8 * s->grid + 56 ? 1 : 0;
     p.samp_row = s->samp_row.as<float>();
     p.samp_lp = s->samp_io.as<double>();
     p.samp_tok = reinterpret_cast<int32_t*>(p.samp_lp + n_steps);
@@ -1394,17 +1404,16 @@ int device_greedy_run(w4h_session* s, const RulesRun& r, int n_steps, const uint
 }
 
 // Sampled runs with the draw inside the step kernel (one launch per run) instead of a chain of one-step
-// launches and sampling kernels: one-row persistent sessions (W4H_SAMPLE_IN_LAUNCH=0 selects the chain).
+// launches and sampling kernels: one-row persistent sessions.  W4H_SAMPLE_IN_LAUNCH=0 selects the chain;
+// =2 takes the in-launch path without the eligibility checks, so that a session it does not fit fails
+// (run_steps) instead of falling back (tests).
 static bool sample_in_launch(const w4h_session* s) {
-  if (const char* e = getenv("W4H_SAMPLE_IN_LAUNCH"))
+  if (const char* e = getenv("W4H_SAMPLE_IN_LAUNCH")) {
     if (!strcmp(e, "0")) return false;
-  if (!session_device_rules(s) || s->grid > kThreads || (size_t)s->m->dims.n_vocab > (size_t)s->grid * kThreads * kSampEpt)
-    return false;
-  // the draw's scratch (pairs, range sums, scan words) fits the phase region, which ends where the
-  // resident vocabulary rows begin
-  const size_t d = (size_t)s->m->dims.n_text_state;
-  const size_t big0 = 8 + kMaxRows + (size_t)kResItems * kMaxRows * 8 + (size_t)s->S * 4 * d + (size_t)s->S * d;
-  return s->res_off / sizeof(float) >= big0 + (size_t)8 * s->grid + 64;
+    if (!strcmp(e, "2")) return true;
+  }
+  return session_device_rules(s) && s->grid <= kThreads &&
+         (size_t)s->m->dims.n_vocab <= (size_t)s->grid * kThreads * kSampEpt && sample_scratch_fits(s);
 }
 
 bool session_device_sample(const w4h_session* s) {

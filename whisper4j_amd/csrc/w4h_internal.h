@@ -80,8 +80,8 @@ struct StepParams {
   // workgroups draw the step's token together instead of taking the argmax.
   float samp_t;                 // temperature; 0: off
   uint64_t samp_rng;            // generator state; the run's step i takes draw i + 1 after it
-  u64* samp_x;                  // exchange words, kRep replicas samp_stride apart: [grid][6] sums, then 2
-  size_t samp_stride;
+  u64* samp_x;                  // exchange words: [grid][6] sums (three doubles as halves), then 2
+  int samp_lds;                 // 1: the phase region holds the grid's sums (8 grid + 56 floats)
   float* samp_row;              // [V] the step's masked logits (device-coherent stores and loads)
   int32_t* samp_tok;            // [nsteps] drawn tokens
   double* samp_lp;              // [nsteps] their log-probabilities

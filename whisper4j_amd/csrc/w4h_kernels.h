@@ -1963,10 +1963,52 @@ DEV double wg_scan_excl_d(double v, double* red, double* total) {
   return pre;
 }
 
-DEV void ll_st_d(u64* p, double v, uint32_t tag) {
+// Thread k < n waits for the W tagged words src[W k .. W k + W) and takes their values in v; the
+// same bounded wait as ll_poll2 (spin limit, cancel word).  Every thread of the workgroup calls it.
+template <int W>
+DEV bool ll_poll_regs(const u64* src, int n, float (&v)[W], uint32_t tag, unsigned* err) {
+  const int k = threadIdx.x;
+  bool fail = false;
+  if (k < n) {
+    u64 w[W];
+#pragma unroll
+    for (int u = 0; u < W; ++u) w[u] = ll_ld(src + (size_t)W * k + u);
+    unsigned spins = 0;
+    while (true) {
+      bool ok = true;
+#pragma unroll
+      for (int u = 0; u < W; ++u)
+        if ((uint32_t)(w[u] >> 32) != tag) {
+          ok = false;
+          w[u] = ll_ld(src + (size_t)W * k + u);
+        }
+      if (ok) break;
+      ++spins;
+      if (spins > kSpinLimit) {
+        raise_err(err, 1u);
+        fail = true;
+        break;
+      }
+      if ((spins & 63u) == 0 && aborted(err)) {
+        fail = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int u = 0; u < W; ++u) v[u] = __uint_as_float((uint32_t)w[u]);
+  } else {
+#pragma unroll
+    for (int u = 0; u < W; ++u) v[u] = 0.f;
+  }
+  return !wg_any(fail);
+}
+
+// A double as two tagged words, low half at p, high half at p + stride.
+DEV void ll_st_d(u64* p, size_t stride, double v, uint32_t tag) {
   const unsigned long long b = (unsigned long long)__double_as_longlong(v);
   ll_st(p, __uint_as_float((uint32_t)b), tag, 0);
-  ll_st(p + 1, __uint_as_float((uint32_t)(b >> 32)), tag, 0);
+  ll_st(p + stride, __uint_as_float((uint32_t)(b >> 32)), tag, 0);
 }
 DEV double words_d(const float* w) {
   return __longlong_as_double((long long)(((unsigned long long)__float_as_uint(w[1]) << 32) | __float_as_uint(w[0])));
@@ -1993,10 +2035,12 @@ DEV double words_d(const float* w) {
 // for sampled runs (SAMP = 1), so the greedy instances keep their registers.
 DEV bool phase_sample(const StepParams& p, const Lds& m, const StepCtx& c) {
   const int G = gridDim.x, g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, V = p.V;
-  float* pairs = m.big;        // [G][2]
-  float* sums = m.big + 2 * G; // [G][6] (three doubles as 32-bit halves)
-  double* dsc = reinterpret_cast<double*>((reinterpret_cast<uintptr_t>(m.big + 8 * G) + 7) & ~(uintptr_t)7);  // [16]
-  int* isc = reinterpret_cast<int*>(dsc + 16);                                                                // [8]
+  // LDS: the pairs [G][2] (then the token words), 16 doubles and 8 ints of scan scratch (within the
+  // phase region, which the selection reduce already sizes to at least 2 G + 48 floats), then, with
+  // p.samp_lds, the grid's sums [G][6]
+  float* pairs = m.big;
+  double* dsc = reinterpret_cast<double*>((reinterpret_cast<uintptr_t>(m.big + 2 * G) + 7) & ~(uintptr_t)7);
+  int* isc = reinterpret_cast<int*>(dsc + 16);
   const int per = (V + G - 1) / G, ept = (per + kThreads - 1) / kThreads;
   const float T = p.samp_t;
   u64* sx = p.samp_x;
@@ -2031,17 +2075,27 @@ DEV bool phase_sample(const StepParams& p, const Lds& m, const StepCtx& c) {
     dsc[12 + wave] = tse;
   }
   lds_barrier();
-  if (tid == 0) {
-    ll_st_d(sx + (size_t)g * 6, ((dsc[8] + dsc[9]) + dsc[10]) + dsc[11], c.tag);
-    ll_st_d(sx + (size_t)g * 6 + 2, tsf, c.tag);
-    ll_st_d(sx + (size_t)g * 6 + 4, ((dsc[12] + dsc[13]) + dsc[14]) + dsc[15], c.tag);
+  if (tid == 0) {  // workgroup g's six words together (fewer workgroups writing one line)
+    ll_st_d(sx + (size_t)g * 6, 1, ((dsc[8] + dsc[9]) + dsc[10]) + dsc[11], c.tag);
+    ll_st_d(sx + (size_t)g * 6 + 2, 1, tsf, c.tag);
+    ll_st_d(sx + (size_t)g * 6 + 4, 1, ((dsc[12] + dsc[13]) + dsc[14]) + dsc[15], c.tag);
   }
   // 3. every workgroup: totals, the draw, the crossing range (thread k < G takes workgroup k)
-  if (!ll_poll1<8>(sx, G * 6, sums, c.tag, p.err)) return false;
+  // thread k < G takes workgroup k's sums: polled into LDS in bulk where the phase region has room
+  // for them, else each thread polls its six words into registers
   const bool gin = tid < G;
-  const double gsd = gin ? words_d(sums + 6 * tid) : 0.0;
-  const double gsf = gin ? words_d(sums + 6 * tid + 2) : 0.0;
-  const double gse = gin ? words_d(sums + 6 * tid + 4) : 0.0;
+  float sw[6];
+  if (p.samp_lds) {
+    float* sums = reinterpret_cast<float*>(isc + 8);  // [G][6]
+    if (!ll_poll1<8>(sx, G * 6, sums, c.tag, p.err)) return false;
+#pragma unroll
+    for (int u = 0; u < 6; ++u) sw[u] = gin ? sums[6 * tid + u] : 0.f;
+  } else {
+    if (!ll_poll_regs<6>(sx, G, sw, c.tag, p.err)) return false;
+  }
+  const double gsd = gin ? words_d(sw) : 0.0;
+  const double gsf = gin ? words_d(sw + 2) : 0.0;
+  const double gse = gin ? words_d(sw + 4) : 0.0;
   double SD, SF, SE;
   (void)wg_scan_excl_d(gsd, dsc + 4, &SD);
   const double gpre = wg_scan_excl_d(gsf, dsc + 4, &SF);
@@ -2117,7 +2171,7 @@ DEV bool phase_sample(const StepParams& p, const Lds& m, const StepCtx& c) {
     }
   }
   // 5. every workgroup: the token
-  float* tw = sums;  // [2]
+  float* tw = pairs;  // [2] (the pairs were read in step 1)
   if (!ll_poll1<8>(sx + (size_t)G * 6, 2, tw, c.tag, p.err)) return false;
   const int tok = __float_as_int(tw[0]);
   if (tid == 0) {
