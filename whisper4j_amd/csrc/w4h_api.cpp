@@ -1441,12 +1441,41 @@ int device_sampled_run(w4h_session* s, const SampleRun& r, int n_steps, const ui
   const int V = s->m->dims.n_vocab;
   int rc;
   if (sample_in_launch(s)) {
-    // one launch for the whole run: the step kernel draws each token itself (phase_sample)
-    RulesRun rr{r.hist, r.nhist, r.eot, r.tsb};
-    std::vector<w4h_step_out> recs((size_t)n_steps);
-    int done = 0;
-    const int32_t tok = r.hist[r.nhist - 1];
-    return run_steps(s, &tok, nullptr, n_steps, sup, 0, recs.data(), nullptr, nullptr, nullptr, &rr, &done, &r, out);
+    // The step kernel draws each token itself (phase_sample), kSampleLaunch steps per launch: between
+    // launches the host sees a cancel (the device cancel word is a stream write, which waits while a
+    // launch holds the queue it shares) at a cost of two launch gaps per kSampleLaunch tokens.  Each
+    // launch continues the history and the generator (draw i of a launch after `done` draws is draw
+    // done + i + 1 of the run: the state advances by done steps).
+    constexpr int kSampleLaunch = 64;
+    std::vector<int32_t> hist(r.hist, r.hist + r.nhist);
+    std::vector<w4h_step_out> recs((size_t)std::min(kSampleLaunch, n_steps));
+    out->steps = 0;
+    out->ended = false;
+    out->tokens.clear();
+    out->lps.clear();
+    while (out->steps < n_steps) {
+      const int nc = std::min(kSampleLaunch, n_steps - out->steps);
+      const RulesRun rr{hist.data(), (int)hist.size(), r.eot, r.tsb};
+      SampleRun rc_run = r;
+      rc_run.hist = hist.data();
+      rc_run.nhist = (int)hist.size();
+      rc_run.rng = r.rng + (uint64_t)out->steps * 0x9e3779b97f4a7c15ull;
+      SampleRunOut so;
+      int done = 0;
+      const int32_t tok = hist.back();
+      if ((rc = run_steps(s, &tok, nullptr, nc, sup, 0, recs.data(), nullptr, nullptr, nullptr, &rr, &done, &rc_run, &so)))
+        return rc;
+      out->steps += so.steps;
+      out->tokens.insert(out->tokens.end(), so.tokens.begin(), so.tokens.end());
+      out->lps.insert(out->lps.end(), so.lps.begin(), so.lps.end());
+      if (so.ended) {
+        out->ended = true;
+        break;
+      }
+      hist.insert(hist.end(), so.tokens.begin(), so.tokens.end());
+      if (s->cancel.load()) return fail(W4H_ERR_CANCELLED, "session cancelled");
+    }
+    return W4H_OK;
   }
   HIPCHK(hipSetDevice(s->m->device));
   if ((rc = ensure(s->samp_row, sizeof(float) * (size_t)s->S * V)) || (rc = ensure(s->samp_sup, sizeof(uint32_t) * (size_t)s->mw)))
