@@ -421,7 +421,7 @@ def other_configs(w4h, synth):
     smp = measure_sampled_driver(w4h, synth, "base.en", 224)
     out["base.en sampled decode driver w4h_decode at T = 0.6, 224 tokens (prompt prefill, then sampled tokens with suppress + n-gram + timestamp rules; EOT suppressed)"] = {
         "tokens_per_s": round(smp["device_sampling"][0], 1), "us_per_token": round(smp["device_sampling"][1], 2),
-        "sampling": "on the device, each token drawn inside the step kernel (one launch per run)",
+        "sampling": "on the device, each token drawn inside the step kernel (one launch per 64 tokens)",
         "host_loop_tokens_per_s": round(smp["host_loop"][0], 1), "host_loop_us_per_token": round(smp["host_loop"][1], 2)}
     sps, hps, us, steps, frac = measure_beam(w4h, synth, "small", 224, 5)
     out["small beam 5, 224 steps (library beam driver w4h_decode_beam: prompt prefill, then the search on the device; seeded logit bias N(0,1), end token at -inf)"] = {
